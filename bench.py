@@ -1,0 +1,221 @@
+"""Benchmark: causal attention fwd+bwd on one MI355X.
+
+A step is one forward plus one backward pass of the fused causal attention
+through the C-ABI (inf_attn_fwd + inf_attn_bwd) over the config-2 batch:
+B=8 H=12 T=1024 D=64, fp32, Q/K/V/dO ~ N(0,1) from the seeded generator,
+scale 1/sqrt(64), all inputs resident in HBM before timing.  Work is counted
+with the FlashAttention causal convention: F_fwd = 2*B*H*T^2*D,
+F_fwd+bwd = 3.5*F_fwd = 45.097 GFLOP.
+
+Prints one JSON line.  Timing: W untimed warm-up steps, then K steps between
+two torch.cuda.synchronize() calls; per-entry-point durations come from HIP
+events recorded on the launch stream around every call in the timed region.
+The CPU baseline is the restated reference CPU path (oracle/liboracle.so, one
+core) on a bounded sample of heads of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+MFMA_FP32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix
+HBM_PEAK_GBS = 8000.0
+
+METRIC = "causal attn fwd+bwd TFLOP/s (B8 H12 T1024 D64 fp32) + % of MFMA peak"
+
+
+def flops_fwd(B, H, T, D):
+    return 2.0 * B * H * T * T * D  # 4*B*H*T^2*D / 2 (causal)
+
+
+def cpu_baseline(B, H, T, D, heads: int):
+    """Time the restated reference CPU path (one core) on `heads` heads of the workload."""
+    import numpy as np
+
+    import oracle
+
+    Hs = min(heads, B * H)
+    q, k, v, do = oracle.attn_inputs(1, Hs, T, D, seed=42)
+    t0 = time.perf_counter()
+    oracle.attn_fwd(q, k, v)
+    oracle.attn_bwd(q, k, v, do)
+    dt = time.perf_counter() - t0
+    f = 3.5 * flops_fwd(1, Hs, T, D)
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": f / dt / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{Hs} of {B * H} heads (T={T}, D={D}) fwd+bwd through the restated reference "
+                  f"CPU chain, {dt:.2f} s single-threaded on {cpu}; the backward recomputes the "
+                  f"forward as the reference chain would; FLOPs counted with the causal convention",
+        "seconds": dt,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
+    ap.add_argument("--cpu-heads", type=int, default=12, help="heads in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU only: every (b, h) head is independent, "
+                                   "so the path shards by heads with no communication; run with --gpus 1"}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import inferno_amd as ia
+    import oracle
+
+    B, H, T, D = 8, 12, 1024, 64
+    dt = torch.float32 if args.dtype == "f32" else torch.bfloat16
+    dev = torch.device("cuda:0")
+    q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=42)
+    if args.dtype == "bf16":
+        q, k, v, do = (oracle.bf16_to_f32(oracle.round_bf16(x)) for x in (q, k, v, do))
+    Q, K, V, dO = (torch.from_numpy(x).to(dev, dt) for x in (q, k, v, do))
+    O = torch.empty_like(Q)
+    LSE = torch.empty((B, H, T), device=dev, dtype=torch.float32)
+    dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+    ws = torch.empty(max(ia.workspace_bytes(ia.OP_ATTN_BWD, B, H, T, T, D, ia.ops._dt(Q)), 1),
+                     dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        ia.attn_fwd(Q, K, V, out=O, lse=LSE, stream=stream)
+        ia.attn_bwd(Q, K, V, O, dO, LSE, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        ia.attn_fwd(Q, K, V, out=O, lse=LSE, stream=stream)
+        ev[i][1].record(stream)
+        ia.attn_bwd(Q, K, V, O, dO, LSE, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
+        ev[i][2].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    fwd_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
+    bwd_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+    ms_per_step = wall * 1e3 / args.steps
+
+    F_fwd = flops_fwd(B, H, T, D)
+    F_bwd = 2.5 * F_fwd
+    F_step = 3.5 * F_fwd
+    peak = MFMA_FP32_PEAK_TFLOPS if args.dtype == "f32" else MFMA_BF16_PEAK_TFLOPS
+    value = F_step / (ms_per_step * 1e-3) / 1e12
+    bwd_tf = F_bwd / (bwd_ms * 1e-3) / 1e12
+    fwd_tf = F_fwd / (fwd_ms * 1e-3) / 1e12
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if args.dtype == "f32" else "bf16-in/f32-acc",
+        "data": "synthetic: Q,K,V,dO iid N(0,1), MT19937-64 + Box-Muller, seed 42+{0,1,2,3}",
+        "config": {"workload": "causal self-attention fwd+bwd, B=8 H=12 T=1024 D=64 (BASELINE config 2)",
+                   "B": B, "H": H, "T": T, "D": D, "causal": True, "scale": ia.default_scale(D)},
+        "frac_of_peak": round(value / peak, 4),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "bwd (bwd_pre + bwd_main; bwd_main dominates)",
+            "achieved": round(bwd_tf, 3),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(bwd_tf / peak, 4),
+            "traffic": None,
+            "algorithmic_flop_per_launch": F_bwd,
+            "avg_launch_ms": round(bwd_ms, 4),
+        },
+        "roofline_fwd": {
+            "bound": "mfma", "kernel": "attn_fwd_kernel", "achieved": round(fwd_tf, 3), "peak": peak,
+            "unit": "TFLOP/s", "frac": round(fwd_tf / peak, 4), "algorithmic_flop_per_launch": F_fwd,
+            "avg_launch_ms": round(fwd_ms, 4),
+        },
+    }
+
+    if not args.no_decode:
+        out["decode"] = bench_decode(ia, oracle, torch, np, dev)
+
+    if args.cpu_heads > 0:
+        out["cpu_baseline"] = cpu_baseline(B, H, T, D, args.cpu_heads)
+    print(json.dumps(out), flush=True)
+
+
+def bench_decode(ia, oracle, torch, np, dev, reps=50):
+    """Config 5: B32 H12 Tk2048 D64 fp32 decode, rotating two KV sets (> the 256 MB MALL)."""
+    B, H, Tk, D = 32, 12, 2048, 64
+    sets = []
+    for s in range(3):
+        kc = torch.from_numpy(oracle.randn(500 + 10 * s, (B, H, Tk, D))).to(dev)
+        vc = torch.from_numpy(oracle.randn(501 + 10 * s, (B, H, Tk, D))).to(dev)
+        q = torch.from_numpy(oracle.randn(502 + 10 * s, (B, H, 1, D))).to(dev)
+        sets.append((q, kc, vc))
+    out = torch.empty((B, H, 1, D), device=dev)
+    ws = torch.empty(ia.workspace_bytes(ia.OP_ATTN_DECODE, B, H, 1, Tk, D), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    for i in range(10):
+        q, kc, vc = sets[i % 3]
+        ia.attn_decode(q, kc, vc, out=out, workspace=ws, stream=stream)
+    torch.cuda.synchronize()
+    evs = []
+    for i in range(reps):
+        q, kc, vc = sets[i % 3]
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        ia.attn_decode(q, kc, vc, out=out, workspace=ws, stream=stream)
+        e1.record(stream)
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    ts = np.array([a.elapsed_time(b) for a, b in evs])
+    nbytes = 2 * B * H * Tk * D * 4 + 2 * B * H * D * 4
+    med = float(np.median(ts))
+    return {
+        "workload": "decode B32 H12 Tk2048 D64 fp32 (BASELINE config 5), 3 KV sets rotated",
+        "median_us": round(med * 1e3, 2),
+        "p10_us": round(float(np.percentile(ts, 10)) * 1e3, 2),
+        "p90_us": round(float(np.percentile(ts, 90)) * 1e3, 2),
+        "algorithmic_bytes": nbytes,
+        "achieved_GBs": round(nbytes / (med * 1e-3) / 1e9, 1),
+        "peak_GBs": HBM_PEAK_GBS,
+        "frac": round(nbytes / (med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,137 @@
+"""inferno_amd -- MI355X-native causal self-attention for Inferno.
+
+``libinferno_hip.so`` (built in-tree by ``inferno_amd.build``) is the product:
+the C-ABI launch layer declared in ``include/inferno_hip.h`` and its gfx950
+kernels.  This module binds that ABI with ctypes and offers thin helpers that
+take torch tensors as device-memory handles (torch is plumbing here: storage
+and streams).  There is no fallback: if the library is missing, every call
+raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libinferno_hip.so"
+
+INF_F32 = 0
+INF_BF16 = 1
+OP_ATTN_FWD, OP_ATTN_BWD, OP_ATTN_DECODE = 0, 1, 2
+
+STATUS = {
+    0: "INF_OK",
+    1: "INF_ERR_NULL_POINTER",
+    2: "INF_ERR_BAD_SHAPE",
+    3: "INF_ERR_BAD_STRIDE",
+    4: "INF_ERR_BAD_DTYPE",
+    5: "INF_ERR_UNSUPPORTED",
+    6: "INF_ERR_WORKSPACE",
+    7: "INF_ERR_ALIGNMENT",
+    8: "INF_ERR_BAD_SCALE",
+    9: "INF_ERR_HIP",
+}
+
+# Every symbol include/inferno_hip.h declares.
+EXPORTS = (
+    "inf_status_string",
+    "inf_version",
+    "inf_attn_workspace_bytes",
+    "inf_attn_fwd",
+    "inf_attn_bwd",
+    "inf_softmax_fwd",
+    "inf_softmax_bwd",
+    "inf_attn_decode",
+)
+
+
+class Strides(ctypes.Structure):
+    """inf_strides: element strides of a [B, H, T, D] view."""
+
+    _fields_ = [("b", ctypes.c_int64), ("h", ctypes.c_int64), ("t", ctypes.c_int64), ("d", ctypes.c_int64)]
+
+
+class InfernoError(RuntimeError):
+    def __init__(self, status: int, where: str):
+        self.status = status
+        super().__init__(f"{where}: {STATUS.get(status, status)} ({status_string(status)})")
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libinferno_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m inferno_amd.build` "
+                "(there is no CPU fallback)"
+            )
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i32, i64, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+        S = Strides
+        L.inf_status_string.argtypes = [i32]
+        L.inf_status_string.restype = ctypes.c_char_p
+        L.inf_version.argtypes = []
+        L.inf_version.restype = i32
+        L.inf_attn_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32, i32, ctypes.POINTER(ctypes.c_size_t)]
+        L.inf_attn_workspace_bytes.restype = i32
+        L.inf_attn_fwd.argtypes = [vp, S, vp, S, vp, S, vp, S, vp, i32, i32, i32, i32, i32, f32, i32, i32, vp]
+        L.inf_attn_fwd.restype = i32
+        L.inf_attn_bwd.argtypes = [vp, S, vp, S, vp, S, vp, S, vp, S, vp, vp, S, vp, S, vp, S, vp,
+                                   ctypes.c_size_t, i32, i32, i32, i32, i32, f32, i32, i32, vp]
+        L.inf_attn_bwd.restype = i32
+        L.inf_softmax_fwd.argtypes = [vp, vp, i64, i64, i64, i64, i32, vp]
+        L.inf_softmax_fwd.restype = i32
+        L.inf_softmax_bwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp]
+        L.inf_softmax_bwd.restype = i32
+        L.inf_attn_decode.argtypes = [vp, S, vp, S, vp, S, vp, S, i32, i32, i32, i32, f32, i32, vp,
+                                      ctypes.c_size_t, vp]
+        L.inf_attn_decode.restype = i32
+        _lib = L
+    return _lib
+
+
+def status_string(status: int) -> str:
+    return lib().inf_status_string(int(status)).decode()
+
+
+def workspace_bytes(op: int, B: int, H: int, Tq: int, Tk: int, D: int, dtype: int = INF_F32) -> int:
+    out = ctypes.c_size_t(0)
+    st = lib().inf_attn_workspace_bytes(op, B, H, Tq, Tk, D, dtype, ctypes.byref(out))
+    if st:
+        raise InfernoError(st, "inf_attn_workspace_bytes")
+    return int(out.value)
+
+
+def default_scale(D: int) -> float:
+    """1.0f / std::sqrt((float)D), as InfernoApp/main.cpp:743 computes it (fp32)."""
+    import numpy as np
+
+    return float(np.float32(1.0) / np.sqrt(np.float32(D)))
+
+
+from .ops import (  # noqa: E402  (torch-facing helpers need lib())
+    attn_bwd,
+    attn_decode,
+    attn_fwd,
+    softmax_bwd,
+    softmax_fwd,
+    strides_of,
+)
+
+__all__ = [
+    "lib",
+    "attn_fwd",
+    "attn_bwd",
+    "attn_decode",
+    "softmax_fwd",
+    "softmax_bwd",
+    "strides_of",
+    "workspace_bytes",
+    "default_scale",
+    "InfernoError",
+    "EXPORTS",
+]

@@ -1,0 +1,313 @@
+// attn_bwd.hip -- fused causal attention backward for gfx950 (recompute).
+//
+// Kernel 1 (bwd_pre): delta[i] = sum_d dO[i,d] * O[i,d] per query row (the
+// row dot that SoftmaxBackward computes as sum_j dP_ij P_ij), and zeroes the
+// fp32 dQ accumulator.
+//
+// Kernel 2 (bwd_main): one workgroup = 4 waves = 128 keys of one (b, h); each
+// wave owns 32 keys and keeps K and V for them in VGPRs plus its dK^T and dV^T
+// accumulators for the whole kernel, so dK and dV are written exactly once,
+// with no atomics.  The workgroup walks query tiles of 32 rows from the first
+// row that can see its keys to the end.  Per tile and wave:
+//
+//   S  (q x keys)   = Q K^T          A = Q from LDS, B = K^T in VGPRs
+//   dP (q x keys)   = dO V^T         A = dO from LDS, B = V^T in VGPRs
+//   P  = exp2(S*c - lse*log2e), masked entries exactly 0
+//   dS = P * (dP - delta)
+//   dV^T += dO^T P                   B = P straight from the S accumulators
+//   dK^T += Q^T dS                   B = dS straight from the dP accumulators
+//
+// All four keep keys on the lane axis.  dQ = dS K needs queries on the lane
+// axis instead, so each wave writes its dS block to LDS, and after a barrier
+// the four waves compute the tile's dQ (32 x D over all 128 keys) with
+// v_mfma_f32_16x16x4_f32 and add it to the fp32 accumulator with one
+// global atomic add per element per 128-key block.  Workgroup w takes key
+// block w / (B*H), so the blocks with the most query tiles start first.
+//
+// Kernel 3 (bwd_cvt, bf16 only): dQ accumulator -> bf16 dq.
+#include "common.h"
+#include "kernels.h"
+
+namespace inf {
+
+template <int D, typename E>
+__global__ __launch_bounds__(256) void bwd_pre_kernel(BwdParams p) {
+    constexpr int TPR = D / 4;         // threads per row
+    constexpr int RPB = 256 / TPR;     // rows per block
+    const int tid = threadIdx.x;
+    const int64_t row = (int64_t)blockIdx.x * RPB + tid / TPR;
+    const int c4 = tid % TPR;
+    const int64_t rows = (int64_t)p.B * p.H * p.Tq;
+    float s = 0.f;
+    int64_t bh = 0, i = 0;
+    if (row < rows) {
+        bh = row / p.Tq;
+        i = row % p.Tq;
+        const int64_t b = bh / p.H, h = bh % p.H;
+        const f32x4 o4 = ld4((const E*)p.o + b * p.so.b + h * p.so.h + i * p.so.t + 4 * c4);
+        const f32x4 d4 = ld4((const E*)p.dout + b * p.sdo.b + h * p.sdo.h + i * p.sdo.t + 4 * c4);
+        s = o4[0] * d4[0] + o4[1] * d4[1] + o4[2] * d4[2] + o4[3] * d4[3];
+        *reinterpret_cast<f32x4*>(p.dq_acc + b * p.sacc.b + h * p.sacc.h + i * p.sacc.t + 4 * c4) =
+            f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int m = TPR / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
+    if (row < rows && c4 == 0) p.delta[row] = s;
+}
+
+template <int D>
+struct BwdTile {
+    static constexpr int QS = D + 4;         // Q / dO row stride in LDS (floats)
+    static constexpr int SS = kBwdBK + 4;    // dS row stride
+    static constexpr int KTS = kBwdBK + 4;   // K^T row stride
+};
+
+template <int D, typename E>
+__global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdParams p) {
+    constexpr int BQ = kBwdBQ;
+    constexpr int BK = kBwdBK;
+    constexpr int HD = D / 2;
+    constexpr int NDB = D / 32;
+    constexpr int C4 = D / 4;
+    constexpr int QS = BwdTile<D>::QS;
+    constexpr int SS = BwdTile<D>::SS;
+    constexpr int KTS = BwdTile<D>::KTS;
+    constexpr int QLPT = BQ * C4 / 256;   // 4-element loads per thread for a Q / dO tile
+    constexpr int KLPT = BK * C4 / 256;   // for the K^T staging
+    constexpr int DQB = D / 32;           // 16x16 dQ blocks per wave
+
+    __shared__ __attribute__((aligned(16))) float Qs[BQ][QS];
+    __shared__ __attribute__((aligned(16))) float dOs[BQ][QS];
+    __shared__ __attribute__((aligned(16))) float dSs[BQ][SS];
+    __shared__ __attribute__((aligned(16))) float Kts[D][KTS];
+    __shared__ __attribute__((aligned(16))) float lse_s[BQ];
+    __shared__ __attribute__((aligned(16))) float dl_s[BQ];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+    const int l16 = lane & 15;
+    const int g4 = lane >> 4;
+
+    const int BH = p.B * p.H;
+    const int w = blockIdx.x;
+    const int kblk = w / BH;
+    const int bh = w % BH;
+    const int b = bh / p.H;
+    const int h = bh % p.H;
+
+    const E* Q = (const E*)p.q + b * p.sq.b + h * p.sq.h;
+    const E* K = (const E*)p.k + b * p.sk.b + h * p.sk.h;
+    const E* V = (const E*)p.v + b * p.sv.b + h * p.sv.h;
+    const E* dO = (const E*)p.dout + b * p.sdo.b + h * p.sdo.h;
+    float* dQa = p.dq_acc + b * p.sacc.b + h * p.sacc.h;
+    const float* LSE = p.lse + (int64_t)bh * p.Tq;
+    const float* DL = p.delta + (int64_t)bh * p.Tq;
+
+    const int k0 = kblk * BK;
+    const int k0w = k0 + wave * 32;
+    const int key = k0w + l32;  // this lane's key
+
+    // K^T and V^T operands: lane (l32, g) holds row `key`, columns g*HD + i.
+    float kf[HD], vf[HD];
+    if (key < p.Tk) {
+        const E* ks = K + (int64_t)key * p.sk.t + g * HD;
+        const E* vs = V + (int64_t)key * p.sv.t + g * HD;
+#pragma unroll
+        for (int i = 0; i < HD; i += 4) {
+            const f32x4 a = ld4(ks + i);
+            const f32x4 c = ld4(vs + i);
+            kf[i] = a[0]; kf[i + 1] = a[1]; kf[i + 2] = a[2]; kf[i + 3] = a[3];
+            vf[i] = c[0]; vf[i + 1] = c[1]; vf[i + 2] = c[2]; vf[i + 3] = c[3];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < HD; ++i) kf[i] = vf[i] = 0.f;
+    }
+
+    // K^T of the whole 128-key block in LDS, for the dQ product.
+#pragma unroll
+    for (int i = 0; i < KLPT; ++i) {
+        const int f = tid + 256 * i;
+        const int r = f / C4;
+        const int c4 = f % C4;
+        f32x4 val = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (k0 + r < p.Tk) val = ld4(K + (int64_t)(k0 + r) * p.sk.t + 4 * c4);
+        Kts[4 * c4 + 0][r] = val[0];
+        Kts[4 * c4 + 1][r] = val[1];
+        Kts[4 * c4 + 2][r] = val[2];
+        Kts[4 * c4 + 3][r] = val[3];
+    }
+
+    f32x16 dv_acc[NDB], dk_acc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) {
+        dv_acc[i] = f32x16{};
+        dk_acc[i] = f32x16{};
+    }
+
+    int q_begin = 0;
+    if (p.causal) q_begin = max(0, k0 - p.off);
+    q_begin = (q_begin / BQ) * BQ;
+    const float c = p.c;
+
+    for (int q0 = q_begin; q0 < p.Tq; q0 += BQ) {
+        // ---- stage the query tile ----------------------------------------------
+#pragma unroll
+        for (int i = 0; i < QLPT; ++i) {
+            const int f = tid + 256 * i;
+            const int r = f / C4;
+            const int c4 = f % C4;
+            const int qi = q0 + r;
+            f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, d = a;
+            if (qi < p.Tq) {
+                a = ld4(Q + (int64_t)qi * p.sq.t + 4 * c4);
+                d = ld4(dO + (int64_t)qi * p.sdo.t + 4 * c4);
+            }
+            *reinterpret_cast<f32x4*>(&Qs[r][4 * c4]) = a;
+            *reinterpret_cast<f32x4*>(&dOs[r][4 * c4]) = d;
+        }
+        if (tid < BQ) {
+            const int qi = q0 + tid;
+            lse_s[tid] = (qi < p.Tq) ? LSE[qi] * kLog2e : 0.f;
+            dl_s[tid] = (qi < p.Tq) ? DL[qi] : 0.f;
+        }
+        __syncthreads();
+
+        // Does any query of this tile see any key of this wave?
+        const bool active = !p.causal || (q0 + BQ - 1 + p.off >= k0w);
+        f32x16 ds = f32x16{};
+        if (active && k0w < p.Tk) {
+            f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+            for (int i = 0; i < HD; i += 4) {
+                const f32x4 qa = *reinterpret_cast<const f32x4*>(&Qs[l32][g * HD + i]);
+                const f32x4 da = *reinterpret_cast<const f32x4*>(&dOs[l32][g * HD + i]);
+                s = mfma32x32x2(qa[0], kf[i + 0], s);
+                dp = mfma32x32x2(da[0], vf[i + 0], dp);
+                s = mfma32x32x2(qa[1], kf[i + 1], s);
+                dp = mfma32x32x2(da[1], vf[i + 1], dp);
+                s = mfma32x32x2(qa[2], kf[i + 2], s);
+                dp = mfma32x32x2(da[2], vf[i + 2], dp);
+                s = mfma32x32x2(qa[3], kf[i + 3], s);
+                dp = mfma32x32x2(da[3], vf[i + 3], dp);
+            }
+            // P and dS; reg r holds query row 8*(r/4) + 4*g + r%4 of the tile.
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]);
+                const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    const int r = 4 * j + cc;
+                    const int qi = q0 + 8 * j + 4 * g + cc;
+                    const bool vis = (qi < p.Tq) && (key < p.Tk) && (!p.causal || key <= qi + p.off);
+                    const float pr = vis ? fast_exp2(fmaf(s[r], c, -L[cc])) : 0.f;
+                    s[r] = pr;
+                    ds[r] = pr * (dp[r] - Dl[cc]);
+                }
+            }
+            // dV^T += dO^T P ; dK^T += Q^T dS
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) {
+                const int qr = 8 * (kk >> 2) + 4 * g + (kk & 3);
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    const float ado = dOs[qr][db * 32 + l32];
+                    const float aq = Qs[qr][db * 32 + l32];
+                    dv_acc[db] = mfma32x32x2(ado, s[kk], dv_acc[db]);
+                    dk_acc[db] = mfma32x32x2(aq, ds[kk], dk_acc[db]);
+                }
+            }
+        }
+        // dS block of this wave -> LDS (rows = queries, columns = the 128 keys)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dSs[8 * (r >> 2) + 4 * g + (r & 3)][wave * 32 + l32] = ds[r];
+        __syncthreads();
+
+        // ---- dQ tile (32 x D) += dS (32 x 128) K (128 x D) ---------------------
+#pragma unroll
+        for (int bi = 0; bi < DQB; ++bi) {
+            const int blk = wave * DQB + bi;
+            const int qh = blk & 1;
+            const int dc = blk >> 1;
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 32; kk += 4) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(&dSs[16 * qh + l16][g4 * 32 + kk]);
+                const f32x4 bb = *reinterpret_cast<const f32x4*>(&Kts[16 * dc + l16][g4 * 32 + kk]);
+                acc = mfma16x16x4(a[0], bb[0], acc);
+                acc = mfma16x16x4(a[1], bb[1], acc);
+                acc = mfma16x16x4(a[2], bb[2], acc);
+                acc = mfma16x16x4(a[3], bb[3], acc);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int qi = q0 + 16 * qh + 4 * g4 + r;
+                if (qi < p.Tq) unsafeAtomicAdd(dQa + (int64_t)qi * p.sacc.t + 16 * dc + l16, acc[r] * p.scale);
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- dK = scale * dK^T^T, dV = dV^T^T ------------------------------------------
+    if (key < p.Tk) {
+        E* dKp = (E*)p.dk + b * p.sdk.b + h * p.sdk.h + (int64_t)key * p.sdk.t;
+        E* dVp = (E*)p.dv + b * p.sdv.b + h * p.sdv.h + (int64_t)key * p.sdv.t;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f32x4 a, v;
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    a[cc] = dk_acc[db][4 * j + cc] * p.scale;
+                    v[cc] = dv_acc[db][4 * j + cc];
+                }
+                st4(dKp + db * 32 + 8 * j + 4 * g, a);
+                st4(dVp + db * 32 + 8 * j + 4 * g, v);
+            }
+    }
+}
+
+// dQ accumulator (fp32) -> bf16 dq.
+template <int D>
+__global__ __launch_bounds__(256) void bwd_cvt_kernel(BwdParams p) {
+    constexpr int TPR = D / 4;
+    constexpr int RPB = 256 / TPR;
+    const int tid = threadIdx.x;
+    const int64_t row = (int64_t)blockIdx.x * RPB + tid / TPR;
+    const int c4 = tid % TPR;
+    const int64_t rows = (int64_t)p.B * p.H * p.Tq;
+    if (row >= rows) return;
+    const int64_t bh = row / p.Tq, i = row % p.Tq;
+    const int64_t b = bh / p.H, h = bh % p.H;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p.dq_acc + b * p.sacc.b + h * p.sacc.h +
+                                                     i * p.sacc.t + 4 * c4);
+    st4((uint16_t*)p.dq + b * p.sdq.b + h * p.sdq.h + i * p.sdq.t + 4 * c4, a);
+}
+
+template <int D, typename E>
+static int launch_bwd_t(const BwdParams& p, hipStream_t s) {
+    constexpr int RPB = 256 / (D / 4);
+    const int64_t rows = (int64_t)p.B * p.H * p.Tq;
+    const dim3 pre_grid((unsigned)((rows + RPB - 1) / RPB));
+    hipLaunchKernelGGL((bwd_pre_kernel<D, E>), pre_grid, dim3(256), 0, s, p);
+    const dim3 grid((unsigned)(p.n_kblocks * p.B * p.H));
+    hipLaunchKernelGGL((bwd_main_kernel<D, E>), grid, dim3(256), 0, s, p);
+    if (sizeof(E) == 2) hipLaunchKernelGGL((bwd_cvt_kernel<D>), pre_grid, dim3(256), 0, s, p);
+    return (int)hipGetLastError();
+}
+
+int launch_attn_bwd(const BwdParams& p, int bf16, hipStream_t s) {
+    switch (p.D) {
+        case 32: return bf16 ? launch_bwd_t<32, uint16_t>(p, s) : launch_bwd_t<32, float>(p, s);
+        case 64: return bf16 ? launch_bwd_t<64, uint16_t>(p, s) : launch_bwd_t<64, float>(p, s);
+        case 128: return bf16 ? launch_bwd_t<128, uint16_t>(p, s) : launch_bwd_t<128, float>(p, s);
+        default: return (int)hipErrorInvalidValue;
+    }
+}
+
+}  // namespace inf

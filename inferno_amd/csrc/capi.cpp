@@ -1,0 +1,223 @@
+// capi.cpp -- the extern "C" boundary (include/inferno_hip.h): host-side
+// argument validation, workspace sizing and kernel launches.
+//
+// Every check runs before the first HIP call, so invalid arguments return a
+// status code on a machine without a GPU.  Nothing here allocates.
+#include "inferno_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "kernels.h"
+
+namespace {
+
+constexpr size_t kAlign = 256;
+
+size_t round_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+int elem_bytes(inf_dtype dt) { return dt == INF_F32 ? 4 : 2; }
+
+bool dtype_ok(int dt) { return dt == INF_F32 || dt == INF_BF16; }
+
+bool head_dim_ok(int D) { return D == 32 || D == 64 || D == 128; }
+
+// A [B,H,T,D] view: unit d stride, non-negative strides, rows aligned for
+// 4-element vector access (16 B fp32, 8 B bf16).
+int check_view(const void* p, const inf_strides& s, inf_dtype dt) {
+    if (!p) return INF_ERR_NULL_POINTER;
+    if (s.d != 1 || s.b < 0 || s.h < 0 || s.t < 0) return INF_ERR_BAD_STRIDE;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uintptr_t need = (uintptr_t)(4 * elem_bytes(dt));
+    if (a % need) return INF_ERR_ALIGNMENT;
+    if ((s.b % 4) || (s.h % 4) || (s.t % 4)) return INF_ERR_ALIGNMENT;
+    return INF_OK;
+}
+
+inf::View4 view(const inf_strides& s) { return inf::View4{s.b, s.h, s.t}; }
+
+int hip_status(int e) { return e == 0 ? INF_OK : INF_ERR_HIP; }
+
+int common_shape(int B, int H, int Tq, int Tk, int D, float scale, int dt) {
+    if (!dtype_ok(dt)) return INF_ERR_BAD_DTYPE;
+    if (B < 1 || H < 1 || Tq < 1 || Tk < 1 || D < 1) return INF_ERR_BAD_SHAPE;
+    if (!head_dim_ok(D)) return INF_ERR_UNSUPPORTED;
+    if (!(scale > 0.f) || !std::isfinite(scale)) return INF_ERR_BAD_SCALE;
+    // grid sizes are 32-bit; keep head counts and lengths well inside them
+    if ((int64_t)B * H > (1LL << 24) || Tq > (1 << 24) || Tk > (1 << 24)) return INF_ERR_BAD_SHAPE;
+    return INF_OK;
+}
+
+int decode_nsplit(int Tk) { return (Tk + inf::kDecodeChunk - 1) / inf::kDecodeChunk; }
+
+}  // namespace
+
+extern "C" {
+
+const char* inf_status_string(int status) {
+    switch (status) {
+        case INF_OK: return "ok";
+        case INF_ERR_NULL_POINTER: return "null pointer argument";
+        case INF_ERR_BAD_SHAPE: return "invalid shape";
+        case INF_ERR_BAD_STRIDE: return "invalid stride (head-dim stride must be 1, strides >= 0)";
+        case INF_ERR_BAD_DTYPE: return "unsupported dtype";
+        case INF_ERR_UNSUPPORTED: return "unsupported configuration (head dim must be 32, 64 or 128)";
+        case INF_ERR_WORKSPACE: return "workspace missing or too small";
+        case INF_ERR_ALIGNMENT: return "misaligned pointer or stride (rows must allow 4-element vector access)";
+        case INF_ERR_BAD_SCALE: return "scale must be finite and > 0";
+        case INF_ERR_HIP: return "HIP runtime error";
+        default: return "unknown status";
+    }
+}
+
+int inf_version(void) { return 100; }
+
+int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dtype dt,
+                             size_t* out_bytes) {
+    if (!out_bytes) return INF_ERR_NULL_POINTER;
+    *out_bytes = 0;
+    if (op == INF_OP_ATTN_DECODE) Tq = 1;
+    const int st = common_shape(B, H, Tq, Tk, D, 1.0f, dt);
+    if (st != INF_OK) return st;
+    const size_t bh = (size_t)B * H;
+    switch (op) {
+        case INF_OP_ATTN_FWD: *out_bytes = 0; return INF_OK;
+        case INF_OP_ATTN_BWD: {
+            size_t n = round_up(bh * Tq * sizeof(float));                       // delta
+            if (dt == INF_BF16) n += round_up(bh * Tq * (size_t)D * sizeof(float));  // dQ accumulator
+            *out_bytes = n;
+            return INF_OK;
+        }
+        case INF_OP_ATTN_DECODE:
+            *out_bytes = round_up(bh * (size_t)decode_nsplit(Tk) * (D + 2) * sizeof(float));
+            return INF_OK;
+        default: return INF_ERR_UNSUPPORTED;
+    }
+}
+
+int inf_attn_fwd(const void* q, inf_strides sq, const void* k, inf_strides sk, const void* v,
+                 inf_strides sv, void* o, inf_strides so, float* lse, int B, int H, int Tq,
+                 int Tk, int D, float scale, int causal, inf_dtype dt, void* stream) {
+    int st = common_shape(B, H, Tq, Tk, D, scale, dt);
+    if (st != INF_OK) return st;
+    if (causal && Tq > Tk) return INF_ERR_BAD_SHAPE;
+    if ((st = check_view(q, sq, dt)) || (st = check_view(k, sk, dt)) ||
+        (st = check_view(v, sv, dt)) || (st = check_view(o, so, dt)))
+        return st;
+    inf::FwdParams p{};
+    p.q = q; p.k = k; p.v = v; p.o = o; p.lse = lse;
+    p.sq = view(sq); p.sk = view(sk); p.sv = view(sv); p.so = view(so);
+    p.B = B; p.H = H; p.Tq = Tq; p.Tk = Tk; p.D = D;
+    p.causal = causal ? 1 : 0;
+    p.off = Tk - Tq;
+    p.scale = scale;
+    p.c = scale * 1.4426950408889634f;
+    p.n_qtiles = (Tq + inf::kFwdBM - 1) / inf::kFwdBM;
+    return hip_status(inf::launch_attn_fwd(p, dt == INF_BF16, (hipStream_t)stream));
+}
+
+int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, const void* v,
+                 inf_strides sv, const void* o, inf_strides so, const void* dout,
+                 inf_strides sdo, const float* lse, void* dq, inf_strides sdq, void* dk,
+                 inf_strides sdk, void* dv, inf_strides sdv, void* workspace, size_t ws_bytes,
+                 int B, int H, int Tq, int Tk, int D, float scale, int causal, inf_dtype dt,
+                 void* stream) {
+    int st = common_shape(B, H, Tq, Tk, D, scale, dt);
+    if (st != INF_OK) return st;
+    if (causal && Tq > Tk) return INF_ERR_BAD_SHAPE;
+    if (!lse) return INF_ERR_NULL_POINTER;
+    if ((st = check_view(q, sq, dt)) || (st = check_view(k, sk, dt)) ||
+        (st = check_view(v, sv, dt)) || (st = check_view(o, so, dt)) ||
+        (st = check_view(dout, sdo, dt)) || (st = check_view(dq, sdq, dt)) ||
+        (st = check_view(dk, sdk, dt)) || (st = check_view(dv, sdv, dt)))
+        return st;
+    size_t need = 0;
+    inf_attn_workspace_bytes(INF_OP_ATTN_BWD, B, H, Tq, Tk, D, dt, &need);
+    if (!workspace || ws_bytes < need) return INF_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % kAlign) return INF_ERR_ALIGNMENT;
+
+    inf::BwdParams p{};
+    p.q = q; p.k = k; p.v = v; p.o = o; p.dout = dout; p.lse = lse;
+    p.dq = dq; p.dk = dk; p.dv = dv;
+    p.sq = view(sq); p.sk = view(sk); p.sv = view(sv); p.so = view(so);
+    p.sdo = view(sdo); p.sdq = view(sdq); p.sdk = view(sdk); p.sdv = view(sdv);
+    const size_t bh = (size_t)B * H;
+    char* ws = static_cast<char*>(workspace);
+    p.delta = reinterpret_cast<float*>(ws);
+    if (dt == INF_BF16) {
+        p.dq_acc = reinterpret_cast<float*>(ws + round_up(bh * Tq * sizeof(float)));
+        p.sacc = inf::View4{(int64_t)H * Tq * D, (int64_t)Tq * D, (int64_t)D};
+    } else {
+        p.dq_acc = static_cast<float*>(dq);
+        p.sacc = view(sdq);
+    }
+    p.B = B; p.H = H; p.Tq = Tq; p.Tk = Tk; p.D = D;
+    p.causal = causal ? 1 : 0;
+    p.off = Tk - Tq;
+    p.scale = scale;
+    p.c = scale * 1.4426950408889634f;
+    p.n_kblocks = (Tk + inf::kBwdBK - 1) / inf::kBwdBK;
+    return hip_status(inf::launch_attn_bwd(p, dt == INF_BF16, (hipStream_t)stream));
+}
+
+static int softmax_common(const void* a, const void* b, void* c, int64_t rows, int64_t cols,
+                          inf_dtype dt, int* vec_ok, int64_t s1, int64_t s2, int64_t s3) {
+    if (!dtype_ok(dt)) return INF_ERR_BAD_DTYPE;
+    if (!a || !b || !c) return INF_ERR_NULL_POINTER;
+    if (rows < 1 || cols < 1 || rows > (1LL << 31)) return INF_ERR_BAD_SHAPE;
+    if (s1 < cols || s2 < cols || s3 < cols) return INF_ERR_BAD_STRIDE;
+    const uintptr_t need = (uintptr_t)(4 * elem_bytes(dt));
+    *vec_ok = (cols % 4 == 0) && (s1 % 4 == 0) && (s2 % 4 == 0) && (s3 % 4 == 0) &&
+              (reinterpret_cast<uintptr_t>(a) % need == 0) &&
+              (reinterpret_cast<uintptr_t>(b) % need == 0) &&
+              (reinterpret_cast<uintptr_t>(c) % need == 0);
+    return INF_OK;
+}
+
+int inf_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int64_t x_row_stride,
+                    int64_t y_row_stride, inf_dtype dt, void* stream) {
+    int vec_ok = 0;
+    const int st = softmax_common(x, x, y, rows, cols, dt, &vec_ok, x_row_stride, y_row_stride,
+                                  y_row_stride);
+    if (st != INF_OK) return st;
+    inf::SoftmaxParams p{x, nullptr, y, rows, cols, x_row_stride, 0, y_row_stride};
+    return hip_status(inf::launch_softmax_fwd(p, dt == INF_BF16, vec_ok, (hipStream_t)stream));
+}
+
+int inf_softmax_bwd(const void* y, const void* dy, void* dx, int64_t rows, int64_t cols,
+                    int64_t y_row_stride, int64_t dy_row_stride, int64_t dx_row_stride,
+                    inf_dtype dt, void* stream) {
+    int vec_ok = 0;
+    const int st = softmax_common(y, dy, dx, rows, cols, dt, &vec_ok, y_row_stride, dy_row_stride,
+                                  dx_row_stride);
+    if (st != INF_OK) return st;
+    inf::SoftmaxParams p{y, dy, dx, rows, cols, y_row_stride, dy_row_stride, dx_row_stride};
+    return hip_status(inf::launch_softmax_bwd(p, dt == INF_BF16, vec_ok, (hipStream_t)stream));
+}
+
+int inf_attn_decode(const void* q, inf_strides sq, const void* kcache, inf_strides sk,
+                    const void* vcache, inf_strides sv, void* o, inf_strides so, int B, int H,
+                    int Tk, int D, float scale, inf_dtype dt, void* workspace, size_t ws_bytes,
+                    void* stream) {
+    int st = common_shape(B, H, 1, Tk, D, scale, dt);
+    if (st != INF_OK) return st;
+    if ((st = check_view(q, sq, dt)) || (st = check_view(kcache, sk, dt)) ||
+        (st = check_view(vcache, sv, dt)) || (st = check_view(o, so, dt)))
+        return st;
+    size_t need = 0;
+    inf_attn_workspace_bytes(INF_OP_ATTN_DECODE, B, H, 1, Tk, D, dt, &need);
+    if (!workspace || ws_bytes < need) return INF_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % kAlign) return INF_ERR_ALIGNMENT;
+    inf::DecodeParams p{};
+    p.q = q; p.k = kcache; p.v = vcache; p.o = o;
+    p.part = static_cast<float*>(workspace);
+    p.sq = view(sq); p.sk = view(sk); p.sv = view(sv); p.so = view(so);
+    p.B = B; p.H = H; p.Tk = Tk; p.D = D;
+    p.nsplit = decode_nsplit(Tk);
+    p.c = scale * 1.4426950408889634f;
+    return hip_status(inf::launch_attn_decode(p, dt == INF_BF16, (hipStream_t)stream));
+}
+
+}  // extern "C"

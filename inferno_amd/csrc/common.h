@@ -1,0 +1,106 @@
+// common.h -- shared device helpers for the gfx950 (CDNA4) attention kernels.
+//
+// Wave64 throughout.  MFMA operand/result layouts used by every kernel here
+// (lane l = 0..63, l32 = l % 32, g = l / 32; checked on the GPU by
+// tests/test_gpu_parity.py through the attention results themselves):
+//   v_mfma_f32_32x32x2_f32   A: lane gives A[l32][g]   B: lane gives B[g][l32]
+//                            D: reg r holds D[8*(r/4) + 4*g + r%4][l32]
+//   v_mfma_f32_16x16x4_f32   A: lane gives A[l%16][l/16]  B: B[l/16][l%16]
+//                            D: reg r holds D[4*(l/16) + r][l%16]
+//   v_mfma_f32_32x32x16_bf16 A: lane gives A[l32][8*g .. 8*g+7]  B: B[8*g .. 8*g+7][l32]
+//                            D: as 32x32x2
+// The reduction index of an MFMA may be permuted freely as long as A and B
+// agree, which is how the kernels feed a result tile straight back in as the
+// next product's operand without a shuffle.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace inf {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f32x16 mfma32x32x2(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32x32x16bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Hardware exp2 (v_exp_f32): exp2(-inf) = 0, ~1 ulp.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Cross-lane exchange within the wave (ds_bpermute; no LDS allocation).
+__device__ __forceinline__ float shfl_xor(float v, int mask) {
+    int lane = __lane_id();
+    int src = lane ^ mask;
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+    return v;
+}
+
+// bf16 <-> fp32 (round to nearest even; inputs here are finite).
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(((uint32_t)h) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t b = __float_as_uint(f);
+    if ((b & 0x7F800000u) == 0x7F800000u && (b & 0x007FFFFFu)) return (uint16_t)((b >> 16) | 0x40u);
+    b += 0x7FFFu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+
+// Element type tags: fp32 storage or bf16 storage (fp32 arithmetic either way).
+struct F32 {
+    using T = float;
+    static __device__ __forceinline__ float ld(const float* p) { return *p; }
+    static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
+};
+struct BF16 {
+    using T = uint16_t;
+    static __device__ __forceinline__ float ld(const uint16_t* p) { return bf16_to_f32(*p); }
+    static __device__ __forceinline__ void st(uint16_t* p, float v) { *p = f32_to_bf16(v); }
+};
+
+// Load 4 consecutive elements as fp32 (16-byte load for fp32, 8-byte for bf16).
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ f32x4 ld4(const uint16_t* p) {
+    u16x4 h = *reinterpret_cast<const u16x4*>(p);
+    f32x4 r;
+    r[0] = bf16_to_f32(h[0]);
+    r[1] = bf16_to_f32(h[1]);
+    r[2] = bf16_to_f32(h[2]);
+    r[3] = bf16_to_f32(h[3]);
+    return r;
+}
+__device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+__device__ __forceinline__ void st4(uint16_t* p, f32x4 v) {
+    u16x4 h;
+    h[0] = f32_to_bf16(v[0]);
+    h[1] = f32_to_bf16(v[1]);
+    h[2] = f32_to_bf16(v[2]);
+    h[3] = f32_to_bf16(v[3]);
+    *reinterpret_cast<u16x4*>(p) = h;
+}
+
+}  // namespace inf

@@ -1,0 +1,83 @@
+// kernels.h -- parameter blocks and host launchers shared by the C-ABI layer
+// (capi.cpp) and the kernel translation units.  Internal; not installed.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace inf {
+
+struct View4 {            // element strides of a [B,H,T,D] view, d stride 1
+    int64_t b, h, t;
+};
+
+struct FwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;           // dense [B,H,Tq] or null
+    View4 sq, sk, sv, so;
+    int B, H, Tq, Tk, D;
+    int causal;
+    int off;              // Tk - Tq: key j visible to query i iff j <= i + off
+    float scale;          // softmax scale
+    float c;              // scale * log2(e)
+    int n_qtiles;
+};
+
+struct BwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const void* dout;
+    const float* lse;     // dense [B,H,Tq]
+    float* delta;         // workspace, dense [B,H,Tq]: rowsum(dO * O)
+    float* dq_acc;        // fp32 dQ accumulation (dq itself for fp32)
+    View4 sacc;           // strides of dq_acc
+    void* dq;
+    void* dk;
+    void* dv;
+    View4 sq, sk, sv, so, sdo, sdq, sdk, sdv;
+    int B, H, Tq, Tk, D;
+    int causal, off;
+    float scale, c;
+    int n_kblocks;
+};
+
+struct DecodeParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* part;          // workspace [B*H, nsplit, D + 2]
+    View4 sq, sk, sv, so;
+    int B, H, Tk, D;
+    int nsplit;
+    float c;              // scale * log2(e)
+};
+
+struct SoftmaxParams {
+    const void* x;        // fwd: x; bwd: y
+    const void* g;        // bwd: dy
+    void* y;              // fwd: y; bwd: dx
+    int64_t rows;
+    int64_t cols;
+    int64_t sx, sg, sy;   // row strides (elements)
+};
+
+// Launchers return a hipError_t value (0 = hipSuccess).
+int launch_attn_fwd(const FwdParams& p, int bf16, hipStream_t s);
+int launch_attn_bwd(const BwdParams& p, int bf16, hipStream_t s);
+int launch_attn_decode(const DecodeParams& p, int bf16, hipStream_t s);
+int launch_softmax_fwd(const SoftmaxParams& p, int bf16, int vec_ok, hipStream_t s);
+int launch_softmax_bwd(const SoftmaxParams& p, int bf16, int vec_ok, hipStream_t s);
+
+// Tile shapes the host needs for grids and workspace sizing.
+constexpr int kFwdBM = 128;      // query rows per forward workgroup
+constexpr int kBwdBK = 128;      // keys per backward workgroup
+constexpr int kBwdBQ = 32;       // query rows per backward inner step
+constexpr int kDecodeChunk = 256;  // cached keys per decode workgroup
+
+}  // namespace inf

@@ -1,0 +1,129 @@
+"""Torch-facing helpers over the C-ABI (device memory and streams come from torch).
+
+Each helper validates nothing itself: the C-ABI validates on the host and a
+non-zero status raises InfernoError.  Tensors must live on the GPU; the
+launches go to torch's current stream.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import INF_BF16, INF_F32, OP_ATTN_BWD, OP_ATTN_DECODE, InfernoError, Strides, default_scale, lib, workspace_bytes
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return INF_F32
+    if t.dtype == torch.bfloat16:
+        return INF_BF16
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def strides_of(t: torch.Tensor) -> Strides:
+    """inf_strides of a 4-D [B, H, T, D] tensor view."""
+    if t.dim() != 4:
+        raise ValueError("expected a 4-D [B, H, T, D] tensor")
+    s = t.stride()
+    return Strides(s[0], s[1], s[2], s[3])
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _check(st: int, where: str) -> None:
+    if st:
+        raise InfernoError(st, where)
+
+
+def attn_fwd(q, k, v, causal=True, scale=None, out=None, lse=None, stream=None):
+    """O, LSE = causal attention forward of [B,H,T,D] views (fp32 or bf16)."""
+    B, H, Tq, D = q.shape
+    Tk = k.shape[2]
+    scale = default_scale(D) if scale is None else float(scale)
+    if out is None:
+        out = torch.empty((B, H, Tq, D), dtype=q.dtype, device=q.device)
+    if lse is None:
+        lse = torch.empty((B, H, Tq), dtype=torch.float32, device=q.device)
+    st = lib().inf_attn_fwd(
+        q.data_ptr(), strides_of(q), k.data_ptr(), strides_of(k), v.data_ptr(), strides_of(v),
+        out.data_ptr(), strides_of(out), lse.data_ptr(), B, H, Tq, Tk, D, scale, int(bool(causal)),
+        _dt(q), _stream(stream),
+    )
+    _check(st, "inf_attn_fwd")
+    return out, lse
+
+
+def attn_bwd(q, k, v, o, dout, lse, causal=True, scale=None, dq=None, dk=None, dv=None,
+             workspace=None, stream=None):
+    """dQ, dK, dV of causal attention (recompute from q, k, v, o, lse)."""
+    B, H, Tq, D = q.shape
+    Tk = k.shape[2]
+    scale = default_scale(D) if scale is None else float(scale)
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format) if dq is None else dq
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format) if dk is None else dk
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format) if dv is None else dv
+    nbytes = workspace_bytes(OP_ATTN_BWD, B, H, Tq, Tk, D, _dt(q))
+    if workspace is None:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    st = lib().inf_attn_bwd(
+        q.data_ptr(), strides_of(q), k.data_ptr(), strides_of(k), v.data_ptr(), strides_of(v),
+        o.data_ptr(), strides_of(o), dout.data_ptr(), strides_of(dout), lse.data_ptr(),
+        dq.data_ptr(), strides_of(dq), dk.data_ptr(), strides_of(dk), dv.data_ptr(), strides_of(dv),
+        workspace.data_ptr(), workspace.numel(), B, H, Tq, Tk, D, scale, int(bool(causal)), _dt(q),
+        _stream(stream),
+    )
+    _check(st, "inf_attn_bwd")
+    return dq, dk, dv
+
+
+def attn_decode(q, kcache, vcache, scale=None, out=None, workspace=None, stream=None):
+    """Single-query attention: q [B,H,1,D] against caches [B,H,Tk,D]."""
+    B, H, _, D = q.shape
+    Tk = kcache.shape[2]
+    scale = default_scale(D) if scale is None else float(scale)
+    if out is None:
+        out = torch.empty((B, H, 1, D), dtype=q.dtype, device=q.device)
+    nbytes = workspace_bytes(OP_ATTN_DECODE, B, H, 1, Tk, D, _dt(q))
+    if workspace is None:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    st = lib().inf_attn_decode(
+        q.data_ptr(), strides_of(q), kcache.data_ptr(), strides_of(kcache), vcache.data_ptr(),
+        strides_of(vcache), out.data_ptr(), strides_of(out), B, H, Tk, D, scale, _dt(q),
+        workspace.data_ptr(), workspace.numel(), _stream(stream),
+    )
+    _check(st, "inf_attn_decode")
+    return out
+
+
+def _rows(t: torch.Tensor):
+    cols = t.shape[-1]
+    if t.stride(-1) != 1:
+        raise ValueError("last axis must have unit stride")
+    t2 = t.reshape(-1, cols) if t.dim() != 2 else t
+    if t2.data_ptr() != t.data_ptr():
+        raise ValueError("rows must be addressable with one row stride")
+    return t2, t2.shape[0], cols, t2.stride(0) if t2.shape[0] > 1 else cols
+
+
+def softmax_fwd(x, out=None, stream=None):
+    """Row softmax over the last axis."""
+    x2, rows, cols, sx = _rows(x)
+    out = torch.empty_like(x2) if out is None else out.reshape(rows, cols)
+    st = lib().inf_softmax_fwd(x2.data_ptr(), out.data_ptr(), rows, cols, sx,
+                               out.stride(0) if rows > 1 else cols, _dt(x), _stream(stream))
+    _check(st, "inf_softmax_fwd")
+    return out.reshape(x.shape)
+
+
+def softmax_bwd(y, dy, out=None, stream=None):
+    """dx = y * (dy - sum(dy * y)) per row."""
+    y2, rows, cols, sy = _rows(y)
+    g2, _, _, sg = _rows(dy)
+    out = torch.empty_like(y2) if out is None else out.reshape(rows, cols)
+    st = lib().inf_softmax_bwd(y2.data_ptr(), g2.data_ptr(), out.data_ptr(), rows, cols, sy, sg,
+                               out.stride(0) if rows > 1 else cols, _dt(y), _stream(stream))
+    _check(st, "inf_softmax_bwd")
+    return out.reshape(y.shape)

@@ -1,0 +1,272 @@
+/*
+ * oracle.c -- CPU restatement of Inferno's causal-attention arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP path and the timed CPU
+ * baseline.  The product library never links, loads or calls this file.
+ *
+ * Build with -O2 -ffp-contract=off and no -march flags, so every `sum += a*b`
+ * rounds the product and the sum separately, as the reference's x86-64 build
+ * does.  See oracle.h for the per-function reference citations.
+ *
+ * Pinning (tests/test_oracle.py):
+ *   - orc_matmul_f32, orc_scale_f32, orc_triu_ones_i32, orc_masked_fill_f32,
+ *     orc_softmax_f32 and the composed forward: bit-exact against the
+ *     reference's own header kernels compiled from /root/reference into
+ *     oracle/_ref (ref_shim.cpp), on config-1 inputs and ragged shapes.
+ *   - orc_softmax_bwd_f32 (its reference header cannot be compiled here):
+ *     closed form y*(g - <g,y>) in fp64, sum-to-zero invariant, and fp64
+ *     central differences of the forward.
+ *   - orc_attn_bwd_f32: per-stage bit-exact against the reference matmul and
+ *     multiply kernels in oracle/_ref, plus fp64 finite differences of
+ *     L = sum(O * dO) on small shapes, and Q = 0 => dK = 0.
+ *   - LSE: closed form in fp64 and P = exp(s - LSE).
+ *   - generator: the C++ standard's value for the 10000th mt19937_64 draw and
+ *     std::mt19937_64 itself.
+ */
+#include "oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------- */
+/* MT19937-64: Matsumoto & Nishimura's published parameters.                 */
+/* ------------------------------------------------------------------------- */
+#define MT_N 312
+#define MT_M 156
+#define MT_MATRIX_A 0xB5026F5AA96619E9ULL
+#define MT_UPPER 0xFFFFFFFF80000000ULL
+#define MT_LOWER 0x000000007FFFFFFFULL
+
+void orc_mt64_seed(orc_mt64* g, uint64_t seed) {
+    g->mt[0] = seed;
+    for (int i = 1; i < MT_N; ++i)
+        g->mt[i] = 6364136223846793005ULL * (g->mt[i - 1] ^ (g->mt[i - 1] >> 62)) + (uint64_t)i;
+    g->idx = MT_N;
+}
+
+static void mt64_twist(orc_mt64* g) {
+    for (int i = 0; i < MT_N; ++i) {
+        uint64_t x = (g->mt[i] & MT_UPPER) | (g->mt[(i + 1) % MT_N] & MT_LOWER);
+        uint64_t xa = x >> 1;
+        if (x & 1ULL) xa ^= MT_MATRIX_A;
+        g->mt[i] = g->mt[(i + MT_M) % MT_N] ^ xa;
+    }
+    g->idx = 0;
+}
+
+uint64_t orc_mt64_next(orc_mt64* g) {
+    if (g->idx >= MT_N) mt64_twist(g);
+    uint64_t y = g->mt[g->idx++];
+    y ^= (y >> 29) & 0x5555555555555555ULL;
+    y ^= (y << 17) & 0x71D67FFFEDA60000ULL;
+    y ^= (y << 37) & 0xFFF7EEE000000000ULL;
+    y ^= y >> 43;
+    return y;
+}
+
+/* 53-bit uniform strictly inside (0,1): (x>>11 + 0.5) * 2^-53. */
+static double u53(orc_mt64* g) {
+    return ((double)(orc_mt64_next(g) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+}
+
+void orc_randn_f32(uint64_t seed, double sigma, float* out, size_t n) {
+    orc_mt64 g;
+    orc_mt64_seed(&g, seed);
+    const double two_pi = 6.283185307179586476925286766559;
+    size_t i = 0;
+    while (i < n) {
+        double u1 = u53(&g), u2 = u53(&g);
+        double r = sqrt(-2.0 * log(u1));
+        double z0 = r * cos(two_pi * u2), z1 = r * sin(two_pi * u2);
+        out[i++] = (float)(sigma * z0);
+        if (i < n) out[i++] = (float)(sigma * z1);
+    }
+}
+
+void orc_round_bf16(const float* in, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        uint32_t b;
+        memcpy(&b, &in[i], 4);
+        if ((b & 0x7F800000u) == 0x7F800000u && (b & 0x007FFFFFu)) {
+            out[i] = (uint16_t)((b >> 16) | 0x0040u); /* quiet NaN */
+            continue;
+        }
+        b += 0x7FFFu + ((b >> 16) & 1u);
+        out[i] = (uint16_t)(b >> 16);
+    }
+}
+
+void orc_bf16_to_f32(const uint16_t* in, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        uint32_t b = (uint32_t)in[i] << 16;
+        memcpy(&out[i], &b, 4);
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Reference kernels, restated.                                              */
+/* ------------------------------------------------------------------------- */
+
+/* cpuops.h:412-431: for m, for n: RT sum = 0; for k: sum += a*b; out = sum. */
+void orc_matmul_f32(const float* a, int64_t sa0, int64_t sa1,
+                    const float* b, int64_t sb0, int64_t sb1,
+                    float* out, int64_t M, int64_t K, int64_t N) {
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            float sum = 0.0f;
+            for (int64_t k = 0; k < K; ++k)
+                sum += a[m * sa0 + k * sa1] * b[k * sb0 + n * sb1];
+            out[m * N + n] = sum;
+        }
+    }
+}
+
+/* cpuops.h:222: optr[i] = (RT)a * (RT)b, b broadcast from a [1] tensor. */
+void orc_scale_f32(const float* a, float s, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = a[i] * s;
+}
+
+/* cpuops.h:649: keep (col - row >= diagonal); applied to ones -> 1 / 0. */
+void orc_triu_ones_i32(int32_t* out, int64_t rows, int64_t cols, int diagonal) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+            out[r * cols + c] = ((int)c - (int)r >= diagonal) ? 1 : 0;
+}
+
+/* cpuops.h:703: out = (mask != 0) ? fill : in. */
+void orc_masked_fill_f32(const float* in, const int32_t* mask, float fill,
+                         float* out, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c)
+            out[r * cols + c] = (mask[r * cols + c] != 0) ? fill : in[r * cols + c];
+}
+
+/* softmax_kernels.h:77-102: max (init lowest, strict >), e = (RT)exp((double)(x-max)),
+ * fp32 running sum, then divide in place. */
+void orc_softmax_f32(const float* x, float* y, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * cols;
+        float* yr = y + r * cols;
+        float mx = -FLT_MAX;
+        for (int64_t k = 0; k < cols; ++k)
+            if (xr[k] > mx) mx = xr[k];
+        float sum = 0.0f;
+        for (int64_t k = 0; k < cols; ++k) {
+            float e = (float)exp((double)(xr[k] - mx));
+            yr[k] = e;
+            sum += e;
+        }
+        for (int64_t k = 0; k < cols; ++k) yr[k] /= sum;
+    }
+}
+
+/* softmaxbackward.h:111-128: dot = sum g*y (fp32, axis order); dx = y*(g - dot). */
+void orc_softmax_bwd_f32(const float* y, const float* g, float* dx, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* yr = y + r * cols;
+        const float* gr = g + r * cols;
+        float* dr = dx + r * cols;
+        float dot = 0.0f;
+        for (int64_t k = 0; k < cols; ++k) dot += gr[k] * yr[k];
+        for (int64_t k = 0; k < cols; ++k) dr[k] = yr[k] * (gr[k] - dot);
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Attention compositions.  Heads are independent in every reference op used */
+/* (cpu_matmul loops batches outermost, the elementwise ops are per element), */
+/* so each (b,h) is run through the chain on its own; the arithmetic per     */
+/* element is the same as the batched call.                                  */
+/* ------------------------------------------------------------------------- */
+
+/* main.cpp:740-748 for one head: S = q @ kt; S = S * scale; masked_fill(triu). */
+static void head_scores(const float* q, const float* k, int64_t Tq, int64_t Tk, int64_t D,
+                        float scale, int causal, int32_t* mask, float* S) {
+    /* kt = k.transpose(-1,-2).contiguous() holds kt[d][j] = k[j][d]; read it in place. */
+    orc_matmul_f32(q, D, 1, k, 1, D, S, Tq, D, Tk);
+    orc_scale_f32(S, scale, S, Tq * Tk);
+    if (causal) {
+        /* triu(ones, 1) (main.cpp:806); end-aligned when Tq < Tk. */
+        orc_triu_ones_i32(mask, Tq, Tk, (int)(1 + (Tk - Tq)));
+        orc_masked_fill_f32(S, mask, -1e9f, S, Tq, Tk);
+    }
+}
+
+void orc_attn_fwd_f32(const float* q, const float* k, const float* v,
+                      int64_t B, int64_t H, int64_t Tq, int64_t Tk, int64_t D,
+                      float scale, int causal, float* o, float* lse, float* p) {
+    float* S = (float*)malloc(sizeof(float) * Tq * Tk);
+    float* P = (float*)malloc(sizeof(float) * Tq * Tk);
+    int32_t* mask = (int32_t*)malloc(sizeof(int32_t) * Tq * Tk);
+    for (int64_t bh = 0; bh < B * H; ++bh) {
+        const float* qh = q + bh * Tq * D;
+        const float* kh = k + bh * Tk * D;
+        const float* vh = v + bh * Tk * D;
+        head_scores(qh, kh, Tq, Tk, D, scale, causal, mask, S);
+        orc_softmax_f32(S, P, Tq, Tk);                          /* main.cpp:751 */
+        orc_matmul_f32(P, Tk, 1, vh, D, 1, o + bh * Tq * D, Tq, Tk, D); /* main.cpp:754 */
+        if (lse) {
+            for (int64_t i = 0; i < Tq; ++i) {
+                const float* sr = S + i * Tk;
+                double mx = -INFINITY;
+                for (int64_t j = 0; j < Tk; ++j)
+                    if ((double)sr[j] > mx) mx = sr[j];
+                double acc = 0.0;
+                for (int64_t j = 0; j < Tk; ++j) acc += exp((double)sr[j] - mx);
+                lse[bh * Tq + i] = (float)(mx + log(acc));
+            }
+        }
+        if (p) memcpy(p + bh * Tq * Tk, P, sizeof(float) * Tq * Tk);
+    }
+    free(S);
+    free(P);
+    free(mask);
+}
+
+void orc_attn_bwd_f32(const float* q, const float* k, const float* v, const float* dout,
+                      int64_t B, int64_t H, int64_t Tq, int64_t Tk, int64_t D,
+                      float scale, int causal, float* dq, float* dk, float* dv, float* ds) {
+    float* S = (float*)malloc(sizeof(float) * Tq * Tk);
+    float* P = (float*)malloc(sizeof(float) * Tq * Tk);
+    float* dP = (float*)malloc(sizeof(float) * Tq * Tk);
+    float* dS = (float*)malloc(sizeof(float) * Tq * Tk);
+    float* dKt = (float*)malloc(sizeof(float) * D * Tk);
+    int32_t* mask = (int32_t*)malloc(sizeof(int32_t) * Tq * Tk);
+    for (int64_t bh = 0; bh < B * H; ++bh) {
+        const float* qh = q + bh * Tq * D;
+        const float* kh = k + bh * Tk * D;
+        const float* vh = v + bh * Tk * D;
+        const float* gh = dout + bh * Tq * D;
+        /* forward recomputed exactly as orc_attn_fwd_f32 */
+        head_scores(qh, kh, Tq, Tk, D, scale, causal, mask, S);
+        orc_softmax_f32(S, P, Tq, Tk);
+        /* MMBackward(attn, v), mmbackward.cpp:77,80: dP = dO @ v^T; dV = attn^T @ dO */
+        orc_matmul_f32(gh, D, 1, vh, 1, D, dP, Tq, D, Tk);
+        orc_matmul_f32(P, 1, Tk, gh, D, 1, dv + bh * Tk * D, Tk, Tq, D);
+        /* SoftmaxBackward, softmaxbackward.h:109-129 */
+        orc_softmax_bwd_f32(P, dP, dS, Tq, Tk);
+        if (ds) memcpy(ds + bh * Tq * Tk, dS, sizeof(float) * Tq * Tk);
+        /* MultiplyBackward of scores*scale, multiplybackward.cpp:41: g * scale */
+        orc_scale_f32(dS, scale, dS, Tq * Tk);
+        /* MMBackward(q, kt): dQ = dS' @ kt^T = dS' @ k; dKt = q^T @ dS' */
+        orc_matmul_f32(dS, Tk, 1, kh, D, 1, dq + bh * Tq * D, Tq, Tk, D);
+        orc_matmul_f32(qh, 1, D, dS, Tk, 1, dKt, D, Tq, Tk);
+        /* TransposeBackward (transposebackward.cpp:41): dK = dKt^T */
+        float* dkh = dk + bh * Tk * D;
+        for (int64_t j = 0; j < Tk; ++j)
+            for (int64_t d = 0; d < D; ++d) dkh[j * D + d] = dKt[d * Tk + j];
+    }
+    free(S);
+    free(P);
+    free(dP);
+    free(dS);
+    free(dKt);
+    free(mask);
+}
+
+void orc_attn_decode_f32(const float* q, const float* kc, const float* vc,
+                         int64_t B, int64_t H, int64_t Tk, int64_t D, float scale, float* o) {
+    orc_attn_fwd_f32(q, kc, vc, B, H, 1, Tk, D, scale, 0, o, NULL, NULL);
+}

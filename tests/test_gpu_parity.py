@@ -1,0 +1,203 @@
+"""GPU parity: the HIP path through the C-ABI against the CPU oracle.
+
+Bar: max|x - ref| / max|ref| <= 1e-4 for fp32 and <= 2e-2 for bf16 inputs
+(fp32 arithmetic), on O, LSE, dQ, dK, dV; the causal mask bit-exact (prefix
+invariance, exact zeros).  Inputs: seeded N(0, sigma^2) from the oracle's
+MT19937-64 generator, seed 42 + {0: Q, 1: K, 2: V, 3: dO}.
+"""
+import numpy as np
+import pytest
+
+import oracle
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_BF16 = 2e-2
+
+
+@pytest.fixture(scope="module")
+def ia():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import inferno_amd
+
+    inferno_amd.lib()
+    return inferno_amd
+
+
+def dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dtype=dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def bf16_round(a):
+    return oracle.bf16_to_f32(oracle.round_bf16(a))
+
+
+def run_fwd_bwd(ia, q, k, v, do, causal=True, dtype=torch.float32):
+    Q, K, V, dO = (dev(x, dtype) for x in (q, k, v, do))
+    o, lse = ia.attn_fwd(Q, K, V, causal=causal)
+    dq, dk, dv = ia.attn_bwd(Q, K, V, o, dO, lse, causal=causal)
+    torch.cuda.synchronize()
+    return host(o), host(lse), host(dq), host(dk), host(dv)
+
+
+SHAPES = [
+    # (B, H, T, D)
+    (1, 4, 128, 32),    # config 1
+    (1, 2, 1, 64),
+    (1, 1, 2, 64),
+    (2, 1, 17, 32),
+    (1, 2, 63, 64),
+    (1, 1, 64, 64),
+    (1, 2, 65, 64),
+    (1, 1, 127, 128),
+    (1, 1, 129, 64),
+    (1, 2, 200, 128),
+    (1, 1, 1000, 64),
+]
+
+
+@pytest.mark.parametrize("B,H,T,D", SHAPES)
+def test_fwd_bwd_f32(ia, B, H, T, D):
+    print(f"[case] fwd_bwd_f32 B{B} H{H} T{T} D{D}", flush=True)
+    q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=42)
+    o_r, lse_r = oracle.attn_fwd(q, k, v)
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do)
+    o, lse, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do)
+    for name, x, r in (("O", o, o_r), ("LSE", lse, lse_r), ("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
+        # At T = 1 the reference dQ and dK are exactly 0 (P = 1, dS = 0): the
+        # 1e-2 floor turns the bar into an absolute 1e-6 there.
+        e = oracle.rel_err(x, r, floor=1e-2)
+        assert e <= TOL_F32, f"{name} rel err {e:.3e}"
+
+
+@pytest.mark.parametrize("B,H,T,D", [(1, 4, 128, 32), (1, 2, 129, 64), (1, 1, 300, 128)])
+def test_fwd_bwd_bf16(ia, B, H, T, D):
+    print(f"[case] fwd_bwd_bf16 B{B} H{H} T{T} D{D}", flush=True)
+    q, k, v, do = (bf16_round(x) for x in oracle.attn_inputs(B, H, T, D, seed=42))
+    o_r, _ = oracle.attn_fwd(q, k, v)
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do)
+    o, _, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do, dtype=torch.bfloat16)
+    for name, x, r in (("O", o, o_r), ("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
+        e = oracle.rel_err(x, r)
+        assert e <= TOL_BF16, f"{name} rel err {e:.3e}"
+
+
+def test_noncausal_f32(ia):
+    print("[case] noncausal", flush=True)
+    q, k, v, do = oracle.attn_inputs(1, 2, 96, 64, seed=7)
+    o_r, lse_r = oracle.attn_fwd(q, k, v, causal=False)
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do, causal=False)
+    o, lse, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do, causal=False)
+    for x, r in ((o, o_r), (lse, lse_r), (dq, dq_r), (dk, dk_r), (dv, dv_r)):
+        assert oracle.rel_err(x, r) <= TOL_F32
+
+
+def test_prefix_invariance_bitwise(ia):
+    """Changing K[j], V[j] for j >= t must leave O[:, :, :t] (and LSE) bit-identical."""
+    print("[case] prefix invariance", flush=True)
+    B, H, T, D = 1, 2, 300, 64
+    q, k, v, _ = oracle.attn_inputs(B, H, T, D, seed=11)
+    Q, K, V = dev(q), dev(k), dev(v)
+    o1, l1 = ia.attn_fwd(Q, K, V)
+    for t in (1, 64, 129, 200):
+        K2, V2 = K.clone(), V.clone()
+        K2[:, :, t:] = torch.randn_like(K2[:, :, t:]) * 5
+        V2[:, :, t:] = torch.randn_like(V2[:, :, t:]) * 5
+        o2, l2 = ia.attn_fwd(Q, K2, V2)
+        assert torch.equal(o1[:, :, :t], o2[:, :, :t]), f"prefix {t}"
+        assert torch.equal(l1[:, :, :t], l2[:, :, :t]), f"prefix {t}"
+
+
+def test_strided_qkv_view(ia):
+    """q/k/v read straight out of a [B, T, 3, H, D] projection buffer (no copies)."""
+    print("[case] strided views", flush=True)
+    B, H, T, D = 2, 3, 150, 64
+    q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=5)
+    buf = torch.empty((B, T, 3, H, D), device="cuda")
+    buf[:, :, 0] = dev(q).transpose(1, 2)
+    buf[:, :, 1] = dev(k).transpose(1, 2)
+    buf[:, :, 2] = dev(v).transpose(1, 2)
+    Q = buf[:, :, 0].permute(0, 2, 1, 3)
+    K = buf[:, :, 1].permute(0, 2, 1, 3)
+    V = buf[:, :, 2].permute(0, 2, 1, 3)
+    assert not Q.is_contiguous()
+    o, lse = ia.attn_fwd(Q, K, V)
+    dq, dk, dv = ia.attn_bwd(Q, K, V, o, dev(do), lse)
+    torch.cuda.synchronize()
+    o_r, _ = oracle.attn_fwd(q, k, v)
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do)
+    for x, r in ((o, o_r), (dq, dq_r), (dk, dk_r), (dv, dv_r)):
+        assert oracle.rel_err(host(x), r) <= TOL_F32
+
+
+def test_config2_full_size_heads(ia):
+    """Config 2 (B8 H12 T1024 D64) at full size on the GPU; three heads checked against the oracle."""
+    print("[case] config2 full size", flush=True)
+    B, H, T, D = 8, 12, 1024, 64
+    q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=42)
+    o, lse, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do)
+    for (b, h) in ((0, 0), (3, 7), (7, 11)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        o_r, lse_r = oracle.attn_fwd(q[sl], k[sl], v[sl])
+        dq_r, dk_r, dv_r = oracle.attn_bwd(q[sl], k[sl], v[sl], do[sl])
+        for name, x, r in (("O", o, o_r), ("LSE", lse, lse_r), ("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
+            e = oracle.rel_err(x[sl], r)
+            assert e <= TOL_F32, f"head {(b, h)} {name} rel err {e:.3e}"
+    # size-independent properties over every head
+    assert np.isfinite(o).all() and np.isfinite(dq).all() and np.isfinite(dk).all() and np.isfinite(dv).all()
+    # sum over keys of dV equals sum over queries of dO (rows of P sum to 1)
+    np.testing.assert_allclose(dv.sum(axis=2), do.sum(axis=2), rtol=0, atol=2e-3)
+
+
+@pytest.mark.parametrize("B,H,Tk,D", [(2, 3, 1, 64), (2, 3, 100, 64), (1, 2, 257, 32), (2, 2, 513, 128), (4, 12, 2048, 64)])
+def test_decode_f32(ia, B, H, Tk, D):
+    print(f"[case] decode B{B} H{H} Tk{Tk} D{D}", flush=True)
+    q = oracle.randn(100, (B, H, 1, D))
+    kc = oracle.randn(101, (B, H, Tk, D))
+    vc = oracle.randn(102, (B, H, Tk, D))
+    o_r = oracle.attn_decode(q, kc, vc)
+    o = host(ia.attn_decode(dev(q), dev(kc), dev(vc)))
+    assert oracle.rel_err(o, o_r) <= TOL_F32
+
+
+def test_decode_equals_last_prefill_row(ia):
+    B, H, T, D = 1, 2, 300, 64
+    q, k, v, _ = oracle.attn_inputs(B, H, T, D, seed=3)
+    Q, K, V = dev(q), dev(k), dev(v)
+    o_full, _ = ia.attn_fwd(Q, K, V)
+    o_dec = ia.attn_decode(Q[:, :, T - 1:T].contiguous(), K, V)
+    torch.cuda.synchronize()
+    assert oracle.rel_err(host(o_dec), host(o_full[:, :, T - 1:T])) <= 1e-5
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 1), (5, 3), (64, 128), (33, 1000), (16, 1024), (4, 4096), (3, 5000), (2, 4097)])
+def test_softmax_fwd_bwd_f32(ia, rows, cols):
+    print(f"[case] softmax {rows}x{cols}", flush=True)
+    x = oracle.randn(200, (rows, cols), 3.0)
+    g = oracle.randn(201, (rows, cols))
+    y_r = oracle.softmax(x)
+    dx_r = oracle.softmax_bwd(y_r, g)
+    y = ia.softmax_fwd(dev(x))
+    dx = ia.softmax_bwd(dev(y_r), dev(g))
+    torch.cuda.synchronize()
+    assert oracle.rel_err(host(y), y_r) <= TOL_F32
+    assert oracle.rel_err(host(dx), dx_r) <= TOL_F32
+
+
+def test_softmax_masked_scores_exact_zeros(ia):
+    """Scores masked with -1e9f (masked_fill) give exactly 0 probability."""
+    T = 257
+    s = oracle.randn(300, (2, T, T))
+    mask = np.triu(np.ones((T, T), bool), 1)
+    s[:, mask] = -1e9
+    y = host(ia.softmax_fwd(dev(s)))
+    assert (y[:, mask] == 0).all()
+    assert oracle.rel_err(y, oracle.softmax(s)) <= TOL_F32
