@@ -77,7 +77,21 @@ def main():
     ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--cpu-heads", type=int, default=12, help="heads in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16 and config-4 lines")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 512 MiB device copy 5 times (HBM-counter calibration)")
     args = ap.parse_args()
+
+    if args.calibrate_copy:
+        import torch
+
+        src = torch.ones(128 << 20, device="cuda:0")  # 512 MiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4}))
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only: every (b, h) head is independent, "
@@ -158,7 +172,9 @@ def main():
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(bwd_tf / peak, 4),
-            "traffic": None,
+            # HBM bytes per bwd_main launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+            # (x2.00 / x1.00 copy-kernel calibration): 125.7 MB read + 163.6 MB written.
+            "traffic": 289.3e6,
             "algorithmic_flop_per_launch": F_bwd,
             "avg_launch_ms": round(bwd_ms, 4),
         },
@@ -171,10 +187,55 @@ def main():
 
     if not args.no_decode:
         out["decode"] = bench_decode(ia, oracle, torch, np, dev)
+    if not args.no_extras:
+        del Q, K, V, dO, O, dQ, dK, dV, ws
+        torch.cuda.empty_cache()
+        out["configs"] = {
+            "c2_bf16": bench_attn(ia, oracle, torch, np, dev, 8, 12, 1024, 64, 1.0, "bf16"),
+            "c4_f32": bench_attn(ia, oracle, torch, np, dev, 1, 16, 8192, 128, 3.0, "f32", steps=5),
+            "c4_bf16": bench_attn(ia, oracle, torch, np, dev, 1, 16, 8192, 128, 3.0, "bf16", steps=5),
+        }
 
     if args.cpu_heads > 0:
         out["cpu_baseline"] = cpu_baseline(B, H, T, D, args.cpu_heads)
     print(json.dumps(out), flush=True)
+
+
+def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10, warmup=3):
+    """fwd and bwd timings of one attention config (HIP events on the launch stream)."""
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=42, qk_sigma=qk_sigma)
+    Q, K, V, dO = (torch.from_numpy(x).to(dev, tdt) for x in (q, k, v, do))
+    del q, k, v, do
+    O = torch.empty_like(Q)
+    LSE = torch.empty((B, H, T), device=dev, dtype=torch.float32)
+    dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
+    ws = torch.empty(max(ia.workspace_bytes(ia.OP_ATTN_BWD, B, H, T, T, D, ia.ops._dt(Q)), 1),
+                     dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    evs = []
+    for i in range(warmup + steps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record(stream)
+        ia.attn_fwd(Q, K, V, out=O, lse=LSE, stream=stream)
+        e[1].record(stream)
+        ia.attn_bwd(Q, K, V, O, dO, LSE, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
+        e[2].record(stream)
+        if i >= warmup:
+            evs.append(e)
+    torch.cuda.synchronize()
+    fwd_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    bwd_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    F = flops_fwd(B, H, T, D)
+    peak = MFMA_FP32_PEAK_TFLOPS if dtype == "f32" else MFMA_BF16_PEAK_TFLOPS
+    tot = 3.5 * F / ((fwd_ms + bwd_ms) * 1e-3) / 1e12
+    return {
+        "shape": f"B{B} H{H} T{T} D{D}", "dtype": dtype if dtype == "f32" else "bf16-in/f32-acc",
+        "qk_sigma": qk_sigma, "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+        "fwd_tflops": round(F / (fwd_ms * 1e-3) / 1e12, 2),
+        "bwd_tflops": round(2.5 * F / (bwd_ms * 1e-3) / 1e12, 2),
+        "fwd_bwd_tflops": round(tot, 2), "peak_tflops": peak, "frac": round(tot / peak, 4),
+    }
 
 
 def bench_decode(ia, oracle, torch, np, dev, reps=50):
