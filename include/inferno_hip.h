@@ -127,6 +127,34 @@ int inf_attn_decode(const void* q, inf_strides sq, const void* kcache, inf_strid
                     int Tk, int D, float scale, inf_dtype dt, void* workspace, size_t ws_bytes,
                     void* stream);
 
+/* ---- element-wise support for the Tensor layer around the path ------------- */
+
+/* dst[i] = value for i < n; elem_bytes 1, 2 or 4; `bits` holds the value's bit
+ * pattern in the low elem_bytes bytes.  Replaces cuda_fill
+ * (src/inferno/cuda/cudafilltensor.cu:16-42), which seeds Engine::backward with
+ * ones_like (src/inferno/gradengine/engine.cpp:59). */
+int inf_fill(void* dst, int64_t n, int elem_bytes, uint32_t bits, void* stream);
+
+/* out[i] = a[i] (op) b[i], op INF_BIN_ADD or INF_BIN_MUL, dense operands of n
+ * elements; a_scalar / b_scalar mark an operand broadcast from one element.
+ * Replaces cuda_add / cuda_multiply (src/inferno/cuda/cudaadd.cu:20-142,
+ * cudamultiply.cu:16-146) for the same-shape and scalar cases the path uses
+ * (scores * scale, main.cpp:744; gradient accumulation, engine.cpp:166). */
+enum { INF_BIN_ADD = 0, INF_BIN_MUL = 1 };
+int inf_binary(int op, const void* a, const void* b, void* out, int64_t n, int a_scalar, int b_scalar,
+               inf_dtype dt, void* stream);
+
+/* Strided copy: for every index tuple idx over `shape` (rank <= 8),
+ * dst[sum_d idx_d * dst_strides[d]] = src[sum_d idx_d * src_strides[d]]
+ * (element strides, elem_bytes 1, 2, 4 or 8).  With dense dst_strides this is
+ * cuda_contiguous_copy (src/inferno/cuda/cudacontiguous.cu:16-139) without its
+ * per-call metadata cudaMalloc and device synchronisation; with strided dst it
+ * writes a gradient back into a view of a larger tensor (SliceBackward,
+ * src/inferno/gradfn/slicebackward.cpp:35-53). */
+int inf_copy_strided(const void* src, const int64_t* src_strides, void* dst,
+                     const int64_t* dst_strides, int ndim, const int64_t* shape, int elem_bytes,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,6 +42,9 @@ EXPORTS = (
     "inf_softmax_fwd",
     "inf_softmax_bwd",
     "inf_attn_decode",
+    "inf_fill",
+    "inf_binary",
+    "inf_copy_strided",
 )
 
 
@@ -90,6 +93,13 @@ def lib() -> ctypes.CDLL:
         L.inf_attn_decode.argtypes = [vp, S, vp, S, vp, S, vp, S, i32, i32, i32, i32, f32, i32, vp,
                                       ctypes.c_size_t, vp]
         L.inf_attn_decode.restype = i32
+        L.inf_fill.argtypes = [vp, i64, i32, ctypes.c_uint32, vp]
+        L.inf_fill.restype = i32
+        L.inf_binary.argtypes = [i32, vp, vp, vp, i64, i32, i32, i32, vp]
+        L.inf_binary.restype = i32
+        i64p = ctypes.POINTER(ctypes.c_int64)
+        L.inf_copy_strided.argtypes = [vp, i64p, vp, i64p, i32, i64p, i32, vp]
+        L.inf_copy_strided.restype = i32
         _lib = L
     return _lib
 

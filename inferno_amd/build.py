@@ -33,7 +33,7 @@ COMMON = [
     f"-I{CSRC}",
 ]
 
-SOURCES = ["capi.cpp", "attn_fwd.hip", "attn_bwd.hip", "decode.hip", "softmax.hip"]
+SOURCES = ["capi.cpp", "attn_fwd.hip", "attn_bwd.hip", "decode.hip", "softmax.hip", "elementwise.hip"]
 
 
 def _compile(src: Path, obj: Path) -> None:
@@ -41,6 +41,51 @@ def _compile(src: Path, obj: Path) -> None:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+
+
+# The C++ Tensor / autograd layer (host code only; g++ with the HIP runtime API headers).
+HOST_LIB = PKG / "libinferno.so"
+CPP = PKG / "cpp"
+CPP_SOURCES = ["dtype.cpp", "storage.cpp", "hipctx.cpp", "tensor.cpp", "engine.cpp", "softmax.cpp", "attention.cpp"]
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+CXX = os.environ.get("CXX", "g++")
+# -ffp-contract=off: the CPU-device branches keep the reference's separate
+# product and sum roundings.
+HOST_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function",
+              "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}", f"-I{ROCM / 'include'}"]
+DRIVER_SRC = ROOT / "tests" / "cpp" / "api_driver.cpp"
+DRIVER = ROOT / "tests" / "cpp" / "api_driver"
+
+
+def _run(cmd, what):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{what} failed:\n{' '.join(map(str, cmd))}\n{r.stdout}\n{r.stderr}")
+
+
+def build_host(verbose: bool = True) -> Path:
+    """libinferno.so (Tensor, autograd, ops) linked against libinferno_hip.so, plus the test driver."""
+    BUILD.mkdir(exist_ok=True)
+    objs = []
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(CPP_SOURCES))) as ex:
+        jobs = []
+        for src in CPP_SOURCES:
+            obj = BUILD / ("host_" + src.replace(".", "_") + ".o")
+            objs.append(obj)
+            jobs.append(ex.submit(_run, [CXX, *HOST_FLAGS, "-c", str(CPP / src), "-o", str(obj)], f"g++ {src}"))
+        for j in jobs:
+            j.result()
+    tmp = HOST_LIB.with_suffix(".so.tmp")
+    _run([CXX, "-shared", "-o", str(tmp), *map(str, objs), f"-L{PKG}", "-linferno_hip", f"-L{ROCM / 'lib'}",
+          "-lamdhip64", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM / 'lib'}"], "link libinferno.so")
+    os.replace(tmp, HOST_LIB)
+    if DRIVER_SRC.exists():
+        _run([CXX, *HOST_FLAGS, str(DRIVER_SRC), "-o", str(DRIVER), f"-L{PKG}", "-linferno", "-linferno_hip",
+              f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{PKG}", f"-Wl,-rpath,{ROCM / 'lib'}",
+              "-Wl,-rpath,$ORIGIN/../../inferno_amd"], "build api_driver")
+    if verbose:
+        print(f"built {HOST_LIB}", file=sys.stderr)
+    return HOST_LIB
 
 
 def build(verbose: bool = True) -> Path:
@@ -63,6 +108,7 @@ def build(verbose: bool = True) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}", file=sys.stderr)
+    build_host(verbose)
     return LIB
 
 

@@ -220,4 +220,44 @@ int inf_attn_decode(const void* q, inf_strides sq, const void* kcache, inf_strid
     return hip_status(inf::launch_attn_decode(p, dt == INF_BF16, (hipStream_t)stream));
 }
 
+int inf_fill(void* dst, int64_t n, int elem_bytes, uint32_t bits, void* stream) {
+    if (n < 0) return INF_ERR_BAD_SHAPE;
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4) return INF_ERR_BAD_DTYPE;
+    if (n == 0) return INF_OK;
+    if (!dst) return INF_ERR_NULL_POINTER;
+    return hip_status(inf::launch_fill(dst, n, elem_bytes, bits, (hipStream_t)stream));
+}
+
+int inf_binary(int op, const void* a, const void* b, void* out, int64_t n, int a_scalar, int b_scalar,
+               inf_dtype dt, void* stream) {
+    if (op != INF_BIN_ADD && op != INF_BIN_MUL) return INF_ERR_UNSUPPORTED;
+    if (!dtype_ok(dt)) return INF_ERR_BAD_DTYPE;
+    if (n < 0) return INF_ERR_BAD_SHAPE;
+    if (n == 0) return INF_OK;
+    if (!a || !b || !out) return INF_ERR_NULL_POINTER;
+    return hip_status(inf::launch_binary(op, a, b, out, n, a_scalar ? 1 : 0, b_scalar ? 1 : 0,
+                                         dt == INF_BF16, (hipStream_t)stream));
+}
+
+int inf_copy_strided(const void* src, const int64_t* src_strides, void* dst,
+                     const int64_t* dst_strides, int ndim, const int64_t* shape, int elem_bytes,
+                     void* stream) {
+    if (ndim < 0 || ndim > inf::kMaxRank) return INF_ERR_UNSUPPORTED;
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) return INF_ERR_BAD_DTYPE;
+    if (ndim > 0 && (!shape || !src_strides || !dst_strides)) return INF_ERR_NULL_POINTER;
+    inf::StridedCopy c{};
+    c.ndim = ndim;
+    c.n = 1;
+    for (int d = 0; d < ndim; ++d) {
+        if (shape[d] < 0 || src_strides[d] < 0 || dst_strides[d] < 0) return INF_ERR_BAD_STRIDE;
+        c.shape[d] = shape[d];
+        c.sstride[d] = src_strides[d];
+        c.dstride[d] = dst_strides[d];
+        c.n *= shape[d];
+    }
+    if (c.n == 0) return INF_OK;
+    if (!src || !dst) return INF_ERR_NULL_POINTER;
+    return hip_status(inf::launch_copy_strided(src, dst, c, elem_bytes, (hipStream_t)stream));
+}
+
 }  // extern "C"

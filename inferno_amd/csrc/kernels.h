@@ -67,12 +67,25 @@ struct SoftmaxParams {
     int64_t sx, sg, sy;   // row strides (elements)
 };
 
+constexpr int kMaxRank = 8;
+struct StridedCopy {      // element strides of source and destination
+    int ndim;
+    int64_t n;
+    int64_t shape[kMaxRank];
+    int64_t sstride[kMaxRank];
+    int64_t dstride[kMaxRank];
+};
+
 // Launchers return a hipError_t value (0 = hipSuccess).
 int launch_attn_fwd(const FwdParams& p, int bf16, hipStream_t s);
 int launch_attn_bwd(const BwdParams& p, int bf16, hipStream_t s);
 int launch_attn_decode(const DecodeParams& p, int bf16, hipStream_t s);
 int launch_softmax_fwd(const SoftmaxParams& p, int bf16, int vec_ok, hipStream_t s);
 int launch_softmax_bwd(const SoftmaxParams& p, int bf16, int vec_ok, hipStream_t s);
+int launch_fill(void* dst, int64_t n, int elem_bytes, uint32_t bits, hipStream_t s);
+int launch_binary(int op, const void* a, const void* b, void* out, int64_t n, int a_scalar, int b_scalar,
+                  int bf16, hipStream_t s);
+int launch_copy_strided(const void* src, void* dst, const StridedCopy& c, int elem_bytes, hipStream_t s);
 
 // Tile shapes the host needs for grids and workspace sizing.
 constexpr int kFwdBM = 128;      // query rows per forward workgroup

@@ -1,0 +1,179 @@
+"""The C++ Tensor / autograd drop-in (libinferno.so) through tests/cpp/api_driver.
+
+CPU-device runs must equal the oracle bit for bit (the CPU branch runs the
+reference chain); HIP-device runs must be within the parity bar (1e-4 fp32,
+2e-2 bf16 inputs) -- the device-parameterised pattern of the reference's tests.
+"""
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+
+ROOT = Path(__file__).resolve().parents[1]
+DRIVER = ROOT / "tests" / "cpp" / "api_driver"
+
+
+def have_gpu():
+    try:
+        import torch
+
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+def run(*args, timeout=300):
+    if not DRIVER.exists():
+        pytest.skip("api_driver not built (run __graft_entry__.build())")
+    r = subprocess.run([str(DRIVER), *map(str, args)], capture_output=True, text=True, timeout=timeout)
+    return r
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def write(d, **arrs):
+    for k, v in arrs.items():
+        np.ascontiguousarray(v, np.float32).tofile(d / f"{k}.bin")
+
+
+def read(d, name, shape):
+    return np.fromfile(d / f"{name}.bin", dtype=np.float32).reshape(shape)
+
+
+def bf16_round(a):
+    return oracle.bf16_to_f32(oracle.round_bf16(a))
+
+
+def attn_case(tmp_path, B, H, T, D, dtype, device, causal=True, layout=None, seed=42):
+    q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=seed)
+    if dtype == "bf16":
+        q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
+    write(tmp_path, q=q, k=k, v=v, do=do)
+    args = ["attn", tmp_path, B, H, T, D, dtype, device, int(causal)] + ([layout] if layout else [])
+    r = run(*args)
+    assert r.returncode == 0, r.stdout + r.stderr
+    out = {n: read(tmp_path, n, (B, H, T, D)) for n in ("o", "dq", "dk", "dv")}
+    out["lse"] = read(tmp_path, "lse", (B, H, T))
+    o_r, lse_r = oracle.attn_fwd(q, k, v, causal=causal)
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do, causal=causal)
+    return out, dict(o=o_r, lse=lse_r, dq=dq_r, dk=dk_r, dv=dv_r)
+
+
+# ------------------------------------------------------------------ CPU device
+def test_selftest_cpu():
+    r = run("selftest", "cpu")
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "SELFTEST OK 0" in r.stdout
+
+
+@pytest.mark.parametrize("B,H,T,D,causal", [(1, 4, 128, 32, True), (2, 1, 17, 8, True), (1, 2, 33, 16, False)])
+def test_attention_cpu_equals_reference_chain_bitwise(tmp_path, B, H, T, D, causal):
+    out, ref = attn_case(tmp_path, B, H, T, D, "f32", "cpu", causal)
+    for n in ("o", "dq", "dk", "dv", "lse"):
+        assert np.array_equal(bits(out[n]), bits(ref[n])), n
+
+
+def test_attention_cpu_qkv_views_bitwise(tmp_path):
+    """q, k, v sliced out of one [B, T, 3C] tensor (views all the way), grads back into it."""
+    out, ref = attn_case(tmp_path, 2, 3, 20, 8, "f32", "cpu", True, layout="qkv")
+    for n in ("o", "dq", "dk", "dv"):
+        assert np.array_equal(bits(out[n]), bits(ref[n])), n
+
+
+def test_softmax_cpu_bitwise(tmp_path):
+    x = oracle.randn(7, (6, 50), 3.0)
+    g = oracle.randn(8, (6, 50))
+    write(tmp_path, x=x, g=g)
+    r = run("softmax", tmp_path, 6, 50, "f32", "cpu", -1)
+    assert r.returncode == 0, r.stderr
+    y = read(tmp_path, "y", (6, 50))
+    assert np.array_equal(bits(y), bits(oracle.softmax(x)))
+    assert np.array_equal(bits(read(tmp_path, "dx", (6, 50))), bits(oracle.softmax_bwd(y, g)))
+
+
+def test_decode_cpu(tmp_path):
+    q = oracle.randn(1, (2, 3, 1, 16))
+    kc = oracle.randn(2, (2, 3, 40, 16))
+    vc = oracle.randn(3, (2, 3, 40, 16))
+    write(tmp_path, q=q, kc=kc, vc=vc)
+    r = run("decode", tmp_path, 2, 3, 40, 16, "f32", "cpu")
+    assert r.returncode == 0, r.stderr
+    assert np.array_equal(bits(read(tmp_path, "o", (2, 3, 1, 16))), bits(oracle.attn_decode(q, kc, vc)))
+
+
+def test_error_paths_cpu(tmp_path):
+    r = run("attn", tmp_path, 1, 1, 4, 8, "f32", "cpu", 1)  # missing input files
+    assert r.returncode == 3 and "cannot read" in r.stderr
+
+
+# ------------------------------------------------------------------ HIP device
+gpu = pytest.mark.gpu
+
+
+@gpu
+def test_selftest_hip():
+    if not have_gpu():
+        pytest.skip("no GPU")
+    print("[case] api_driver selftest hip", flush=True)
+    r = run("selftest", "hip")
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "SELFTEST OK 0" in r.stdout
+
+
+@gpu
+@pytest.mark.parametrize("B,H,T,D,dtype,layout", [
+    (1, 4, 128, 32, "f32", None),
+    (2, 3, 200, 64, "f32", None),
+    (1, 2, 129, 128, "f32", None),
+    (2, 3, 150, 64, "f32", "qkv"),
+    (1, 4, 128, 32, "bf16", None),
+])
+def test_attention_hip_parity(tmp_path, B, H, T, D, dtype, layout):
+    if not have_gpu():
+        pytest.skip("no GPU")
+    print(f"[case] api_driver attn hip B{B} H{H} T{T} D{D} {dtype} {layout}", flush=True)
+    out, ref = attn_case(tmp_path, B, H, T, D, dtype, "hip", True, layout)
+    tol = 1e-4 if dtype == "f32" else 2e-2
+    for n in ("o", "dq", "dk", "dv"):
+        e = oracle.rel_err(out[n], ref[n])
+        assert e <= tol, f"{n} rel err {e:.3e}"
+
+
+@gpu
+def test_softmax_hip_parity(tmp_path):
+    if not have_gpu():
+        pytest.skip("no GPU")
+    print("[case] api_driver softmax hip", flush=True)
+    x = oracle.randn(7, (64, 1024), 3.0)
+    g = oracle.randn(8, (64, 1024))
+    write(tmp_path, x=x, g=g)
+    for axis in (-1, 0):
+        r = run("softmax", tmp_path, 64, 1024, "f32", "hip", axis)
+        assert r.returncode == 0, r.stderr
+        xr = x if axis == -1 else np.ascontiguousarray(x.T)
+        gr = g if axis == -1 else np.ascontiguousarray(g.T)
+        y_r = oracle.softmax(xr)
+        dx_r = oracle.softmax_bwd(y_r, gr)
+        if axis == 0:
+            y_r, dx_r = y_r.T, dx_r.T
+        assert oracle.rel_err(read(tmp_path, "y", (64, 1024)), y_r) <= 1e-4
+        assert oracle.rel_err(read(tmp_path, "dx", (64, 1024)), dx_r) <= 1e-4
+
+
+@gpu
+def test_decode_hip_parity(tmp_path):
+    if not have_gpu():
+        pytest.skip("no GPU")
+    print("[case] api_driver decode hip", flush=True)
+    q = oracle.randn(1, (4, 12, 1, 64))
+    kc = oracle.randn(2, (4, 12, 700, 64))
+    vc = oracle.randn(3, (4, 12, 700, 64))
+    write(tmp_path, q=q, kc=kc, vc=vc)
+    r = run("decode", tmp_path, 4, 12, 700, 64, "f32", "hip")
+    assert r.returncode == 0, r.stderr
+    assert oracle.rel_err(read(tmp_path, "o", (4, 12, 1, 64)), oracle.attn_decode(q, kc, vc)) <= 1e-4
