@@ -248,7 +248,7 @@ def bench_decode(ia, oracle, torch, np, dev, reps=50):
         q = torch.from_numpy(oracle.randn(502 + 10 * s, (B, H, 1, D))).to(dev)
         sets.append((q, kc, vc))
     out = torch.empty((B, H, 1, D), device=dev)
-    ws = torch.empty(ia.workspace_bytes(ia.OP_ATTN_DECODE, B, H, 1, Tk, D), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(ia.workspace_bytes(ia.OP_ATTN_DECODE, B, H, 1, Tk, D), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     for i in range(10):
         q, kc, vc = sets[i % 3]

@@ -120,7 +120,9 @@ int inf_softmax_bwd(const void* y, const void* dy, void* dx, int64_t rows, int64
  * over all Tk cached keys (q, o: [B, H, 1, D]; caches [B, H, Tk, D]).  The
  * reference has no decode path; this equals the last row of a Tk-long causal
  * prefill through the same chain (InfernoApp/main.cpp:737-754 with Tq = 1).
- * workspace: inf_attn_workspace_bytes(INF_OP_ATTN_DECODE, ...) bytes.
+ * workspace: inf_attn_workspace_bytes(INF_OP_ATTN_DECODE, ...) bytes, 256-byte
+ * aligned (may be NULL when that size is 0, i.e. when one split covers Tk);
+ * its contents on entry do not matter.
  */
 int inf_attn_decode(const void* q, inf_strides sq, const void* kcache, inf_strides sk,
                     const void* vcache, inf_strides sv, void* o, inf_strides so, int B, int H,

@@ -13,6 +13,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <cmath>
+#include <mutex>
 
 #include "detail.h"
 #include "inferno/functional/attention.h"
@@ -64,6 +65,21 @@ struct Workspace {
         ptr = reinterpret_cast<void*>((p + 255) & ~uintptr_t(255));
     }
 };
+
+// The decode workspace of each device: grown on demand and reused by every call
+// (all calls on a device are ordered on that device's library stream).  Kept for
+// the life of the process (never destroyed, so no free runs after HIP teardown).
+void* decode_workspace(size_t bytes, const Device& dev) {
+    static std::mutex mu;
+    static auto* per_device = new std::vector<Tensor>();
+    if (bytes == 0) return nullptr;
+    std::lock_guard<std::mutex> lk(mu);
+    if (per_device->size() <= (size_t)dev.index) per_device->resize((size_t)dev.index + 1);
+    Tensor& t = (*per_device)[(size_t)dev.index];
+    if (!t.defined() || t.size() < bytes + 256) t = Tensor(DType::Float32, {bytes / 4 + 128}, "decode_ws", dev, false);
+    const uintptr_t p = reinterpret_cast<uintptr_t>(t.data_ptr());
+    return reinterpret_cast<void*>((p + 255) & ~uintptr_t(255));
+}
 
 inf_strides strides_of(const Tensor& t) {
     const auto& s = t.strides();
@@ -299,12 +315,12 @@ Tensor attention_decode(const Tensor& q, const Tensor& kcache, const Tensor& vca
     detail::status_check(inf_attn_workspace_bytes(INF_OP_ATTN_DECODE, (int)s.B, (int)s.H, 1, (int)s.Tk, (int)s.D, dt,
                                                   &ws_bytes),
                          "inf_attn_workspace_bytes");
-    Workspace ws(ws_bytes, q.device());
+    void* ws = decode_workspace(ws_bytes, q.device());
     Tensor qa = abi_view(q), ka = abi_view(kcache), va = abi_view(vcache);
     detail::DeviceGuard g(q.device().index);
     detail::status_check(inf_attn_decode(qa.data_ptr(), strides_of(qa), ka.data_ptr(), strides_of(ka), va.data_ptr(),
                                          strides_of(va), out.data_ptr(), strides_of(out), (int)s.B, (int)s.H, (int)s.Tk,
-                                         (int)s.D, sc, dt, ws.ptr, ws_bytes, detail::stream_of(q)),
+                                         (int)s.D, sc, dt, ws, ws_bytes, detail::stream_of(q)),
                          "inf_attn_decode");
     return out;
 }

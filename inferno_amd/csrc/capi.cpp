@@ -50,7 +50,6 @@ int common_shape(int B, int H, int Tq, int Tk, int D, float scale, int dt) {
     return INF_OK;
 }
 
-int decode_nsplit(int Tk) { return (Tk + inf::kDecodeChunk - 1) / inf::kDecodeChunk; }
 
 }  // namespace
 
@@ -90,9 +89,12 @@ int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dt
             *out_bytes = n;
             return INF_OK;
         }
-        case INF_OP_ATTN_DECODE:
-            *out_bytes = round_up(bh * (size_t)decode_nsplit(Tk) * (D + 2) * sizeof(float));
+        case INF_OP_ATTN_DECODE: {
+            int ns = 1, ch = 0;
+            inf::decode_plan(B, H, Tk, D, &ns, &ch);
+            *out_bytes = ns > 1 ? round_up(bh * (size_t)ns * (D + 2) * sizeof(float)) : 0;
             return INF_OK;
+        }
         default: return INF_ERR_UNSUPPORTED;
     }
 }
@@ -208,14 +210,14 @@ int inf_attn_decode(const void* q, inf_strides sq, const void* kcache, inf_strid
         return st;
     size_t need = 0;
     inf_attn_workspace_bytes(INF_OP_ATTN_DECODE, B, H, 1, Tk, D, dt, &need);
-    if (!workspace || ws_bytes < need) return INF_ERR_WORKSPACE;
-    if (reinterpret_cast<uintptr_t>(workspace) % kAlign) return INF_ERR_ALIGNMENT;
+    if (need && (!workspace || ws_bytes < need)) return INF_ERR_WORKSPACE;
+    if (need && reinterpret_cast<uintptr_t>(workspace) % kAlign) return INF_ERR_ALIGNMENT;
     inf::DecodeParams p{};
     p.q = q; p.k = kcache; p.v = vcache; p.o = o;
     p.part = static_cast<float*>(workspace);
+    inf::decode_plan(B, H, Tk, D, &p.nsplit, &p.chunk);
     p.sq = view(sq); p.sk = view(sk); p.sv = view(sv); p.so = view(so);
     p.B = B; p.H = H; p.Tk = Tk; p.D = D;
-    p.nsplit = decode_nsplit(Tk);
     p.c = scale * 1.4426950408889634f;
     return hip_status(inf::launch_attn_decode(p, dt == INF_BF16, (hipStream_t)stream));
 }

@@ -48,6 +48,27 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
 }
 
+// Sum over aligned groups of W lanes (W = 2..32), result in every lane of the
+// group.  Within a 16-lane DPP row it is VALU-only: quad_perm [1,0,3,2] and
+// [2,3,0,1] build quad sums, row_half_mirror (lane i <- 7-i) pairs the quads of
+// each half-row and row_mirror (lane i <- 15-i) pairs the halves; only W = 32
+// needs one cross-row ds_bpermute.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(W == 2 || W == 4 || W == 8 || W == 16 || W == 32, "group width");
+    if constexpr (W >= 2) v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+    if constexpr (W >= 4) v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+    if constexpr (W >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror
+    if constexpr (W >= 16) v += dpp_mov<0x140>(v); // row_mirror
+    if constexpr (W >= 32) v += shfl_xor(v, 16);
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));

@@ -54,7 +54,8 @@ struct DecodeParams {
     float* part;          // workspace [B*H, nsplit, D + 2]
     View4 sq, sk, sv, so;
     int B, H, Tk, D;
-    int nsplit;
+    int nsplit;           // key splits per (b, h)
+    int chunk;            // keys per split
     float c;              // scale * log2(e)
 };
 
@@ -80,6 +81,8 @@ struct StridedCopy {      // element strides of source and destination
 int launch_attn_fwd(const FwdParams& p, int bf16, hipStream_t s);
 int launch_attn_bwd(const BwdParams& p, int bf16, hipStream_t s);
 int launch_attn_decode(const DecodeParams& p, int bf16, hipStream_t s);
+// Decode split plan (number of key splits per row, keys per split) for a shape.
+void decode_plan(int B, int H, int Tk, int D, int* nsplit, int* chunk);
 int launch_softmax_fwd(const SoftmaxParams& p, int bf16, int vec_ok, hipStream_t s);
 int launch_softmax_bwd(const SoftmaxParams& p, int bf16, int vec_ok, hipStream_t s);
 int launch_fill(void* dst, int64_t n, int elem_bytes, uint32_t bits, hipStream_t s);
@@ -91,6 +94,5 @@ int launch_copy_strided(const void* src, void* dst, const StridedCopy& c, int el
 constexpr int kFwdBM = 128;      // query rows per forward workgroup
 constexpr int kBwdBK = 128;      // keys per backward workgroup
 constexpr int kBwdBQ = 32;       // query rows per backward inner step
-constexpr int kDecodeChunk = 256;  // cached keys per decode workgroup
 
 }  // namespace inf

@@ -211,6 +211,18 @@ def test_decode_f32(ia, B, H, Tk, D):
     assert oracle.rel_err(o, o_r) <= TOL_F32
 
 
+def test_decode_workspace_reuse(ia):
+    """One workspace serves consecutive calls of different shapes (contents on entry do not matter)."""
+    print("[case] decode workspace reuse", flush=True)
+    ws = torch.full((ia.workspace_bytes(ia.OP_ATTN_DECODE, 4, 12, 1, 2048, 64),), 0x7F, dtype=torch.uint8, device="cuda")
+    for i, (B, H, Tk) in enumerate(((4, 12, 2048), (4, 12, 2048), (2, 5, 1000), (4, 12, 2048))):
+        q = oracle.randn(700 + i, (B, H, 1, 64))
+        kc = oracle.randn(710 + i, (B, H, Tk, 64))
+        vc = oracle.randn(720 + i, (B, H, Tk, 64))
+        o = host(ia.attn_decode(dev(q), dev(kc), dev(vc), workspace=ws))
+        assert oracle.rel_err(o, oracle.attn_decode(q, kc, vc)) <= TOL_F32, f"call {i}"
+
+
 def test_decode_equals_last_prefill_row(ia):
     B, H, T, D = 1, 2, 300, 64
     q, k, v, _ = oracle.attn_inputs(B, H, T, D, seed=3)
