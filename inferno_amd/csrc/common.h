@@ -114,6 +114,19 @@ __device__ __forceinline__ f32x4 ld4(const uint16_t* p) {
     r[3] = bf16_to_f32(h[3]);
     return r;
 }
+// Streaming (non-temporal) 4-element loads for data read exactly once.
+__device__ __forceinline__ f32x4 ld4_nt(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+}
+__device__ __forceinline__ f32x4 ld4_nt(const uint16_t* p) {
+    const u16x4 h = __builtin_nontemporal_load(reinterpret_cast<const u16x4*>(p));
+    f32x4 r;
+    r[0] = bf16_to_f32(h[0]);
+    r[1] = bf16_to_f32(h[1]);
+    r[2] = bf16_to_f32(h[2]);
+    r[3] = bf16_to_f32(h[3]);
+    return r;
+}
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 __device__ __forceinline__ void st4(uint16_t* p, f32x4 v) {
     u16x4 h;

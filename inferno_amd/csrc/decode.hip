@@ -63,8 +63,8 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
         for (int u = 0; u < U; ++u) {
             jj[u] = j0 + (it * U + u) * NG + grp;
             if (jj[u] < j1) {
-                kr[u] = ld4(K + (int64_t)jj[u] * p.sk.t);
-                vr[u] = ld4(V + (int64_t)jj[u] * p.sv.t);
+                kr[u] = ld4_nt(K + (int64_t)jj[u] * p.sk.t);
+                vr[u] = ld4_nt(V + (int64_t)jj[u] * p.sv.t);
             } else {
                 kr[u] = vr[u] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
