@@ -240,10 +240,11 @@ static int launch_fwd_t(const FwdParams& p, hipStream_t s) {
 }
 
 int launch_attn_fwd(const FwdParams& p, int bf16, hipStream_t s) {
+    if (bf16) return launch_attn_fwd_bf16(p, s);
     switch (p.D) {
-        case 32: return bf16 ? launch_fwd_t<32, uint16_t>(p, s) : launch_fwd_t<32, float>(p, s);
-        case 64: return bf16 ? launch_fwd_t<64, uint16_t>(p, s) : launch_fwd_t<64, float>(p, s);
-        case 128: return bf16 ? launch_fwd_t<128, uint16_t>(p, s) : launch_fwd_t<128, float>(p, s);
+        case 32: return launch_fwd_t<32, float>(p, s);
+        case 64: return launch_fwd_t<64, float>(p, s);
+        case 128: return launch_fwd_t<128, float>(p, s);
         default: return (int)hipErrorInvalidValue;
     }
 }

@@ -1,0 +1,244 @@
+// attn_fwd_bf16.hip -- fused causal attention forward, bf16 inputs, fp32
+// accumulation, on v_mfma_f32_32x32x16_bf16 (gfx950).
+//
+// Same structure as the fp32 kernel (attn_fwd.hip): 4 waves x 32 query rows,
+// K/V tiles of 64 keys double-buffered through LDS, S^T = K Q^T and
+// O^T += V^T P^T with queries on the lane axis, online softmax in fp32.
+// What bf16 changes is the operand shape: one MFMA reduces 16 elements, each
+// lane supplying 8 consecutive ones.
+//   S^T:  A = K[key][8 d's]  -- a 16-byte row read from the row-major K tile
+//         B = Q[q][8 d's]    -- resident in VGPRs (D/4 registers)
+//   O^T:  B = P^T[8 keys][q] -- straight from the S^T accumulators: MFMA m of
+//         a 32-key block takes registers 8m..8m+7, i.e. keys
+//         16m + 4g + {0..3} and 16m + 8 + 4g + {0..3} (converted to bf16)
+//         A = V^T[d][the same 8 keys] -- V is stored transposed in LDS (keys
+//         contiguous per head-dim row), so this is two 8-byte reads.
+// The transpose happens once per tile while staging: each thread takes a key
+// pair and 8 head-dim columns and writes 8 dwords that pack (V[2k][d],
+// V[2k+1][d]).  Softmax statistics and the row sum stay fp32; P enters the
+// MFMA rounded to bf16.
+#include "common.h"
+#include "kernels.h"
+
+namespace inf {
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+template <int D>
+struct FwdBf16Tile {
+    static constexpr int BN = 64;       // keys per tile
+    static constexpr int KS = D + 8;    // K row stride in LDS (bf16 elements)
+    static constexpr int VS = BN + 4;   // V^T row stride in LDS (bf16 elements)
+};
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
+    constexpr int BM = kFwdBM;
+    constexpr int BN = FwdBf16Tile<D>::BN;
+    constexpr int KS = FwdBf16Tile<D>::KS;
+    constexpr int VS = FwdBf16Tile<D>::VS;
+    constexpr int NKK = D / 16;          // MFMAs along the head dim for S^T
+    constexpr int NKB = BN / 32;         // 32-key blocks per tile
+    constexpr int NDB = D / 32;          // 32-wide head-dim blocks of O^T
+    constexpr int C8 = D / 8;            // 8-element chunks per row
+    constexpr int KLPT = BN * C8 / 256;  // K chunks per thread per tile
+    constexpr int VTASKS = (BN / 2) * C8;      // V (key pair, chunk) tasks per tile
+    constexpr int VLPT = (VTASKS + 255) / 256;  // ... per thread
+    static_assert(BN * C8 % 256 == 0, "K staging assumes whole passes");
+
+    __shared__ __attribute__((aligned(16))) __bf16 Ks[2][BN][KS];
+    __shared__ __attribute__((aligned(16))) __bf16 Vt[2][D][VS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+
+    const int BH = p.B * p.H;
+    const int w = blockIdx.x;
+    const int qtile = p.n_qtiles - 1 - w / BH;
+    const int bh = w % BH;
+    const int b = bh / p.H;
+    const int h = bh % p.H;
+
+    const __bf16* Q = (const __bf16*)p.q + b * p.sq.b + h * p.sq.h;
+    const __bf16* K = (const __bf16*)p.k + b * p.sk.b + h * p.sk.h;
+    const __bf16* V = (const __bf16*)p.v + b * p.sv.b + h * p.sv.h;
+    uint16_t* O = (uint16_t*)p.o + b * p.so.b + h * p.so.h;
+
+    const int q0w = qtile * BM + wave * 32;
+    const int qrow = q0w + l32;
+
+    // Q operand: MFMA kk takes Q[qrow][16kk + 8g .. 16kk + 8g + 7].
+    bf16x8 qf[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+        if (qrow < p.Tq)
+            qf[kk] = *reinterpret_cast<const bf16x8*>(Q + (int64_t)qrow * p.sq.t + 16 * kk + 8 * g);
+        else
+            qf[kk] = bf16x8{};
+    }
+
+    int kv_end = p.Tk;
+    if (p.causal) kv_end = min(p.Tk, qtile * BM + BM + p.off);
+    const int n_tiles = (kv_end + BN - 1) / BN;
+    const int wave_kend = p.causal ? min(kv_end, q0w + 32 + p.off) : kv_end;
+
+    bf16x8 kr[KLPT], va[VLPT], vb[VLPT];
+    auto gload = [&](int t) {
+#pragma unroll
+        for (int i = 0; i < KLPT; ++i) {
+            const int f = tid + 256 * i;
+            const int row = f / C8, c8 = f % C8;
+            const int key = t * BN + row;
+            kr[i] = key < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)key * p.sk.t + 8 * c8) : bf16x8{};
+        }
+#pragma unroll
+        for (int i = 0; i < VLPT; ++i) {
+            const int f = tid + 256 * i;
+            const int kp = f % (BN / 2), c8 = f / (BN / 2);
+            const int key = t * BN + 2 * kp;
+            if (f >= VTASKS) continue;
+            va[i] = key < p.Tk ? *reinterpret_cast<const bf16x8*>(V + (int64_t)key * p.sv.t + 8 * c8) : bf16x8{};
+            vb[i] = key + 1 < p.Tk ? *reinterpret_cast<const bf16x8*>(V + (int64_t)(key + 1) * p.sv.t + 8 * c8)
+                                   : bf16x8{};
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < KLPT; ++i) {
+            const int f = tid + 256 * i;
+            const int row = f / C8, c8 = f % C8;
+            *reinterpret_cast<bf16x8*>(&Ks[buf][row][8 * c8]) = kr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VLPT; ++i) {
+            const int f = tid + 256 * i;
+            const int kp = f % (BN / 2), c8 = f / (BN / 2);
+            if (f >= VTASKS) continue;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+                bf16x2 pr;
+                pr[0] = va[i][e];
+                pr[1] = vb[i][e];
+                *reinterpret_cast<bf16x2*>(&Vt[buf][8 * c8 + e][2 * kp]) = pr;
+            }
+        }
+    };
+
+    f32x16 o[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) o[i] = f32x16{};
+    float m_run = -INFINITY;
+    float l_run = 0.f;
+    const float c = p.c;
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+
+    for (int t = 0; t < n_tiles; ++t) {
+        const int buf = t & 1;
+        const int k0 = t * BN;
+        if (t + 1 < n_tiles) gload(t + 1);
+
+        if (k0 < wave_kend) {
+            f32x16 s[NKB];
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) s[kb] = f32x16{};
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) {
+                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Ks[buf][kb * 32 + l32][16 * kk + 8 * g]);
+                    s[kb] = mfma32x32x16bf16(a, qf[kk], s[kb]);
+                }
+
+            const bool need_mask = (k0 + BN > p.Tk) || (p.causal && (k0 + BN - 1 > q0w + p.off));
+            if (need_mask) {
+                const int lim = p.causal ? min(p.Tk - 1, qrow + p.off) : p.Tk - 1;
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                        if (key > lim) s[kb][r] = -INFINITY;
+                    }
+            }
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kb][r]);
+            mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = fast_exp2((m_run - m_new) * c);
+            const float mc = m_new * c;
+            float lsum = 0.f;
+            bf16x8 pb[NKB][2];
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float e = fast_exp2(fmaf(s[kb][r], c, -mc));
+                    lsum += e;
+                    pb[kb][r >> 3][r & 7] = (__bf16)e;
+                }
+            l_run = fmaf(l_run, alpha, lsum);
+            m_run = m_new;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int mm = 0; mm < 2; ++mm) {
+                    const int key = kb * 32 + 16 * mm + 4 * g;
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        const __bf16* vrow = &Vt[buf][db * 32 + l32][0];
+                        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow + key);
+                        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + key + 8);
+                        const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                        o[db] = mfma32x32x16bf16(a, pb[kb][mm], o[db]);
+                    }
+                }
+        }
+
+        if (t + 1 < n_tiles) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    const float l_tot = l_run + shfl_xor(l_run, 32);
+    const float inv = 1.f / l_tot;
+    if (qrow < p.Tq) {
+        uint16_t* dst = O + (int64_t)qrow * p.so.t;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f32x4 val;
+                val[0] = o[db][4 * j + 0] * inv;
+                val[1] = o[db][4 * j + 1] * inv;
+                val[2] = o[db][4 * j + 2] * inv;
+                val[3] = o[db][4 * j + 3] * inv;
+                st4(dst + db * 32 + 8 * j + 4 * g, val);
+            }
+        if (g == 0 && p.lse) p.lse[(int64_t)bh * p.Tq + qrow] = m_run * p.scale + logf(l_tot);
+    }
+}
+
+int launch_attn_fwd_bf16(const FwdParams& p, hipStream_t s) {
+    const dim3 grid((unsigned)(p.n_qtiles * p.B * p.H));
+    switch (p.D) {
+        case 32: hipLaunchKernelGGL((attn_fwd_bf16_kernel<32>), grid, dim3(256), 0, s, p); break;
+        case 64: hipLaunchKernelGGL((attn_fwd_bf16_kernel<64>), grid, dim3(256), 0, s, p); break;
+        case 128: hipLaunchKernelGGL((attn_fwd_bf16_kernel<128>), grid, dim3(256), 0, s, p); break;
+        default: return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
+}  // namespace inf
