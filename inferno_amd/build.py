@@ -33,7 +33,7 @@ COMMON = [
     f"-I{CSRC}",
 ]
 
-SOURCES = ["capi.cpp", "attn_fwd.hip", "attn_fwd_bf16.hip", "attn_bwd.hip", "decode.hip", "softmax.hip", "elementwise.hip"]
+SOURCES = ["capi.cpp", "attn_fwd.hip", "attn_fwd_bf16.hip", "attn_bwd.hip", "attn_bwd_bf16.hip", "decode.hip", "softmax.hip", "elementwise.hip"]
 
 
 def _compile(src: Path, obj: Path) -> None:

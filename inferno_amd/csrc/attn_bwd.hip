@@ -24,7 +24,9 @@
 // global atomic add per element per 128-key block.  Workgroup w takes key
 // block w / (B*H), so the blocks with the most query tiles start first.
 //
-// Kernel 3 (bwd_cvt, bf16 only): dQ accumulator -> bf16 dq.
+// bf16 inputs use the bf16-MFMA main kernel (attn_bwd_bf16.hip) between the
+// same pre kernel and a final bwd_cvt that turns the fp32 dQ accumulator into
+// bf16 dq.
 #include "common.h"
 #include "kernels.h"
 
@@ -295,9 +297,14 @@ static int launch_bwd_t(const BwdParams& p, hipStream_t s) {
     const int64_t rows = (int64_t)p.B * p.H * p.Tq;
     const dim3 pre_grid((unsigned)((rows + RPB - 1) / RPB));
     hipLaunchKernelGGL((bwd_pre_kernel<D, E>), pre_grid, dim3(256), 0, s, p);
-    const dim3 grid((unsigned)(p.n_kblocks * p.B * p.H));
-    hipLaunchKernelGGL((bwd_main_kernel<D, E>), grid, dim3(256), 0, s, p);
-    if (sizeof(E) == 2) hipLaunchKernelGGL((bwd_cvt_kernel<D>), pre_grid, dim3(256), 0, s, p);
+    if constexpr (sizeof(E) == 2) {
+        const int e = launch_bwd_main_bf16(p, s);
+        if (e) return e;
+        hipLaunchKernelGGL((bwd_cvt_kernel<D>), pre_grid, dim3(256), 0, s, p);
+    } else {
+        const dim3 grid((unsigned)(p.n_kblocks * p.B * p.H));
+        hipLaunchKernelGGL((bwd_main_kernel<D, E>), grid, dim3(256), 0, s, p);
+    }
     return (int)hipGetLastError();
 }
 

@@ -1,0 +1,271 @@
+// attn_bwd_bf16.hip -- fused causal attention backward, bf16 inputs, fp32
+// accumulation, on gfx950 bf16 MFMAs.
+//
+// Same ownership as the fp32 kernel (attn_bwd.hip): 4 waves x 32 keys per
+// workgroup, K and V operands and the dK^T / dV^T accumulators in VGPRs for
+// the whole kernel (atomic-free dK, dV), query tiles of 32 rows, dQ through
+// LDS and fp32 atomics into the accumulator.  A bf16 MFMA reduces 16 (32x32x16)
+// or 32 (16x16x32) elements with each lane supplying 8 consecutive ones, so
+// every operand must be contiguous along its reduction index:
+//   S = Q K^T, dP = dO V^T      reduce over d: Q, dO row-major in LDS; K, V rows
+//                               in VGPRs
+//   dV^T += dO^T P, dK^T += Q^T dS
+//                               reduce over queries: dO and Q are also staged
+//                               transposed (queries contiguous per head-dim row);
+//                               P and dS come straight from the S / dP
+//                               accumulators, registers 8m..8m+7 = queries
+//                               16m + 4g + {0..3} and 16m + 8 + 4g + {0..3}
+//   dQ += dS K                  reduce over keys: dS (bf16) through LDS with
+//                               keys contiguous, K staged transposed once per
+//                               workgroup; v_mfma_f32_16x16x32_bf16 tiles
+// Transposed staging writes dwords that pack two rows' elements, so the LDS
+// stores stay 32-bit.  Softmax statistics, P and dS are computed in fp32.
+#include "common.h"
+#include "kernels.h"
+
+namespace inf {
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma16x16x32bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 cat4(bf16x4 lo, bf16x4 hi) {
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <int D>
+__global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(BwdParams p) {
+    constexpr int BQ = kBwdBQ;           // 32 query rows per step
+    constexpr int BK = kBwdBK;           // 128 keys per workgroup
+    constexpr int NKK = D / 16;          // S / dP MFMAs along d
+    constexpr int NDB = D / 32;          // 32-wide d blocks of dK^T / dV^T
+    constexpr int C8 = D / 8;            // 8-element chunks per row
+    constexpr int QS = D + 8;            // row-major Q / dO stride (bf16)
+    constexpr int TS = BQ + 4;           // transposed Q / dO stride (bf16)
+    constexpr int SS = BK + 8;           // dS stride (bf16)
+    constexpr int KTS = BK + 8;          // K^T stride (bf16)
+    constexpr int QTASK = (BQ / 2) * C8;                 // (row pair, chunk) tasks per tensor
+    constexpr int QLPT = (2 * QTASK + 255) / 256;        // Q and dO together, per thread
+    constexpr int KTASK = (BK / 2) * C8;
+    constexpr int KLPT = (KTASK + 255) / 256;
+    constexpr int DQB = D / 32;          // 16x16 dQ blocks per wave (2 * D/16 over 4 waves)
+
+    __shared__ __attribute__((aligned(16))) __bf16 Qs[BQ][QS];
+    __shared__ __attribute__((aligned(16))) __bf16 dOs[BQ][QS];
+    __shared__ __attribute__((aligned(16))) __bf16 QTs[D][TS];
+    __shared__ __attribute__((aligned(16))) __bf16 dOTs[D][TS];
+    __shared__ __attribute__((aligned(16))) __bf16 dSs[BQ][SS];
+    __shared__ __attribute__((aligned(16))) __bf16 KTs[D][KTS];
+    __shared__ __attribute__((aligned(16))) float lse_s[BQ];
+    __shared__ __attribute__((aligned(16))) float dl_s[BQ];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+    const int l16 = lane & 15;
+    const int g4 = lane >> 4;
+
+    const int BH = p.B * p.H;
+    const int w = blockIdx.x;
+    const int kblk = w / BH;
+    const int bh = w % BH;
+    const int b = bh / p.H;
+    const int h = bh % p.H;
+
+    const __bf16* Q = (const __bf16*)p.q + b * p.sq.b + h * p.sq.h;
+    const __bf16* K = (const __bf16*)p.k + b * p.sk.b + h * p.sk.h;
+    const __bf16* V = (const __bf16*)p.v + b * p.sv.b + h * p.sv.h;
+    const __bf16* dO = (const __bf16*)p.dout + b * p.sdo.b + h * p.sdo.h;
+    float* dQa = p.dq_acc + b * p.sacc.b + h * p.sacc.h;
+    const float* LSE = p.lse + (int64_t)bh * p.Tq;
+    const float* DL = p.delta + (int64_t)bh * p.Tq;
+
+    const int k0 = kblk * BK;
+    const int k0w = k0 + wave * 32;
+    const int key = k0w + l32;
+
+    // K / V operands: MFMA kk takes row `key`, columns 16kk + 8g .. +7.
+    bf16x8 kf[NKK], vf[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+        if (key < p.Tk) {
+            kf[kk] = *reinterpret_cast<const bf16x8*>(K + (int64_t)key * p.sk.t + 16 * kk + 8 * g);
+            vf[kk] = *reinterpret_cast<const bf16x8*>(V + (int64_t)key * p.sv.t + 16 * kk + 8 * g);
+        } else {
+            kf[kk] = vf[kk] = bf16x8{};
+        }
+    }
+
+    // K^T of the 128-key block (keys contiguous per d row), for dQ.
+#pragma unroll
+    for (int i = 0; i < KLPT; ++i) {
+        const int f = tid + 256 * i;
+        if (f >= KTASK) continue;
+        const int kp = f % (BK / 2), c8 = f / (BK / 2);
+        const int r0 = k0 + 2 * kp;
+        const bf16x8 a = r0 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)r0 * p.sk.t + 8 * c8) : bf16x8{};
+        const bf16x8 c = r0 + 1 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)(r0 + 1) * p.sk.t + 8 * c8)
+                                       : bf16x8{};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            bf16x2 pr;
+            pr[0] = a[e];
+            pr[1] = c[e];
+            *reinterpret_cast<bf16x2*>(&KTs[8 * c8 + e][2 * kp]) = pr;
+        }
+    }
+
+    f32x16 dv_acc[NDB], dk_acc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) {
+        dv_acc[i] = f32x16{};
+        dk_acc[i] = f32x16{};
+    }
+
+    int q_begin = 0;
+    if (p.causal) q_begin = max(0, k0 - p.off);
+    q_begin = (q_begin / BQ) * BQ;
+    const float c = p.c;
+
+    for (int q0 = q_begin; q0 < p.Tq; q0 += BQ) {
+        // ---- stage Q and dO, row-major and transposed --------------------------
+#pragma unroll
+        for (int i = 0; i < QLPT; ++i) {
+            const int f = tid + 256 * i;
+            if (f >= 2 * QTASK) continue;
+            const int which = f / QTASK;  // 0: Q, 1: dO
+            const int rem = f % QTASK;
+            const int qp = rem % (BQ / 2), c8 = rem / (BQ / 2);
+            const __bf16* src = which ? dO : Q;
+            const int64_t st = which ? p.sdo.t : p.sq.t;
+            const int r0 = q0 + 2 * qp;
+            const bf16x8 a = r0 < p.Tq ? *reinterpret_cast<const bf16x8*>(src + (int64_t)r0 * st + 8 * c8) : bf16x8{};
+            const bf16x8 bb = r0 + 1 < p.Tq ? *reinterpret_cast<const bf16x8*>(src + (int64_t)(r0 + 1) * st + 8 * c8)
+                                            : bf16x8{};
+            __bf16(*rows)[QS] = which ? dOs : Qs;
+            __bf16(*cols)[TS] = which ? dOTs : QTs;
+            *reinterpret_cast<bf16x8*>(&rows[2 * qp][8 * c8]) = a;
+            *reinterpret_cast<bf16x8*>(&rows[2 * qp + 1][8 * c8]) = bb;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                bf16x2 pr;
+                pr[0] = a[e];
+                pr[1] = bb[e];
+                *reinterpret_cast<bf16x2*>(&cols[8 * c8 + e][2 * qp]) = pr;
+            }
+        }
+        if (tid < BQ) {
+            const int qi = q0 + tid;
+            lse_s[tid] = (qi < p.Tq) ? LSE[qi] * kLog2e : 0.f;
+            dl_s[tid] = (qi < p.Tq) ? DL[qi] : 0.f;
+        }
+        __syncthreads();
+
+        const bool active = !p.causal || (q0 + BQ - 1 + p.off >= k0w);
+        bf16x8 pb[2], dsb[2];
+        if (active && k0w < p.Tk) {
+            f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk) {
+                const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&Qs[l32][16 * kk + 8 * g]);
+                const bf16x8 da = *reinterpret_cast<const bf16x8*>(&dOs[l32][16 * kk + 8 * g]);
+                s = mfma32x32x16bf16(qa, kf[kk], s);
+                dp = mfma32x32x16bf16(da, vf[kk], dp);
+            }
+            // P and dS; register r holds query row 8*(r/4) + 4*g + r%4 of the tile.
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]);
+                const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    const int r = 4 * j + cc;
+                    const int qi = q0 + 8 * j + 4 * g + cc;
+                    const bool vis = (qi < p.Tq) && (key < p.Tk) && (!p.causal || key <= qi + p.off);
+                    const float pr = vis ? fast_exp2(fmaf(s[r], c, -L[cc])) : 0.f;
+                    pb[r >> 3][r & 7] = (__bf16)pr;
+                    dsb[r >> 3][r & 7] = (__bf16)(pr * (dp[r] - Dl[cc]));
+                }
+            }
+            // dV^T += dO^T P ; dK^T += Q^T dS  (reduce over the 32 queries, 16 per MFMA)
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const int qc = 16 * m + 4 * g;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    const __bf16* dorow = &dOTs[db * 32 + l32][0];
+                    const __bf16* qrow = &QTs[db * 32 + l32][0];
+                    const bf16x8 ado = cat4(*reinterpret_cast<const bf16x4*>(dorow + qc),
+                                            *reinterpret_cast<const bf16x4*>(dorow + qc + 8));
+                    const bf16x8 aq = cat4(*reinterpret_cast<const bf16x4*>(qrow + qc),
+                                           *reinterpret_cast<const bf16x4*>(qrow + qc + 8));
+                    dv_acc[db] = mfma32x32x16bf16(ado, pb[m], dv_acc[db]);
+                    dk_acc[db] = mfma32x32x16bf16(aq, dsb[m], dk_acc[db]);
+                }
+            }
+        } else {
+            pb[0] = pb[1] = dsb[0] = dsb[1] = bf16x8{};
+        }
+        // dS block of this wave -> LDS (rows = queries, columns = the 128 keys)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dSs[8 * (r >> 2) + 4 * g + (r & 3)][wave * 32 + l32] = dsb[r >> 3][r & 7];
+        __syncthreads();
+
+        // ---- dQ tile (32 x D) += dS (32 x 128) K (128 x D), 16x16 blocks ---------
+#pragma unroll
+        for (int bi = 0; bi < DQB; ++bi) {
+            const int blk = wave * DQB + bi;
+            const int qh = blk & 1;
+            const int dc = blk >> 1;
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < BK / 32; ++kk) {
+                const bf16x8 a = *reinterpret_cast<const bf16x8*>(&dSs[16 * qh + l16][32 * kk + 8 * g4]);
+                const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&KTs[16 * dc + l16][32 * kk + 8 * g4]);
+                acc = mfma16x16x32bf16(a, bb, acc);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int qi = q0 + 16 * qh + 4 * g4 + r;
+                if (qi < p.Tq) unsafeAtomicAdd(dQa + (int64_t)qi * p.sacc.t + 16 * dc + l16, acc[r] * p.scale);
+            }
+        }
+        __syncthreads();
+    }
+
+    if (key < p.Tk) {
+        uint16_t* dKp = (uint16_t*)p.dk + b * p.sdk.b + h * p.sdk.h + (int64_t)key * p.sdk.t;
+        uint16_t* dVp = (uint16_t*)p.dv + b * p.sdv.b + h * p.sdv.h + (int64_t)key * p.sdv.t;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f32x4 a, v;
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    a[cc] = dk_acc[db][4 * j + cc] * p.scale;
+                    v[cc] = dv_acc[db][4 * j + cc];
+                }
+                st4(dKp + db * 32 + 8 * j + 4 * g, a);
+                st4(dVp + db * 32 + 8 * j + 4 * g, v);
+            }
+    }
+}
+
+int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s) {
+    const dim3 grid((unsigned)(p.n_kblocks * p.B * p.H));
+    switch (p.D) {
+        case 32: hipLaunchKernelGGL((bwd_main_bf16_kernel<32>), grid, dim3(256), 0, s, p); break;
+        case 64: hipLaunchKernelGGL((bwd_main_bf16_kernel<64>), grid, dim3(256), 0, s, p); break;
+        case 128: hipLaunchKernelGGL((bwd_main_bf16_kernel<128>), grid, dim3(256), 0, s, p); break;
+        default: return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
+}  // namespace inf

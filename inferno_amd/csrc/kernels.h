@@ -81,6 +81,7 @@ struct StridedCopy {      // element strides of source and destination
 int launch_attn_fwd(const FwdParams& p, int bf16, hipStream_t s);
 int launch_attn_fwd_bf16(const FwdParams& p, hipStream_t s);  // bf16-MFMA forward
 int launch_attn_bwd(const BwdParams& p, int bf16, hipStream_t s);
+int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s);  // bf16-MFMA backward main kernel
 int launch_attn_decode(const DecodeParams& p, int bf16, hipStream_t s);
 // Decode split plan (number of key splits per row, keys per split) for a shape.
 void decode_plan(int B, int H, int Tk, int D, int* nsplit, int* chunk);
