@@ -10,9 +10,16 @@
 //   online softmax on S^T             query = lane%32, so the row max needs one
 //                                     xor-32 exchange; the row sum stays
 //                                     per-lane until the end
-//   O^T (d x queries) += V^T P^T      A = V from LDS, B = P^T straight from the
-//                                     S^T accumulators (reduction index
+//   O^T (d x queries) += V^T P^T      A = V^T from LDS, B = P^T straight from
+//                                     the S^T accumulators (reduction index
 //                                     permuted to match their layout)
+//
+// V is stored transposed in LDS (Vt[d][key]) so that the four keys a lane
+// feeds to four consecutive MFMAs are adjacent: one ds_read_b128 per four
+// MFMAs in both products, issued well ahead of use, instead of a dependent
+// ds_read_b32 per MFMA.  V tiles are fetched with a row-fastest lane mapping
+// (16 keys x 4 column chunks per wave) so the transposing LDS stores hit 64
+// distinct banks.
 //
 // Keeping queries on the lane axis in both products is what lets P stay in
 // registers.  The scale is folded into exp2: p = exp2(s*c - m*c) with
@@ -34,7 +41,7 @@ template <int D>
 struct FwdTile {
     static constexpr int BN = (D >= 128) ? 32 : 64;  // keys per LDS tile
     static constexpr int KS = D + 4;                 // K row stride in LDS (floats)
-    static constexpr int VS = D + 8;                 // V row stride in LDS (floats)
+    static constexpr int VTS = BN + 4;               // V^T row stride in LDS (floats)
 };
 
 template <int D, typename E>
@@ -42,7 +49,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
     constexpr int BM = kFwdBM;
     constexpr int BN = FwdTile<D>::BN;
     constexpr int KS = FwdTile<D>::KS;
-    constexpr int VS = FwdTile<D>::VS;
+    constexpr int VTS = FwdTile<D>::VTS;
     constexpr int HD = D / 2;        // reduction elements per lane half
     constexpr int NKB = BN / 32;     // 32-key blocks per tile
     constexpr int NDB = D / 32;      // 32-wide head-dim blocks
@@ -50,7 +57,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
     constexpr int LPT = BN * C4 / 256;  // 4-element loads per thread per tensor per tile
 
     __shared__ __attribute__((aligned(16))) float Ks[2][BN][KS];
-    __shared__ __attribute__((aligned(16))) float Vs[2][BN][VS];
+    __shared__ __attribute__((aligned(16))) float Vt[2][D][VTS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -96,31 +103,32 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
     const int n_tiles = (kv_end + BN - 1) / BN;
     const int wave_kend = p.causal ? min(kv_end, q0w + 32 + p.off) : kv_end;
 
+    // K: chunk f -> (row f / C4, column chunk f % C4), row-major 16-byte loads.
+    // V: chunk f -> (row f % 16 + 16 * (f / (16 * C4)), column chunk (f / 16) % C4).
     f32x4 kr[LPT], vr[LPT];
     auto gload = [&](int t) {
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
             const int f = tid + 256 * i;
-            const int row = f / C4;
-            const int c4 = f % C4;
-            const int key = t * BN + row;
-            if (key < p.Tk) {
-                kr[i] = ld4(K + (int64_t)key * p.sk.t + 4 * c4);
-                vr[i] = ld4(V + (int64_t)key * p.sv.t + 4 * c4);
-            } else {
-                kr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-                vr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
+            const int krow = t * BN + f / C4;
+            const int vrow = t * BN + (f & 15) + 16 * (f / (16 * C4));
+            kr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            vr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (krow < p.Tk) kr[i] = ld4(K + (int64_t)krow * p.sk.t + 4 * (f % C4));
+            if (vrow < p.Tk) vr[i] = ld4(V + (int64_t)vrow * p.sv.t + 4 * ((f >> 4) % C4));
         }
     };
     auto sstore = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
             const int f = tid + 256 * i;
-            const int row = f / C4;
-            const int c4 = f % C4;
-            *reinterpret_cast<f32x4*>(&Ks[buf][row][4 * c4]) = kr[i];
-            *reinterpret_cast<f32x4*>(&Vs[buf][row][4 * c4]) = vr[i];
+            *reinterpret_cast<f32x4*>(&Ks[buf][f / C4][4 * (f % C4)]) = kr[i];
+            const int vrow = (f & 15) + 16 * (f / (16 * C4));
+            const int vc = 4 * ((f >> 4) % C4);
+            Vt[buf][vc + 0][vrow] = vr[i][0];
+            Vt[buf][vc + 1][vrow] = vr[i][1];
+            Vt[buf][vc + 2][vrow] = vr[i][2];
+            Vt[buf][vc + 3][vrow] = vr[i][3];
         }
     };
 
@@ -195,16 +203,21 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
             for (int db = 0; db < NDB; ++db) o[db] *= alpha;
 
             // ---- O^T += V^T P^T --------------------------------------------------
+            // reg 4j+cc of s[kb] holds key kb*32 + 8j + 4g + cc
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-                for (int kk = 0; kk < 16; ++kk) {
-                    const int key = kb * 32 + 8 * (kk >> 2) + 4 * g + (kk & 3);
+                for (int j = 0; j < 4; ++j) {
+                    f32x4 va[NDB];
 #pragma unroll
-                    for (int db = 0; db < NDB; ++db) {
-                        const float a = Vs[buf][key][db * 32 + l32];
-                        o[db] = mfma32x32x2(a, s[kb][kk], o[db]);
-                    }
+                    for (int db = 0; db < NDB; ++db)
+                        va[db] = *reinterpret_cast<const f32x4*>(
+                            &Vt[buf][db * 32 + l32][kb * 32 + 8 * j + 4 * g]);
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+                        for (int db = 0; db < NDB; ++db)
+                            o[db] = mfma32x32x2(va[db][cc], s[kb][4 * j + cc], o[db]);
                 }
         }
 
