@@ -157,6 +157,107 @@ int inf_copy_strided(const void* src, const int64_t* src_strides, void* dst,
                      const int64_t* dst_strides, int ndim, const int64_t* shape, int elem_bytes,
                      void* stream);
 
+/* ---- model ops either side of the path: the GPT training step -------------
+ * (embedding -> [LayerNorm -> MultiHeadAttention -> residual
+ * -> LayerNorm -> Linear -> GELU -> Linear -> residual] x L -> LayerNorm ->
+ * tied logits -> cross-entropy -> AdamW).  Same conventions as above: host-side
+ * validation first, no allocation, caller-provided workspaces (sizes from
+ * inf_nn_workspace_bytes), asynchronous on `stream`.  Matrices are row-major
+ * with a leading dimension in elements; fp32 or bf16 storage, fp32 arithmetic;
+ * LayerNorm parameters, statistics, AdamW moments and reductions are fp32. */
+
+enum { INF_OP_GEMM = 3, INF_OP_LAYERNORM_BWD = 4, INF_OP_COL_SUM = 5, INF_OP_CROSS_ENTROPY = 6 };
+
+/* Workspace bytes for a model op: INF_OP_GEMM (any shape; the hipBLASLt
+ * workspace), INF_OP_LAYERNORM_BWD (rows, cols = dim), INF_OP_COL_SUM (rows,
+ * cols), INF_OP_CROSS_ENTROPY (rows, cols = vocab). */
+int inf_nn_workspace_bytes(int op, int64_t rows, int64_t cols, size_t* out_bytes);
+
+/* C[b] = alpha * op(A[b]) op(B[b]) + beta * C[b] (+ bias[n] added to every row)
+ * for b < batch, row-major: op(A) is M x K (A stored M x K, or K x M when
+ * trans_a), op(B) is K x N (B stored K x N, or N x K when trans_b); batch
+ * strides in elements.  Runs on hipBLASLt (fp32 matrix cores for fp32).
+ * Replaces cublas_mm_strided_batched_row_major and cuda_matmul
+ * (src/inferno/cuda/cudamatmul.cu:120-216, 1114-1179) behind matmul
+ * (src/inferno/core/ops.cpp:437-735) and Linear::forward (linear.cpp:49-54). */
+int inf_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha, const void* A, int64_t lda,
+             int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b, float beta, void* C, int64_t ldc,
+             int64_t stride_c, int64_t batch, const void* bias, inf_dtype dt, void* workspace, size_t ws_bytes,
+             void* stream);
+
+/* LayerNorm over the last `dim` elements of each of `rows` rows:
+ * y = (x - mean) / sqrt(var + eps) * gamma + beta (biased variance), and the
+ * per-row mean and 1/sqrt(var + eps) (either may be NULL).  Replaces
+ * cuda_layer_normalization (src/inferno/cuda/cudaops.h:78, cudalayernorm.cu)
+ * behind LayerNorm::forward (src/inferno/modules/layernorm.cpp:33-80). */
+int inf_layernorm_fwd(const void* x, int64_t ldx, void* y, int64_t ldy, const float* gamma, const float* beta,
+                      float* mean, float* invstd, int64_t rows, int64_t dim, float eps, inf_dtype dt, void* stream);
+
+/* LayerNorm backward from the saved mean / invstd: dx, and dgamma = sum_rows
+ * dy * xhat, dbeta = sum_rows dy (overwritten, or added to when accumulate).
+ * dim % 4 == 0 and dim <= 2048.  Replaces cuda_layernorm_backward
+ * (src/inferno/cuda/cudaops.h:82) behind LayerNormBackward
+ * (src/inferno/gradfn/layernormbackward.cpp:29-110). */
+int inf_layernorm_bwd(const void* x, int64_t ldx, const void* dy, int64_t lddy, const float* gamma, const float* mean,
+                      const float* invstd, void* dx, int64_t lddx, float* dgamma, float* dbeta, int accumulate,
+                      int64_t rows, int64_t dim, inf_dtype dt, void* workspace, size_t ws_bytes, void* stream);
+
+/* tanh-approximation GELU, y = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))),
+ * and its backward dx = dy * gelu'(x), over n dense elements.  Replaces
+ * cuda_gelu / cuda_gelu_backward (src/inferno/cuda/cudaops.h:130, 137) behind
+ * gelu (src/inferno/functional/gelu.cpp) and GeluBackward. */
+int inf_gelu_fwd(const void* x, void* y, int64_t n, inf_dtype dt, void* stream);
+int inf_gelu_bwd(const void* x, const void* dy, void* dx, int64_t n, inf_dtype dt, void* stream);
+
+/* Mean cross-entropy over rows of logits [rows, vocab] (row stride ld) with
+ * int32 targets: loss[0] = mean_r (lse_r - logits[r, target_r]), and the
+ * per-row lse for the backward.  A target outside [0, vocab) makes the loss
+ * NaN (the reference exits).  Replaces cuda_cross_entropy_loss
+ * (src/inferno/cuda/cudaops.h:186) behind CrossEntropyLoss::forward
+ * (src/inferno/loss/crossentropyloss.cpp). */
+int inf_cross_entropy_fwd(const void* logits, int64_t ld, const int32_t* targets, float* loss, float* lse,
+                          int64_t rows, int64_t vocab, inf_dtype dt, void* workspace, size_t ws_bytes, void* stream);
+
+/* dlogits = (softmax(logits) - onehot(target)) * upstream[0] / rows, from the
+ * forward's lse.  Replaces cuda_cross_entropy_loss_backward
+ * (src/inferno/cuda/cudaops.h:190) behind CrossEntropyLossBackward. */
+int inf_cross_entropy_bwd(const void* logits, int64_t ld, const int32_t* targets, const float* lse,
+                          const float* upstream, void* dlogits, int64_t ldg, int64_t rows, int64_t vocab, inf_dtype dt,
+                          void* stream);
+
+/* out[t, :] = table[ids[t], :] (dim % 4 == 0; an id outside [0, vocab) gives a
+ * NaN row).  Replaces cuda_embedding (src/inferno/cuda/cudaops.h:65). */
+int inf_embedding_fwd(const int32_t* ids, int64_t n_tokens, const void* table, int64_t vocab, int64_t dim, void* out,
+                      inf_dtype dt, void* stream);
+
+/* dtable[ids[t], :] += dout[t, :] (fp32, atomic); zero_first clears dtable
+ * first.  Replaces cuda_scatter_add_embedding (src/inferno/cuda/cudaops.h:68)
+ * behind EmbeddingBackward. */
+int inf_embedding_bwd(const int32_t* ids, int64_t n_tokens, const float* dout, int64_t vocab, int64_t dim,
+                      float* dtable, int zero_first, void* stream);
+
+/* One AdamW update of n elements (p, g in dt; m, v fp32), bias corrections
+ * computed by the caller: m = b1 m + (1-b1) g; v = b2 v + (1-b2) g^2;
+ * p -= lr * ((m/bc1) / (sqrt(v/bc2) + eps) + wd * p).  Replaces
+ * cuda_adamw_step_impl (src/inferno/cuda/cudaops.h:61) behind
+ * OptimizerAdamW::step (src/inferno/optim/adamw.cpp). */
+int inf_adamw_step(void* p, const void* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2, float eps,
+                   float weight_decay, float bias_correction1, float bias_correction2, inf_dtype dt, void* stream);
+
+/* out[c] = sum_r x[r * ldx + c] (or out[c] += when accumulate), fp32 result:
+ * the bias gradient of Linear and the gradient of a broadcast operand.
+ * Replaces cuda_sum_to_shape (src/inferno/cuda/cudaops.h:43) for reductions
+ * over leading dimensions. */
+int inf_col_sum(const void* x, int64_t rows, int64_t cols, int64_t ldx, float* out, int accumulate, inf_dtype dt,
+                void* workspace, size_t ws_bytes, void* stream);
+
+/* out[i] = a[i] (op) b[i % nb] for i < n (b repeated over leading dimensions:
+ * a bias over rows, a positional table over the batch); op INF_BIN_ADD or
+ * INF_BIN_MUL.  Replaces cuda_add / cuda_multiply (cudaadd.cu, cudamultiply.cu)
+ * for trailing broadcasts. */
+int inf_binary_bcast(int op, const void* a, const void* b, void* out, int64_t n, int64_t nb, inf_dtype dt,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

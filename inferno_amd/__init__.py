@@ -45,6 +45,19 @@ EXPORTS = (
     "inf_fill",
     "inf_binary",
     "inf_copy_strided",
+    "inf_nn_workspace_bytes",
+    "inf_gemm",
+    "inf_layernorm_fwd",
+    "inf_layernorm_bwd",
+    "inf_gelu_fwd",
+    "inf_gelu_bwd",
+    "inf_cross_entropy_fwd",
+    "inf_cross_entropy_bwd",
+    "inf_embedding_fwd",
+    "inf_embedding_bwd",
+    "inf_adamw_step",
+    "inf_col_sum",
+    "inf_binary_bcast",
 )
 
 
@@ -100,6 +113,24 @@ def lib() -> ctypes.CDLL:
         i64p = ctypes.POINTER(ctypes.c_int64)
         L.inf_copy_strided.argtypes = [vp, i64p, vp, i64p, i32, i64p, i32, vp]
         L.inf_copy_strided.restype = i32
+        sz = ctypes.c_size_t
+        L.inf_nn_workspace_bytes.argtypes = [i32, i64, i64, ctypes.POINTER(sz)]
+        L.inf_gemm.argtypes = [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64, f32, vp, i64, i64, i64,
+                               vp, i32, vp, sz, vp]
+        L.inf_layernorm_fwd.argtypes = [vp, i64, vp, i64, vp, vp, vp, vp, i64, i64, f32, i32, vp]
+        L.inf_layernorm_bwd.argtypes = [vp, i64, vp, i64, vp, vp, vp, vp, i64, vp, vp, i32, i64, i64, i32, vp, sz,
+                                        vp]
+        L.inf_gelu_fwd.argtypes = [vp, vp, i64, i32, vp]
+        L.inf_gelu_bwd.argtypes = [vp, vp, vp, i64, i32, vp]
+        L.inf_cross_entropy_fwd.argtypes = [vp, i64, vp, vp, vp, i64, i64, i32, vp, sz, vp]
+        L.inf_cross_entropy_bwd.argtypes = [vp, i64, vp, vp, vp, vp, i64, i64, i64, i32, vp]
+        L.inf_embedding_fwd.argtypes = [vp, i64, vp, i64, i64, vp, i32, vp]
+        L.inf_embedding_bwd.argtypes = [vp, i64, vp, i64, i64, vp, i32, vp]
+        L.inf_adamw_step.argtypes = [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, i32, vp]
+        L.inf_col_sum.argtypes = [vp, i64, i64, i64, vp, i32, i32, vp, sz, vp]
+        L.inf_binary_bcast.argtypes = [i32, vp, vp, vp, i64, i64, i32, vp]
+        for name in EXPORTS[11:]:
+            getattr(L, name).restype = i32
         _lib = L
     return _lib
 
@@ -113,6 +144,17 @@ def workspace_bytes(op: int, B: int, H: int, Tq: int, Tk: int, D: int, dtype: in
     st = lib().inf_attn_workspace_bytes(op, B, H, Tq, Tk, D, dtype, ctypes.byref(out))
     if st:
         raise InfernoError(st, "inf_attn_workspace_bytes")
+    return int(out.value)
+
+
+OP_GEMM, OP_LAYERNORM_BWD, OP_COL_SUM, OP_CROSS_ENTROPY = 3, 4, 5, 6
+
+
+def nn_workspace_bytes(op: int, rows: int = 0, cols: int = 0) -> int:
+    out = ctypes.c_size_t(0)
+    st = lib().inf_nn_workspace_bytes(op, rows, cols, ctypes.byref(out))
+    if st:
+        raise InfernoError(st, "inf_nn_workspace_bytes")
     return int(out.value)
 
 
@@ -130,6 +172,20 @@ from .ops import (  # noqa: E402  (torch-facing helpers need lib())
     softmax_bwd,
     softmax_fwd,
     strides_of,
+)
+from .nn import (  # noqa: E402
+    adamw_step,
+    col_sum,
+    cross_entropy_bwd,
+    cross_entropy_fwd,
+    embedding_bwd,
+    embedding_fwd,
+    gelu_bwd,
+    gelu_fwd,
+    gemm,
+    layernorm_bwd,
+    layernorm_fwd,
+    binary_bcast,
 )
 
 __all__ = [

@@ -33,7 +33,8 @@ COMMON = [
     f"-I{CSRC}",
 ]
 
-SOURCES = ["capi.cpp", "attn_fwd.hip", "attn_fwd_bf16.hip", "attn_bwd.hip", "attn_bwd_bf16.hip", "decode.hip", "softmax.hip", "elementwise.hip"]
+SOURCES = ["capi.cpp", "attn_fwd.hip", "attn_fwd_bf16.hip", "attn_bwd.hip", "attn_bwd_bf16.hip", "decode.hip", "softmax.hip", "elementwise.hip", "nn.hip",
+           "capi_nn.cpp", "gemm.cpp"]
 
 
 def _compile(src: Path, obj: Path) -> None:
@@ -101,7 +102,8 @@ def build(verbose: bool = True) -> Path:
         for j in jobs:
             j.result()
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
+           f"-L{ROCM / 'lib'}", "-lhipblaslt", f"-Wl,-rpath,{ROCM / 'lib'}"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

@@ -77,6 +77,99 @@ struct StridedCopy {      // element strides of source and destination
     int64_t dstride[kMaxRank];
 };
 
+// ---- model ops around the attention path (nn.hip) ----------------------------
+struct LnParams {         // LayerNorm forward over rows of `dim` (unit column stride)
+    const void* x;
+    void* y;
+    const float* gamma;
+    const float* beta;
+    float* mean;          // [rows] or null
+    float* invstd;        // [rows] or null
+    int64_t rows, ldx, ldy;
+    int dim;
+    float eps;
+    int vec;              // 16-byte rows and parameters: the register kernel
+};
+
+struct LnBwdParams {
+    const void* x;
+    const void* dy;
+    void* dx;
+    const float* gamma;
+    const float* mean;
+    const float* invstd;
+    float* dgamma;
+    float* dbeta;
+    float* part;          // workspace: 2 * ln_bwd_blocks(rows) * dim floats
+    int64_t rows, ldx, lddy, lddx;
+    int dim;
+    int accumulate;       // add into dgamma / dbeta instead of overwriting
+};
+
+struct CeParams {
+    const void* logits;   // [rows, vocab], row stride ld
+    const int32_t* targets;
+    float* row_loss;      // workspace [rows]
+    float* lse;           // [rows]: written by the forward, read by the backward
+    const float* upstream;  // backward: the loss gradient (one element)
+    void* grad;           // backward: dlogits, row stride ldg
+    int64_t rows, vocab, ld, ldg;
+};
+
+struct EmbParams {
+    const int32_t* ids;   // [n_tokens]
+    const void* table;    // [vocab, dim]
+    const void* dout;     // backward: [n_tokens, dim] fp32
+    void* out;            // forward: [n_tokens, dim]; backward: dtable [vocab, dim] fp32 (zeroed)
+    int64_t n_tokens, vocab, dim;
+};
+
+struct AdamWParams {
+    void* p;
+    const void* g;
+    float* m;
+    float* v;
+    int64_t n;
+    float lr, beta1, beta2, eps, weight_decay, bc1, bc2;
+};
+
+struct GemmArgs {         // row-major C = alpha * op(A) op(B) + beta * C (+ bias[N] per row)
+    int ta, tb, bf16;
+    int64_t M, N, K;
+    float alpha, beta;
+    const void* A;
+    int64_t lda, sa;
+    const void* B;
+    int64_t ldb, sb;
+    void* C;
+    int64_t ldc, sc;
+    int64_t batch;
+    const void* bias;     // [N] or null
+    void* ws;
+    size_t ws_bytes;
+};
+// 0 = ok, 1 = library error, 2 = no algorithm for the problem
+int launch_gemm(const GemmArgs& g, hipStream_t s);
+
+constexpr int kLnBwdMaxBlocks = 512;  // stage-1 workgroups of the LayerNorm backward
+constexpr int kLnBwdMaxDim = 2048;    // register path of the LayerNorm backward
+int ln_bwd_blocks(int64_t rows);
+int col_sum_chunks(int64_t rows);     // partial rows the column sum needs
+
+int launch_ln_fwd(const LnParams& p, int bf16, hipStream_t s);
+int launch_ln_bwd(const LnBwdParams& p, int bf16, hipStream_t s);
+int launch_col_sum(const void* x, float* out, float* part, int64_t rows, int64_t cols, int64_t ldx, int accumulate,
+                   int bf16, hipStream_t s);
+int launch_gelu_fwd(const void* x, void* y, int64_t n, int bf16, hipStream_t s);
+int launch_gelu_bwd(const void* x, const void* dy, void* dx, int64_t n, int bf16, hipStream_t s);
+int launch_ce_fwd(const CeParams& p, float* loss, int bf16, hipStream_t s);
+int launch_ce_bwd(const CeParams& p, int bf16, hipStream_t s);
+int launch_embed_fwd(const EmbParams& p, int bf16, hipStream_t s);
+int launch_embed_bwd(const EmbParams& p, hipStream_t s);
+int launch_adamw(const AdamWParams& a, int bf16, hipStream_t s);
+int launch_bcast(int op, const void* a, const void* b, void* out, int64_t n, int64_t nb, int vec, int bf16,
+                 hipStream_t s);
+
 // Launchers return a hipError_t value (0 = hipSuccess).
 int launch_attn_fwd(const FwdParams& p, int bf16, hipStream_t s);
 int launch_attn_fwd_bf16(const FwdParams& p, hipStream_t s);  // bf16-MFMA forward

@@ -77,6 +77,40 @@ void orc_attn_bwd_f32(const float* q, const float* k, const float* v, const floa
 void orc_attn_decode_f32(const float* q, const float* kc, const float* vc,
                          int64_t B, int64_t H, int64_t Tk, int64_t D, float scale, float* o);
 
+/* ---- model ops around the path (oracle_nn.c) ----------------------------- */
+/* cpu_layer_normalization (src/inferno/modules/layernorm_kernels.h:48-87):
+ * mean and biased variance in fp32 sequential sums, invstd = 1/sqrtf(var+eps);
+ * mean_out / invstd_out may be NULL. */
+void orc_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y, float* mean_out,
+                       float* invstd_out, int64_t rows, int64_t dim, float eps);
+/* cpu_layernorm_backward (src/inferno/gradfn/layernormbackward.h:47-97) */
+void orc_layernorm_bwd_f32(const float* x, const float* gout, const float* gamma, const float* mean,
+                           const float* invstd, float* gx, float* ggamma, float* gbeta, int64_t rows, int64_t dim);
+/* cpu_gelu (src/inferno/functional/gelu_kernels.h:9-27): tanh approximation */
+void orc_gelu_f32(const float* x, float* y, int64_t n);
+/* cpu_gelu_backward (src/inferno/gradfn/gelubackward.h:27-61) */
+void orc_gelu_bwd_f32(const float* x, const float* g, float* dx, int64_t n);
+/* cpu_cross_entropy_loss (src/inferno/core/cpuops.h:707-749): mean over rows;
+ * out[0] = NaN for a target outside [0, vocab) (the reference exits) */
+void orc_cross_entropy_f32(const float* logits, const int32_t* targets, float* out, int64_t rows, int64_t vocab);
+/* cpu_cross_entropy_loss_backward (src/inferno/gradfn/crossentropylossbackward.h:45-86) */
+void orc_cross_entropy_bwd_f32(const float* logits, const int32_t* targets, const float* upstream, float* grad,
+                               int64_t rows, int64_t vocab);
+/* cpu_embedding (src/inferno/modules/embedding_kernels.h:19-31) */
+void orc_embedding_f32(const int32_t* ids, const float* table, float* out, int64_t n_tokens, int64_t dim);
+/* scatter_add_embedding / cpu_scatter_add_embedding (src/inferno/core/broadcastops.cpp:120-166,
+ * broadcastops.h:61-74) into a zeroed table gradient */
+void orc_embedding_bwd_f32(const int32_t* ids, const float* gout, float* dtable, int64_t n_tokens, int64_t vocab,
+                           int64_t dim);
+/* cpu_adamw_step_impl (include/inferno/optim/adamw.h:67-111) */
+void orc_adamw_f32(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                   float eps, float weight_decay, float bc1, float bc2);
+/* OptimizerAdamW::step's bias correction 1 - pow(beta, step) in float (src/inferno/optim/adamw.cpp) */
+float orc_adamw_bias_correction(float beta, int64_t step);
+/* cpu_sum_to_shape (src/inferno/core/broadcastops.h:22-48) for [rows, cols] -> [cols]:
+ * the source is walked in linear order, each element added to its column */
+void orc_sum_rows_f32(const float* x, float* out, int64_t rows, int64_t cols);
+
 #ifdef __cplusplus
 }
 #endif

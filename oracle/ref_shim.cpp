@@ -8,8 +8,13 @@
 // arithmetic, bit for bit.
 //
 // What is reachable here: cpu_matmul, cpu_multiply, cpu_triu, cpu_masked_fill,
-// cpu_contiguous_copy (src/inferno/core/cpuops.h) and cpu_softmax
-// (src/inferno/functional/softmax_kernels.h).  cpu_softmax_backward
+// cpu_contiguous_copy, cpu_cross_entropy_loss (src/inferno/core/cpuops.h),
+// cpu_softmax (src/inferno/functional/softmax_kernels.h), cpu_gelu
+// (gelu_kernels.h), cpu_gelu_backward (src/inferno/gradfn/gelubackward.h),
+// cpu_embedding (src/inferno/modules/embedding_kernels.h),
+// cpu_layer_normalization (layernorm_kernels.h) and cpu_adamw_step_impl
+// (include/inferno/optim/adamw.h).  cpu_layernorm_backward and
+// cpu_cross_entropy_loss_backward are not (their headers pull broadcastops.h).  cpu_softmax_backward
 // (src/inferno/gradfn/softmaxbackward.h) is not: that header pulls
 // tensorimpl.h -> cudastorage.h -> <cuda_runtime.h>.  Logger::Append is
 // referenced only on cpu_matmul's rank<2 error path; its definition
@@ -29,6 +34,11 @@
 #include "inferno/util/logger.h"
 #include "inferno/core/cpuops.h"
 #include "inferno/functional/softmax_kernels.h"
+#include "inferno/functional/gelu_kernels.h"
+#include "inferno/gradfn/gelubackward.h"
+#include "inferno/modules/embedding_kernels.h"
+#include "inferno/modules/layernorm_kernels.h"
+#include "inferno/optim/adamw.h"
 
 using Shape = std::vector<size_t>;
 
@@ -140,6 +150,32 @@ void ref_attn_bwd_stages_f32(const float* q, const float* k, const float* v, con
     ref_transpose_contig_f32(q, B, H, T, D, qt.data());
     ref_matmul4_f32(qt.data(), dt, dss.data(), tt, dkt.data(), B, H, D, T, T);
     ref_transpose_contig_f32(dkt.data(), B, H, D, T, dk);
+}
+
+// ---- model ops around the path ----------------------------------------------
+
+void ref_layernorm_f32(const float* x, const float* gamma, const float* beta, float* y, float* mean, float* invstd,
+                       int64_t rows, int64_t dim, float eps) {
+    Inferno::cpu_layer_normalization<float>(x, y, gamma, beta, mean, invstd, (size_t)rows, (size_t)dim, eps);
+}
+
+void ref_gelu_f32(const float* x, float* y, int64_t n) { Inferno::cpu_gelu<float, float>(x, y, (size_t)n, 0); }
+
+void ref_gelu_bwd_f32(const float* x, const float* g, float* dx, int64_t n) {
+    Inferno::cpu_gelu_backward<float, float, float>(x, g, dx, (size_t)n, 0);
+}
+
+void ref_cross_entropy_f32(const float* logits, const int32_t* targets, float* out, int64_t rows, int64_t vocab) {
+    Inferno::cpu_cross_entropy_loss<float>(logits, targets, out, (size_t)rows, (size_t)vocab);
+}
+
+void ref_embedding_f32(const int32_t* ids, const float* table, float* out, int64_t n_tokens, int64_t dim) {
+    Inferno::cpu_embedding<float, int>(ids, table, out, 1, (size_t)n_tokens, (size_t)dim);
+}
+
+void ref_adamw_f32(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                   float eps, float weight_decay, float bc1, float bc2) {
+    Inferno::cpu_adamw_step_impl<float, float>(p, g, m, v, (size_t)n, lr, beta1, beta2, eps, weight_decay, bc1, bc2);
 }
 
 }  // extern "C"
