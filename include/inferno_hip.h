@@ -61,6 +61,11 @@ enum { INF_OP_ATTN_FWD = 0, INF_OP_ATTN_BWD = 1, INF_OP_ATTN_DECODE = 2 };
 /* Human-readable text for a status code (static storage). */
 const char* inf_status_string(int status);
 
+/* Text about the most recent failure inside the library on the calling thread
+ * (which library call failed, with its status and the problem shape), or ""
+ * (thread-local storage, valid until the thread's next failing call). */
+const char* inf_last_error_detail(void);
+
 /* Library ABI version (major*10000 + minor*100 + patch). */
 int inf_version(void);
 

@@ -58,6 +58,7 @@ EXPORTS = (
     "inf_adamw_step",
     "inf_col_sum",
     "inf_binary_bcast",
+    "inf_last_error_detail",
 )
 
 
@@ -129,8 +130,10 @@ def lib() -> ctypes.CDLL:
         L.inf_adamw_step.argtypes = [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, i32, vp]
         L.inf_col_sum.argtypes = [vp, i64, i64, i64, vp, i32, i32, vp, sz, vp]
         L.inf_binary_bcast.argtypes = [i32, vp, vp, vp, i64, i64, i32, vp]
-        for name in EXPORTS[11:]:
+        for name in EXPORTS[11:-1]:
             getattr(L, name).restype = i32
+        L.inf_last_error_detail.argtypes = []
+        L.inf_last_error_detail.restype = ctypes.c_char_p
         _lib = L
     return _lib
 

@@ -1,0 +1,341 @@
+// gpt.cpp -- the GPT training step around the attention path, on the C++
+// drop-in (libinferno.so).  Mirrors the application classes of
+// InfernoApp/main.cpp: PositionalEncoding (:20-64), TransformerBlock
+// (:817-926, LayerNorm -> attention -> residual -> LayerNorm -> Linear ->
+// GELU -> Linear -> residual) and GPTModel (:940-1033), with the attention
+// block replaced by the fused MultiHeadAttention module.  The output
+// projection is tied to the token embedding (logits = x @ E^T) unless --untied
+// is given, in which case it is the reference's separate Linear "linear1".
+//
+//   gpt bench [--layers L] [--dmodel C] [--heads H] [--ctx T] [--vocab V]
+//             [--batch B] [--steps K] [--warmup W] [--untied]
+//       random-init weights N(0, 0.02) (biases 0, LayerNorm gamma 1 / beta 0),
+//       tokens uniform in [0, V), targets = tokens shifted by one, AdamW
+//       lr 3e-4; times K training steps (forward, cross-entropy, backward,
+//       AdamW, zero_grad) on hip:0 and prints one JSON line with tokens/s and
+//       the attention share of the step time.
+//   gpt step <dir> <cpu|hip> [--untied]
+//       reads config.txt ("L C H T V B"), tokens.bin / targets.bin (int32 [B, T])
+//       and one <state-dict name>.bin (fp32) per parameter from <dir>; runs one
+//       training step; writes loss.bin, grad_<name>.bin (before the update) and
+//       param_<name>.bin (after it).
+#include <hip/hip_runtime_api.h>
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <iostream>
+#include <memory>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "inferno/inferno.h"
+
+using namespace Inferno;
+
+// ------------------------------------------------------------------- model
+class PositionalEncoding : public Module {
+public:
+    PositionalEncoding(size_t context_size, size_t embed_dim, Device device) {
+        std::vector<float> pe_data(context_size * embed_dim);
+        for (size_t pos = 0; pos < context_size; ++pos)
+            for (size_t i = 0; i < embed_dim; ++i) {
+                const float exponent = 2.0f * float(i / 2) / float(embed_dim);
+                const float angle = float(pos) / std::pow(10000.0f, exponent);
+                pe_data[pos * embed_dim + i] = (i % 2 == 0) ? std::sin(angle) : std::cos(angle);
+            }
+        pe = Tensor(DType::Float32, pe_data, std::vector<size_t>{context_size, embed_dim}, "positional-encoding",
+                    device);
+        register_buffer("pe", &pe);
+    }
+    Tensor forward(Tensor& x) override {
+        // x [B, T, C] + pe[:T]
+        const size_t T = x.shape()[1];
+        Tensor p = T == pe.shape()[0] ? pe : pe.slice(0, 0, T - 1);
+        return x + p;
+    }
+    Tensor pe;
+};
+
+class TransformerBlock : public Module {
+public:
+    TransformerBlock(size_t embed_dim, size_t nheads, Device device, DType dtype)
+        : attn(embed_dim, nheads, device, dtype),
+          layernorm1(embed_dim, 1e-5f, device, dtype),
+          layernorm2(embed_dim, 1e-5f, device, dtype),
+          feedforward1(embed_dim, 4 * embed_dim, device, dtype),
+          feedforward2(4 * embed_dim, embed_dim, device, dtype) {
+        register_module("attn", &attn);
+        register_module("ln1", &layernorm1);
+        register_module("ln2", &layernorm2);
+        register_module("ff1", &feedforward1);
+        register_module("ff2", &feedforward2);
+    }
+    Tensor forward(Tensor& x) override {
+        Tensor normed = layernorm1.forward(x);
+        Tensor attn_out = attn.forward(normed);
+        Tensor h = x + attn_out;
+        Tensor normed2 = layernorm2.forward(h);
+        Tensor n = feedforward1.forward(static_cast<const Tensor&>(normed2));
+        n = gelu(n);
+        Tensor ff = feedforward2.forward(static_cast<const Tensor&>(n));
+        return h + ff;
+    }
+    MultiHeadAttention attn;
+    LayerNorm layernorm1, layernorm2;
+    Linear feedforward1, feedforward2;
+};
+
+class GPTModel : public Module {
+public:
+    GPTModel(size_t vocab_size, size_t context_size, size_t embed_dim, size_t nheads, size_t nblocks, bool tied,
+             Device device, DType dtype)
+        : emb1(vocab_size, embed_dim, device, dtype),
+          pos_enc(context_size, embed_dim, device),
+          layernorm1(embed_dim, 1e-5f, device, dtype),
+          m_tied(tied) {
+        register_module("tok_embedding", &emb1);
+        register_module("pos_encoding", &pos_enc);
+        blocks.reserve(nblocks);
+        for (size_t i = 0; i < nblocks; ++i) {
+            blocks.push_back(std::make_unique<TransformerBlock>(embed_dim, nheads, device, dtype));
+            register_module("block" + std::to_string(i), blocks.back().get());
+        }
+        if (!tied) {
+            linear1 = std::make_unique<Linear>(embed_dim, vocab_size, device, dtype);
+            register_module("linear1", linear1.get());
+        }
+        register_module("ln1", &layernorm1);
+    }
+    Tensor forward(Tensor& input) override {
+        Tensor x = emb1.forward(input);
+        x = pos_enc.forward(x);
+        for (auto& b : blocks) x = b->forward(x);
+        x = layernorm1.forward(x);
+        if (m_tied) return matmul(x, emb1.weight().transpose(0, 1), "logits");
+        return linear1->forward(static_cast<const Tensor&>(x));
+    }
+    Embedding emb1;
+    PositionalEncoding pos_enc;
+    std::vector<std::unique_ptr<TransformerBlock>> blocks;
+    std::unique_ptr<Linear> linear1;
+    LayerNorm layernorm1;
+    bool m_tied;
+};
+
+// ------------------------------------------------------------------ helpers
+static std::vector<char> read_file(const std::string& path) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) throw Error("cannot read " + path);
+    return std::vector<char>((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+}
+
+static void write_f32(const std::string& path, const std::vector<float>& v) {
+    std::ofstream f(path, std::ios::binary);
+    f.write(reinterpret_cast<const char*>(v.data()), (std::streamsize)(v.size() * 4));
+}
+
+static void set_param(Tensor& p, const std::vector<float>& v) {
+    if (v.size() != p.numel()) throw Error("parameter size mismatch for " + p.name());
+    Tensor h(DType::Float32, v, p.shape(), p.name(), Device::cpu());
+    Tensor d = h.to(p.device());
+    d.set_requires_grad(p.requires_grad());
+    p = d;
+}
+
+static void sync(const Device& d) {
+    if (!d.is_cpu()) (void)hipDeviceSynchronize();
+}
+
+// --------------------------------------------------------------------- step
+static int run_step(const std::string& dir, const Device& dev, bool tied) {
+    std::ifstream cf(dir + "/config.txt");
+    size_t L, C, H, T, V, B;
+    if (!(cf >> L >> C >> H >> T >> V >> B)) throw Error("bad config.txt");
+    GPTModel model(V, T, C, H, L, tied, dev, DType::Float32);
+    // load parameters by state-dict name (pointers from parameters() are stable)
+    {
+        StateDict sd = model.state_dict();
+        std::vector<Tensor*> params = model.parameters();
+        for (auto& [name, t] : sd) {
+            Tensor* target = nullptr;
+            for (Tensor* p : params)
+                if (GetImpl(*p) == GetImpl(t)) target = p;
+            if (!target) continue;  // buffers (pos_encoding.pe) stay as built
+            auto raw = read_file(dir + "/" + name + ".bin");
+            std::vector<float> v(raw.size() / 4);
+            std::memcpy(v.data(), raw.data(), v.size() * 4);
+            set_param(*target, v);
+        }
+    }
+    auto tok = read_file(dir + "/tokens.bin"), tgt = read_file(dir + "/targets.bin");
+    std::vector<int32_t> tv(B * T), gv(B * T);
+    std::memcpy(tv.data(), tok.data(), tv.size() * 4);
+    std::memcpy(gv.data(), tgt.data(), gv.size() * 4);
+    Tensor x(DType::Int32, tv, std::vector<size_t>{B, T}, "tokens", dev);
+    Tensor y(DType::Int32, gv, std::vector<size_t>{B, T}, "targets", dev);
+
+    CrossEntropyLoss loss_fn;
+    OptimizerAdamW opt(model.parameters());
+    Tensor logits = model.forward(x);
+    Tensor loss = loss_fn(logits, y);
+    loss.backward();
+    write_f32(dir + "/loss.bin", loss.to_host_float());
+    StateDict sd = model.state_dict();
+    for (auto& [name, t] : sd) {
+        if (!t.grad()) continue;
+        write_f32(dir + "/grad_" + name + ".bin", t.grad()->to_host_float());
+    }
+    opt.step();
+    opt.zero_grad();
+    sd = model.state_dict();
+    for (auto& [name, t] : sd) write_f32(dir + "/param_" + name + ".bin", t.to_host_float());
+    sync(dev);
+    std::cout << "step ok: loss " << loss.to_host_float()[0] << "\n";
+    return 0;
+}
+
+// -------------------------------------------------------------------- bench
+static size_t arg(int argc, char** argv, const char* name, size_t def) {
+    for (int i = 2; i + 1 < argc; ++i)
+        if (std::strcmp(argv[i], name) == 0) return (size_t)std::strtoull(argv[i + 1], nullptr, 10);
+    return def;
+}
+static bool flag(int argc, char** argv, const char* name) {
+    for (int i = 2; i < argc; ++i)
+        if (std::strcmp(argv[i], name) == 0) return true;
+    return false;
+}
+
+static void init_normal(Module& m, float stddev, const Device& dev) {
+    // Linear weights and the embedding ~ N(0, stddev); biases 0; LayerNorm as built.
+    StateDict sd = m.state_dict();
+    std::vector<Tensor*> params = m.parameters();
+    for (auto& [name, t] : sd) {
+        Tensor* p = nullptr;
+        for (Tensor* q : params)
+            if (GetImpl(*q) == GetImpl(t)) p = q;
+        if (!p) continue;
+        const auto ends = [&](const char* s) {
+            const size_t n = std::strlen(s);
+            return name.size() >= n && name.compare(name.size() - n, n, s) == 0;
+        };
+        std::vector<float> v;
+        if (ends(".weights") || ends("tok_embedding.weight"))
+            v = RandomGenerator::generateNormalFloatVector(p->numel(), 0.0f, stddev);
+        else if (ends(".bias"))
+            v.assign(p->numel(), 0.0f);
+        else
+            continue;
+        Tensor h(DType::Float32, v, p->shape(), p->name(), Device::cpu());
+        Tensor d = h.to(dev);
+        if (p->dtype() != DType::Float32) throw Error("bench init: Float32 parameters only");
+        d.set_requires_grad(true);
+        *p = d;
+    }
+}
+
+static int run_bench(int argc, char** argv) {
+    const size_t L = arg(argc, argv, "--layers", 12), C = arg(argc, argv, "--dmodel", 768),
+                 H = arg(argc, argv, "--heads", 12), T = arg(argc, argv, "--ctx", 1024),
+                 V = arg(argc, argv, "--vocab", 8192), B = arg(argc, argv, "--batch", 8),
+                 K = arg(argc, argv, "--steps", 5), W = arg(argc, argv, "--warmup", 2);
+    const bool tied = !flag(argc, argv, "--untied");
+    const Device dev = Device::hip(0);
+    RandomGenerator::initializeWithSeed(42);
+    GPTModel model(V, T, C, H, L, tied, dev, DType::Float32);
+    init_normal(model, 0.02f, dev);
+    size_t nparams = 0;
+    for (Tensor* p : model.parameters()) nparams += p->numel();
+
+    std::mt19937_64 rng(42);
+    std::uniform_int_distribution<int> tokd(0, (int)V - 1);
+    std::vector<int32_t> seq(B * (T + 1));
+    for (auto& t : seq) t = tokd(rng);
+    std::vector<int32_t> xs(B * T), ys(B * T);
+    for (size_t b = 0; b < B; ++b)
+        for (size_t t = 0; t < T; ++t) {
+            xs[b * T + t] = seq[b * (T + 1) + t];
+            ys[b * T + t] = seq[b * (T + 1) + t + 1];
+        }
+    Tensor x(DType::Int32, xs, std::vector<size_t>{B, T}, "tokens", dev);
+    Tensor y(DType::Int32, ys, std::vector<size_t>{B, T}, "targets", dev);
+    CrossEntropyLoss loss_fn;
+    OptimizerAdamW opt(model.parameters(), 3e-4f);
+    float first_loss = 0.f, last_loss = 0.f;
+    auto step = [&]() {
+        Tensor logits = model.forward(x);
+        Tensor loss = loss_fn(logits, y);
+        loss.backward();
+        opt.step();
+        opt.zero_grad();
+        return loss;
+    };
+    for (size_t i = 0; i < W; ++i) {
+        Tensor l = step();
+        if (i == 0) first_loss = l.to_host_float()[0];
+    }
+    sync(dev);
+    const auto t0 = std::chrono::steady_clock::now();
+    Tensor l;
+    for (size_t i = 0; i < K; ++i) l = step();
+    sync(dev);
+    const auto t1 = std::chrono::steady_clock::now();
+    last_loss = l.to_host_float()[0];
+    const double step_ms = std::chrono::duration<double, std::milli>(t1 - t0).count() / (double)K;
+
+    // Attention share: the fused attention forward + backward of one layer at
+    // this shape, timed alone (wall clock between device synchronisations), times L.
+    double attn_ms = 0.0;
+    {
+        std::vector<float> qv(B * T * 3 * C);
+        std::mt19937 g2(7);
+        std::normal_distribution<float> nd(0.f, 1.f);
+        for (auto& v : qv) v = nd(g2);
+        Tensor qkv = Tensor(DType::Float32, qv, std::vector<size_t>{B, T, 3 * C}, "qkv", dev, true);
+        std::vector<float> gv(B * T * C);
+        for (auto& v : gv) v = nd(g2);
+        Tensor gy(DType::Float32, gv, std::vector<size_t>{B, T, C}, "gy", dev);
+        auto once = [&]() {
+            Tensor yy = qkv_attention(qkv, H, true);
+            yy.backward(gy);
+            qkv.grad() = nullptr;
+        };
+        once();
+        sync(dev);
+        const int reps = 10;
+        const auto a0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < reps; ++i) once();
+        sync(dev);
+        const auto a1 = std::chrono::steady_clock::now();
+        attn_ms = std::chrono::duration<double, std::milli>(a1 - a0).count() / reps * (double)L;
+    }
+    const double tokens = (double)(B * T);
+    std::printf(
+        "{\"workload\": \"GPT training step L%zu C%zu H%zu T%zu V%zu B%zu %s\", \"tokens_per_step\": %.0f, "
+        "\"ms_per_step\": %.4f, \"tokens_per_s\": %.1f, \"attention_ms_per_step\": %.4f, "
+        "\"attention_share\": %.4f, \"params\": %zu, \"loss_first\": %.6f, \"loss_last\": %.6f, "
+        "\"steps\": %zu, \"warmup\": %zu}\n",
+        L, C, H, T, V, B, tied ? "tied" : "untied", tokens, step_ms, tokens / (step_ms * 1e-3), attn_ms,
+        attn_ms / step_ms, nparams, first_loss, last_loss, K, W);
+    return 0;
+}
+
+int main(int argc, char** argv) {
+    try {
+        if (argc >= 2 && std::strcmp(argv[1], "bench") == 0) return run_bench(argc, argv);
+        if (argc >= 4 && std::strcmp(argv[1], "step") == 0) {
+            const Device dev = std::strcmp(argv[3], "hip") == 0 ? Device::hip(0) : Device::cpu();
+            return run_step(argv[2], dev, !flag(argc, argv, "--untied"));
+        }
+        std::cerr << "usage: gpt bench [options] | gpt step <dir> <cpu|hip> [--untied]\n";
+        return 2;
+    } catch (const std::exception& e) {
+        std::cerr << "error: " << e.what() << "\n";
+        return 1;
+    }
+}

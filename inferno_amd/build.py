@@ -47,7 +47,8 @@ def _compile(src: Path, obj: Path) -> None:
 # The C++ Tensor / autograd layer (host code only; g++ with the HIP runtime API headers).
 HOST_LIB = PKG / "libinferno.so"
 CPP = PKG / "cpp"
-CPP_SOURCES = ["dtype.cpp", "storage.cpp", "hipctx.cpp", "tensor.cpp", "engine.cpp", "softmax.cpp", "attention.cpp"]
+CPP_SOURCES = ["dtype.cpp", "storage.cpp", "hipctx.cpp", "tensor.cpp", "engine.cpp", "softmax.cpp", "attention.cpp",
+               "nn_ops.cpp", "modules.cpp"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 CXX = os.environ.get("CXX", "g++")
 # -ffp-contract=off: the CPU-device branches keep the reference's separate
@@ -55,6 +56,8 @@ CXX = os.environ.get("CXX", "g++")
 HOST_FLAGS = ["-std=c++20", "-O2", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function",
               "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}", f"-I{ROCM / 'include'}"]
 DRIVER_SRC = ROOT / "tests" / "cpp" / "api_driver.cpp"
+APP_SRC = PKG / "app" / "gpt.cpp"
+APP = PKG / "gpt"
 DRIVER = ROOT / "tests" / "cpp" / "api_driver"
 
 
@@ -84,6 +87,8 @@ def build_host(verbose: bool = True) -> Path:
         _run([CXX, *HOST_FLAGS, str(DRIVER_SRC), "-o", str(DRIVER), f"-L{PKG}", "-linferno", "-linferno_hip",
               f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{PKG}", f"-Wl,-rpath,{ROCM / 'lib'}",
               "-Wl,-rpath,$ORIGIN/../../inferno_amd"], "build api_driver")
+    _run([CXX, *HOST_FLAGS, str(APP_SRC), "-o", str(APP), f"-L{PKG}", "-linferno", "-linferno_hip",
+          f"-L{ROCM / 'lib'}", "-lamdhip64", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM / 'lib'}"], "build gpt app")
     if verbose:
         print(f"built {HOST_LIB}", file=sys.stderr)
     return HOST_LIB

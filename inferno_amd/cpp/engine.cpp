@@ -1,11 +1,13 @@
 // engine.cpp -- autograd engine and the generic nodes (include/inferno/gradengine/engine.h,
 // include/inferno/gradfn/node.h).  Behaviour follows src/inferno/gradengine/engine.cpp:32-199:
 // topological order from the root's grad edge, seed, reverse execution, release.
+#include <algorithm>
 #include <functional>
 #include <map>
 #include <unordered_set>
 
 #include "detail.h"
+#include "inferno/core/ops.h"
 #include "inferno/gradengine/engine.h"
 #include "inferno/gradfn/node.h"
 
@@ -105,18 +107,20 @@ static Tensor sum_all(const Tensor& g, const Tensor& like) {
     return Tensor::full({1}, s, like.dtype(), like.device(), "sum");
 }
 
+// The gradient of an operand that broadcasting expanded: summed back to the
+// operand's shape (a single element, or the trailing block of a broadcast).
+static Tensor reduce_to(const Tensor& g, const Tensor& like) {
+    if (g.shape() == like.shape()) return g;
+    if (like.numel() == 1 && g.numel() != 1) return sum_all(g, like);
+    return sum_to_shape(g, like.shape());
+}
+
 MultiplyBackward::MultiplyBackward(const Tensor& a, const Tensor& b) : m_a(a), m_b(b) { set_name("MultiplyBackward"); }
 void MultiplyBackward::backward() {
     NoGradGuard ng;
     Tensor g = Engine::grad_in(this, 0);
-    if (wants_grad(m_a)) {
-        Tensor ga = multiply(g, m_b);
-        send(m_a, m_a.numel() == 1 && ga.numel() != 1 ? sum_all(ga, m_a) : ga);
-    }
-    if (wants_grad(m_b)) {
-        Tensor gb = multiply(g, m_a);
-        send(m_b, m_b.numel() == 1 && gb.numel() != 1 ? sum_all(gb, m_b) : gb);
-    }
+    if (wants_grad(m_a)) send(m_a, reduce_to(multiply(g, m_b), m_a));
+    if (wants_grad(m_b)) send(m_b, reduce_to(multiply(g, m_a), m_b));
 }
 void MultiplyBackward::release() { m_a = Tensor(); m_b = Tensor(); }
 void MultiplyBackward::get_inputs(std::vector<Tensor>& out) const { out.push_back(m_a); out.push_back(m_b); }
@@ -125,8 +129,8 @@ AddBackward::AddBackward(const Tensor& a, const Tensor& b) : m_a(a), m_b(b) { se
 void AddBackward::backward() {
     NoGradGuard ng;
     Tensor g = Engine::grad_in(this, 0);
-    if (wants_grad(m_a)) send(m_a, m_a.numel() == 1 && g.numel() != 1 ? sum_all(g, m_a) : g);
-    if (wants_grad(m_b)) send(m_b, m_b.numel() == 1 && g.numel() != 1 ? sum_all(g, m_b) : g);
+    if (wants_grad(m_a)) send(m_a, reduce_to(g, m_a));
+    if (wants_grad(m_b)) send(m_b, reduce_to(g, m_b));
 }
 void AddBackward::release() { m_a = Tensor(); m_b = Tensor(); }
 void AddBackward::get_inputs(std::vector<Tensor>& out) const { out.push_back(m_a); out.push_back(m_b); }
@@ -191,18 +195,54 @@ static Tensor binary(int op, const Tensor& A, const Tensor& B, const char* what)
     detail::same_device(A, B, what);
     if (A.dtype() != B.dtype()) throw Error(std::string(what) + ": dtype mismatch");
     const bool a_s = A.numel() == 1, b_s = B.numel() == 1;
-    if (!a_s && !b_s && A.shape() != B.shape())
-        throw Error(std::string(what) + ": shapes must match (or one side be a single element)");
+    // Trailing broadcast: one operand's shape (leading ones dropped) is a suffix
+    // of the other's, e.g. [B, T, C] + [T, C] or [M, N] + [N].
+    int bcast = 0;  // 1: B repeats over A's leading dims, 2: A repeats over B's
+    if (!a_s && !b_s && A.shape() != B.shape()) {
+        const auto suffix = [](const std::vector<size_t>& big, const std::vector<size_t>& small) {
+            size_t i = 0;
+            while (i < small.size() && small[i] == 1) ++i;
+            const size_t k = small.size() - i;
+            return k <= big.size() && std::equal(small.begin() + (long)i, small.end(), big.end() - (long)k);
+        };
+        if (A.ndim() >= B.ndim() && suffix(A.shape(), B.shape()))
+            bcast = 1;
+        else if (B.ndim() >= A.ndim() && suffix(B.shape(), A.shape()))
+            bcast = 2;
+        else
+            throw Error(std::string(what) + ": shapes must match, broadcast over leading dimensions, "
+                                            "or one side be a single element");
+    }
     Tensor a = A, b = B;
     {
         NoGradGuard ng;
         if (!a.is_contiguous()) a = a.contiguous();
         if (!b.is_contiguous()) b = b.contiguous();
     }
-    const Tensor& big = (a_s && !b_s) ? b : a;
+    const Tensor& big = (bcast == 2 || (a_s && !b_s)) ? b : a;
     Tensor out(A.dtype(), big.shape(), what, A.device(), false);
     const size_t n = out.numel();
-    if (A.device().is_cpu()) {
+    if (bcast) {
+        const Tensor& full = bcast == 1 ? a : b;
+        const Tensor& rep = bcast == 1 ? b : a;
+        const size_t nb = rep.numel();
+        if (A.device().is_cpu()) {
+            const char* pf = static_cast<const char*>(full.data_ptr());
+            const char* pr = static_cast<const char*>(rep.data_ptr());
+            char* po = static_cast<char*>(out.data_ptr());
+            const size_t esz = dtype_size(A.dtype());
+            for (size_t i = 0; i < n; ++i) {
+                const double x = detail::load_elem(pf + i * esz, A.dtype());
+                const double y = detail::load_elem(pr + (i % nb) * esz, A.dtype());
+                detail::store_elem(po + i * esz, A.dtype(), op == INF_BIN_ADD ? (float)x + (float)y : (float)x * (float)y);
+            }
+        } else if (n) {
+            detail::DeviceGuard g(A.device().index);
+            detail::status_check(inf_binary_bcast(op, full.data_ptr(), rep.data_ptr(), out.data_ptr(), (int64_t)n,
+                                                  (int64_t)nb, detail::inf_dt(A.dtype(), what), detail::stream_of(A)),
+                                 "inf_binary_bcast");
+        }
+    } else if (A.device().is_cpu()) {
         const char* pa = static_cast<const char*>(a.data_ptr());
         const char* pb = static_cast<const char*>(b.data_ptr());
         char* po = static_cast<char*>(out.data_ptr());

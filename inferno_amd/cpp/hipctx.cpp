@@ -19,7 +19,9 @@ void hip_check(hipError_t e, const char* what) {
 }
 
 void status_check(int status, const char* what) {
-    if (status != INF_OK) throw Error(std::string(what) + ": " + inf_status_string(status));
+    if (status == INF_OK) return;
+    const std::string detail = inf_last_error_detail();
+    throw Error(std::string(what) + ": " + inf_status_string(status) + (detail.empty() ? "" : " [" + detail + "]"));
 }
 
 DeviceGuard::DeviceGuard(int device) {

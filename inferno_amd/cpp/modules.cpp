@@ -1,0 +1,249 @@
+// modules.cpp -- Module, Linear, LayerNorm, Embedding, MultiHeadAttention,
+// CrossEntropyLoss, OptimizerAdamW and RandomGenerator
+// (include/inferno/modules/*.h, loss/crossentropyloss.h, optim/adamw.h,
+// util/random.h).  Same constructors, parameter names, defaults and
+// registration as the reference's (module.cpp, linear.cpp, layernorm.cpp,
+// embedding.cpp, crossentropyloss.cpp, adamw.cpp, random.cpp,
+// InfernoApp/main.cpp:675-811); the compute goes through the ops of
+// inferno/core/ops.h.
+#include <cmath>
+#include <random>
+
+#include "detail.h"
+#include "inferno/gradengine/engine.h"
+#include "inferno/loss/crossentropyloss.h"
+#include "inferno/modules/embedding.h"
+#include "inferno/modules/layernorm.h"
+#include "inferno/modules/linear.h"
+#include "inferno/modules/module.h"
+#include "inferno/modules/multiheadattention.h"
+#include "inferno/optim/adamw.h"
+#include "inferno/util/random.h"
+
+namespace Inferno {
+
+// ------------------------------------------------------------- RandomGenerator
+namespace {
+std::mt19937& engine_ref() {
+    static std::mt19937 gen(5489u);
+    return gen;
+}
+}  // namespace
+
+void RandomGenerator::initialize() { engine_ref().seed(std::random_device{}()); }
+void RandomGenerator::initializeWithSeed(unsigned int seed) { engine_ref().seed(seed); }
+
+std::vector<float> RandomGenerator::generateRandomFloatVector(size_t size, float minValue, float maxValue) {
+    std::uniform_real_distribution<float> d(minValue, maxValue);
+    std::vector<float> v(size);
+    for (auto& x : v) x = d(engine_ref());
+    return v;
+}
+std::vector<double> RandomGenerator::generateRandomDoubleVector(size_t size, double minValue, double maxValue) {
+    std::uniform_real_distribution<double> d(minValue, maxValue);
+    std::vector<double> v(size);
+    for (auto& x : v) x = d(engine_ref());
+    return v;
+}
+std::vector<int> RandomGenerator::generateRandomIntVector(size_t size, int minValue, int maxValue) {
+    std::uniform_int_distribution<int> d(minValue, maxValue);
+    std::vector<int> v(size);
+    for (auto& x : v) x = d(engine_ref());
+    return v;
+}
+float RandomGenerator::generateRandomFloat(float minValue, float maxValue) {
+    return std::uniform_real_distribution<float>(minValue, maxValue)(engine_ref());
+}
+double RandomGenerator::generateRandomDouble(double minValue, double maxValue) {
+    return std::uniform_real_distribution<double>(minValue, maxValue)(engine_ref());
+}
+int RandomGenerator::generateRandomInt(int minValue, int maxValue) {
+    return std::uniform_int_distribution<int>(minValue, maxValue)(engine_ref());
+}
+std::vector<float> RandomGenerator::generateNormalFloatVector(size_t size, float mean, float stddev) {
+    std::normal_distribution<float> d(mean, stddev);
+    std::vector<float> v(size);
+    for (auto& x : v) x = d(engine_ref());
+    return v;
+}
+
+// ---------------------------------------------------------------------- Module
+Tensor Module::forward(Tensor&) { throw Error("forward(input) not implemented!"); }
+
+std::vector<Tensor*> Module::parameters() const {
+    std::vector<Tensor*> all;
+    for (const auto& [name, t] : _parameters) all.push_back(t);
+    for (const auto& [name, child] : _children) {
+        auto c = child->parameters();
+        all.insert(all.end(), c.begin(), c.end());
+    }
+    return all;
+}
+
+static void check_free(const std::string& name, bool p, bool b, bool c) {
+    if (p) throw std::runtime_error("Parameter already registered: " + name);
+    if (b) throw std::runtime_error("Name already used by buffer: " + name);
+    if (c) throw std::runtime_error("Name already used by submodule: " + name);
+}
+
+void Module::register_parameter(const std::string& name, Tensor* tensor) {
+    check_free(name, _parameters.count(name), _buffers.count(name), _children.count(name));
+    _parameters[name] = tensor;
+}
+void Module::register_module(const std::string& name, Module* module) {
+    check_free(name, _parameters.count(name), _buffers.count(name), _children.count(name));
+    _children[name] = module;
+}
+void Module::register_buffer(const std::string& name, Tensor* tensor) {
+    check_free(name, _parameters.count(name), _buffers.count(name), _children.count(name));
+    _buffers[name] = tensor;
+}
+
+void Module::to(const Device& device) {
+    for (auto& [name, p] : _parameters)
+        if (p) *p = p->to(device);
+    for (auto& [name, b] : _buffers)
+        if (b) *b = b->to(device);
+    for (auto& [name, c] : _children)
+        if (c) c->to(device);
+}
+
+StateDict Module::state_dict() const {
+    StateDict out;
+    collect_state_dict(out, "");
+    return out;
+}
+
+void Module::collect_state_dict(StateDict& out, const std::string& prefix) const {
+    const auto full = [&](const std::string& n) { return prefix.empty() ? n : prefix + "." + n; };
+    for (const auto& [name, t] : _parameters) out[full(name)] = *t;
+    for (const auto& [name, t] : _buffers) out[full(name)] = *t;
+    for (const auto& [name, c] : _children) c->collect_state_dict(out, full(name));
+}
+
+// ---------------------------------------------------------------------- Linear
+Linear::Linear(size_t in_features, size_t out_features, Device device, DType dtype)
+    : m_in_features(in_features), m_out_features(out_features) {
+    if (dtype != DType::Float32 && dtype != DType::BFloat16) throw Error("Unsupported dtype in Linear");
+    const float limit = std::sqrt(6.0f / static_cast<float>(in_features + out_features));
+    auto w = RandomGenerator::generateRandomFloatVector(in_features * out_features, -limit, limit);
+    m_weights = Tensor(dtype, w, std::vector<size_t>{in_features, out_features}, "weights", device, true);
+    auto b = RandomGenerator::generateRandomFloatVector(out_features, -limit, limit);
+    m_biases = Tensor(dtype, b, std::vector<size_t>{out_features}, "biases", device, true);
+    register_parameter("weights", &m_weights);
+    register_parameter("bias", &m_biases);
+}
+
+Tensor Linear::forward(const Tensor& input) { return linear(input, m_weights, m_biases); }
+
+// ------------------------------------------------------------------- LayerNorm
+LayerNorm::LayerNorm(size_t normalized_dim, float eps, Device device, DType dtype)
+    : m_dim(normalized_dim), m_eps(eps) {
+    if (dtype != DType::Float32 && dtype != DType::BFloat16) throw Error("LayerNorm: floating dtype expected");
+    NoGradGuard guard;
+    m_beta = Tensor(DType::Float32, std::vector<float>(normalized_dim, 0.0f), std::vector<size_t>{normalized_dim},
+                    "ln_beta", device, true);
+    m_gamma = Tensor(DType::Float32, std::vector<float>(normalized_dim, 1.0f), std::vector<size_t>{normalized_dim},
+                     "ln_gamma", device, true);
+    register_parameter("beta", &m_beta);
+    register_parameter("gamma", &m_gamma);
+}
+
+Tensor LayerNorm::forward(Tensor& input) {
+    if (input.ndim() == 0 || input.shape().back() != m_dim) throw Error("LayerNorm: last dimension mismatch");
+    return layer_norm(input, m_gamma, m_beta, m_eps);
+}
+
+// ------------------------------------------------------------------- Embedding
+Embedding::Embedding(size_t vocab_size, size_t embed_dim, Device device, DType dtype) {
+    if (dtype != DType::Float32 && dtype != DType::BFloat16) throw Error("Embedding: floating dtype expected");
+    NoGradGuard guard;
+    auto v = RandomGenerator::generateRandomFloatVector(vocab_size * embed_dim, -1.0f, 1.0f);
+    m_embeddings = Tensor(dtype, v, std::vector<size_t>{vocab_size, embed_dim}, "embedding", device, true);
+    register_parameter("weight", &m_embeddings);
+}
+
+Tensor Embedding::forward(Tensor& token_ids) { return embedding(token_ids, m_embeddings); }
+
+// ---------------------------------------------------------- MultiHeadAttention
+MultiHeadAttention::MultiHeadAttention(size_t embed_dim, size_t num_heads, Device device, DType dtype)
+    : m_embed_dim(embed_dim),
+      m_num_heads(num_heads),
+      m_head_dim(num_heads ? embed_dim / num_heads : 0),
+      Wqkv_layer(embed_dim, embed_dim * 3, device, dtype),
+      W_out(embed_dim, embed_dim, device, dtype) {
+    if (num_heads == 0 || embed_dim % num_heads != 0)
+        throw Error("MultiHeadAttention: embed_dim must be divisible by num_heads");
+    register_module("Wqkv", &Wqkv_layer);
+    register_module("W_out", &W_out);
+}
+
+Tensor MultiHeadAttention::forward(Tensor& x) {
+    if (x.ndim() != 3) throw Error("MultiHeadAttention expects [B, T, C]");
+    if (x.shape()[2] != m_embed_dim) throw Error("MultiHeadAttention: embed_dim mismatch");
+    Tensor qkv = Wqkv_layer.forward(static_cast<const Tensor&>(x));  // [B, T, 3C]
+    Tensor y = qkv_attention(qkv, m_num_heads, true);                  // [B, T, C]
+    return W_out.forward(static_cast<const Tensor&>(y));
+}
+
+// ------------------------------------------------------------ CrossEntropyLoss
+Tensor CrossEntropyLoss::forward(Tensor& logits, Tensor& target) { return cross_entropy(logits, target); }
+
+// -------------------------------------------------------------- OptimizerAdamW
+void OptimizerAdamW::step() {
+    NoGradGuard guard;
+    m_step++;
+    const float bc1 = 1.0f - std::pow(m_beta1, static_cast<float>(m_step));
+    const float bc2 = 1.0f - std::pow(m_beta2, static_cast<float>(m_step));
+    for (Tensor* p : m_parameters) {
+        if (p == nullptr || !p->grad()) continue;
+        Tensor* grad = p->grad().get();
+        if (grad->dtype() != p->dtype() || grad->shape() != p->shape())
+            throw Error("OptimizerAdamW: gradient dtype / shape differs from the parameter's");
+        if (!p->is_contiguous()) throw Error("OptimizerAdamW: parameters must be contiguous");
+        Tensor g = grad->contiguous();
+        AdamWState& st = m_state[p];
+        if (!st.initialized) {
+            st.m = Tensor::zeros(p->shape(), DType::Float32, p->device(), "adamw_m");
+            st.v = Tensor::zeros(p->shape(), DType::Float32, p->device(), "adamw_v");
+            st.initialized = true;
+        }
+        const size_t n = p->numel();
+        if (p->device().is_cpu()) {
+            // cpu_adamw_step_impl (adamw.h:67-111)
+            char* pp = static_cast<char*>(p->data_ptr());
+            const char* gp = static_cast<const char*>(g.data_ptr());
+            float* mp = static_cast<float*>(st.m.data_ptr());
+            float* vp = static_cast<float*>(st.v.data_ptr());
+            const size_t esz = dtype_size(p->dtype());
+            for (size_t i = 0; i < n; ++i) {
+                const float gr = (float)detail::load_elem(gp + i * esz, p->dtype());
+                float mi = mp[i], vi = vp[i], pi = (float)detail::load_elem(pp + i * esz, p->dtype());
+                mi = m_beta1 * mi + (1.0f - m_beta1) * gr;
+                vi = m_beta2 * vi + (1.0f - m_beta2) * gr * gr;
+                const float m_hat = mi / bc1;
+                const float v_hat = vi / bc2;
+                float update = m_hat / (std::sqrt(v_hat) + m_eps);
+                if (m_weight_decay != 0.0f) update += m_weight_decay * pi;
+                pi -= m_lr * update;
+                detail::store_elem(pp + i * esz, p->dtype(), pi);
+                mp[i] = mi;
+                vp[i] = vi;
+            }
+        } else {
+            detail::DeviceGuard dg(p->device().index);
+            detail::status_check(inf_adamw_step(p->data_ptr(), g.data_ptr(), static_cast<float*>(st.m.data_ptr()),
+                                                static_cast<float*>(st.v.data_ptr()), (int64_t)n, m_lr, m_beta1,
+                                                m_beta2, m_eps, m_weight_decay, bc1, bc2,
+                                                detail::inf_dt(p->dtype(), "OptimizerAdamW"), detail::stream_of(*p)),
+                                 "inf_adamw_step");
+        }
+    }
+}
+
+void OptimizerAdamW::zero_grad() {
+    for (auto& p : m_parameters)
+        if (p != nullptr) p->grad() = nullptr;
+}
+
+}  // namespace Inferno

@@ -1,0 +1,884 @@
+// nn_ops.cpp -- matmul, linear, layer_norm, gelu, embedding, cross_entropy,
+// qkv_attention and sum_to_shape, with their backward nodes
+// (include/inferno/core/ops.h, include/inferno/gradfn/nnbackward.h).
+//
+// HIP tensors go through the C-ABI (inf_gemm on hipBLASLt, the nn.hip kernels,
+// the fused attention kernels); nothing here falls back to the CPU for a HIP
+// tensor.  CPU tensors run plain loops that follow the reference's CPU kernels
+// (cpu_matmul's k-ordered fp32 sums, cpu_layer_normalization,
+// cpu_cross_entropy_loss, ...).
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <numeric>
+
+#include "detail.h"
+#include "inferno/core/ops.h"
+#include "inferno/functional/attention.h"
+#include "inferno/functional/gelu.h"
+#include "inferno/gradengine/engine.h"
+#include "inferno/gradfn/nnbackward.h"
+
+namespace Inferno {
+
+namespace {
+
+using detail::DeviceGuard;
+using detail::status_check;
+
+size_t prod(const std::vector<size_t>& v, size_t from = 0, size_t to = SIZE_MAX) {
+    size_t p = 1;
+    for (size_t i = from; i < std::min(to, v.size()); ++i) p *= v[i];
+    return p;
+}
+
+// Device scratch of at least `bytes`, 256-byte aligned, from the stream-ordered
+// pool (freed in stream order when it goes out of scope).
+struct Scratch {
+    Tensor buf;
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    Scratch(size_t n, const Device& dev) : bytes(n) {
+        if (n == 0) return;
+        buf = Tensor(DType::Float32, std::vector<size_t>{n / 4 + 65}, "scratch", dev, false);
+        const uintptr_t p = reinterpret_cast<uintptr_t>(buf.data_ptr());
+        ptr = reinterpret_cast<void*>((p + 255) & ~uintptr_t(255));
+    }
+};
+
+// The hipBLASLt workspace of each device, kept for the life of the process.
+void* gemm_workspace(const Device& dev, size_t* bytes) {
+    static std::mutex mu;
+    static auto* per_device = new std::vector<Tensor>();
+    size_t need = 0;
+    status_check(inf_nn_workspace_bytes(INF_OP_GEMM, 0, 0, &need), "inf_nn_workspace_bytes");
+    std::lock_guard<std::mutex> lk(mu);
+    if (per_device->size() <= (size_t)dev.index) per_device->resize((size_t)dev.index + 1);
+    Tensor& t = (*per_device)[(size_t)dev.index];
+    if (!t.defined()) t = Tensor(DType::Float32, {need / 4 + 64}, "gemm_ws", dev, false);
+    const uintptr_t p = reinterpret_cast<uintptr_t>(t.data_ptr());
+    *bytes = need;
+    return reinterpret_cast<void*>((p + 255) & ~uintptr_t(255));
+}
+
+void gemm_hip(const Device& dev, DType dt, bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha,
+              const void* A, int64_t lda, int64_t sa, const void* B, int64_t ldb, int64_t sb, float beta, void* C,
+              int64_t ldc, int64_t sc, int64_t batch, const void* bias) {
+    size_t wsb = 0;
+    void* ws = gemm_workspace(dev, &wsb);
+    DeviceGuard g(dev.index);
+    status_check(inf_gemm(ta, tb, M, N, K, alpha, A, lda, sa, B, ldb, sb, beta, C, ldc, sc, batch, bias,
+                          detail::inf_dt(dt, "gemm"), ws, wsb, detail::stream_for(dev.index)),
+                 "inf_gemm");
+}
+
+// Element (i, j) of a strided matrix on the host, as fp32.
+inline float ld_f(const char* base, DType dt, int64_t off) {
+    return (float)detail::load_elem(base + off * (int64_t)dtype_size(dt), dt);
+}
+inline void st_f(char* base, DType dt, int64_t off, float v) {
+    detail::store_elem(base + off * (int64_t)dtype_size(dt), dt, v);
+}
+
+// The last two dimensions of t as a matrix: (row stride, column stride).
+struct Mat {
+    int64_t rs, cs;
+};
+Mat mat_of(const Tensor& t) {
+    const size_t n = t.ndim();
+    return {(int64_t)t.strides()[n - 2], (int64_t)t.strides()[n - 1]};
+}
+
+// A matrix layout the GEMM accepts: row-major (cs == 1) or its transpose (rs == 1).
+bool gemm_layout(const Mat& m, int64_t rows, int64_t cols, bool* trans, int64_t* ld) {
+    if (m.cs == 1 && (m.rs >= std::max<int64_t>(cols, 1) || rows <= 1)) {
+        *trans = false;
+        *ld = std::max<int64_t>(m.rs, std::max<int64_t>(cols, 1));
+        return true;
+    }
+    if (m.rs == 1 && (m.cs >= std::max<int64_t>(rows, 1) || cols <= 1)) {
+        *trans = true;
+        *ld = std::max<int64_t>(m.cs, std::max<int64_t>(rows, 1));
+        return true;
+    }
+    return false;
+}
+
+// Element offsets of every broadcast batch index of `t` (batch dims = all but
+// the last two), for an output batch shape `ob` (right-aligned broadcasting).
+std::vector<int64_t> batch_offsets(const Tensor& t, const std::vector<size_t>& ob) {
+    const size_t P = prod(ob);
+    std::vector<int64_t> off(P, 0);
+    const size_t tb = t.ndim() - 2;
+    for (size_t p = 0; p < P; ++p) {
+        size_t rem = p;
+        int64_t o = 0;
+        for (int d = (int)ob.size() - 1; d >= 0; --d) {
+            const size_t idx = rem % ob[d];
+            rem /= ob[d];
+            const int td = (int)tb - ((int)ob.size() - d);
+            if (td >= 0 && t.shape()[td] != 1) o += (int64_t)idx * (int64_t)t.strides()[td];
+        }
+        off[p] = o;
+    }
+    return off;
+}
+
+bool uniform(const std::vector<int64_t>& off, int64_t* stride) {
+    *stride = off.size() > 1 ? off[1] - off[0] : 0;
+    for (size_t p = 0; p < off.size(); ++p)
+        if (off[p] != (int64_t)p * *stride) return false;
+    return true;
+}
+
+bool wants_grad(const Tensor& t) { return t.defined() && GetImpl(t)->grad_edge() != nullptr; }
+
+void send(const Tensor& input, const Tensor& g) {
+    if (auto e = GetImpl(input)->grad_edge()) Engine::accumulate(e.get(), 0, g);
+}
+
+void check_float(const Tensor& t, const char* what) {
+    if (t.dtype() != DType::Float32 && t.dtype() != DType::BFloat16)
+        throw Error(std::string(what) + ": Float32 or BFloat16 expected, got " + dtype_name(t.dtype()));
+}
+
+}  // namespace
+
+// ============================================================================
+// matmul
+// ============================================================================
+Tensor matmul(const Tensor& A, const Tensor& B, const std::string& name) {
+    if (!A.defined() || !B.defined()) throw Error("matmul: undefined input");
+    if (A.ndim() < 2 || B.ndim() < 2) throw Error("matmul: operands must have rank >= 2");
+    detail::same_device(A, B, "matmul");
+    if (A.dtype() != B.dtype()) throw Error("matmul: dtype mismatch");
+    check_float(A, "matmul");
+    const size_t M = A.shape()[A.ndim() - 2], K = A.shape()[A.ndim() - 1];
+    const size_t K2 = B.shape()[B.ndim() - 2], N = B.shape()[B.ndim() - 1];
+    if (K != K2) throw Error("matmul: inner dimensions differ");
+    // broadcast batch shape
+    const std::vector<size_t> ab(A.shape().begin(), A.shape().end() - 2), bb(B.shape().begin(), B.shape().end() - 2);
+    std::vector<size_t> ob(std::max(ab.size(), bb.size()), 1);
+    for (size_t i = 0; i < ob.size(); ++i) {
+        const size_t a = i < ob.size() - ab.size() ? 1 : ab[i - (ob.size() - ab.size())];
+        const size_t b = i < ob.size() - bb.size() ? 1 : bb[i - (ob.size() - bb.size())];
+        if (a != b && a != 1 && b != 1) throw Error("matmul: batch dimensions do not broadcast");
+        ob[i] = std::max(a, b);
+    }
+    std::vector<size_t> oshape = ob;
+    oshape.push_back(M);
+    oshape.push_back(N);
+    Tensor out(A.dtype(), oshape, name, A.device(), false);
+    const size_t P = prod(ob);
+    if (out.numel() > 0) {
+        Tensor a = A, b = B;
+        bool ta = false, tb = false;
+        int64_t lda = 0, ldb = 0;
+        {
+            NoGradGuard ng;
+            if (!gemm_layout(mat_of(a), (int64_t)M, (int64_t)K, &ta, &lda)) a = detail::dense_copy(a);
+            if (!gemm_layout(mat_of(b), (int64_t)K, (int64_t)N, &tb, &ldb)) b = detail::dense_copy(b);
+        }
+        gemm_layout(mat_of(a), (int64_t)M, (int64_t)K, &ta, &lda);
+        gemm_layout(mat_of(b), (int64_t)K, (int64_t)N, &tb, &ldb);
+        const auto offa = batch_offsets(a, ob), offb = batch_offsets(b, ob);
+        const size_t esz = dtype_size(A.dtype());
+        const char* pa = static_cast<const char*>(a.data_ptr());
+        const char* pb = static_cast<const char*>(b.data_ptr());
+        char* po = static_cast<char*>(out.data_ptr());
+        if (A.device().is_cpu()) {
+            const Mat ma = mat_of(a), mb = mat_of(b);
+            for (size_t p = 0; p < P; ++p)
+                for (size_t m = 0; m < M; ++m)
+                    for (size_t n = 0; n < N; ++n) {
+                        float s = 0.f;
+                        for (size_t k = 0; k < K; ++k)
+                            s += ld_f(pa, A.dtype(), offa[p] + (int64_t)m * ma.rs + (int64_t)k * ma.cs) *
+                                 ld_f(pb, B.dtype(), offb[p] + (int64_t)k * mb.rs + (int64_t)n * mb.cs);
+                        st_f(po, A.dtype(), (int64_t)((p * M + m) * N + n), s);
+                    }
+        } else if (K == 0) {
+            DeviceGuard g(A.device().index);
+            status_check(inf_fill(out.data_ptr(), (int64_t)out.numel(), (int)esz, 0u, detail::stream_of(A)), "inf_fill");
+        } else {
+            int64_t sa = 0, sb = 0;
+            const bool ua = uniform(offa, &sa), ub = uniform(offb, &sb);
+            // One GEMM over all batch rows when B is shared and A's batches are
+            // consecutive row blocks of one row-major matrix.
+            if (sb == 0 && ub && !ta && ua && (P == 1 || sa == (int64_t)M * lda)) {
+                gemm_hip(A.device(), A.dtype(), false, tb, (int64_t)(P * M), (int64_t)N, (int64_t)K, 1.f, pa, lda, 0,
+                         pb, ldb, 0, 0.f, po, (int64_t)N, 0, 1, nullptr);
+            } else if (ua && ub) {
+                gemm_hip(A.device(), A.dtype(), ta, tb, (int64_t)M, (int64_t)N, (int64_t)K, 1.f, pa, lda, sa, pb, ldb,
+                         sb, 0.f, po, (int64_t)N, (int64_t)(M * N), (int64_t)P, nullptr);
+            } else {
+                for (size_t p = 0; p < P; ++p)
+                    gemm_hip(A.device(), A.dtype(), ta, tb, (int64_t)M, (int64_t)N, (int64_t)K, 1.f,
+                             pa + offa[p] * (int64_t)esz, lda, 0, pb + offb[p] * (int64_t)esz, ldb, 0, 0.f,
+                             po + (int64_t)(p * M * N * esz), (int64_t)N, 0, 1, nullptr);
+            }
+        }
+    }
+    if (grad_enabled && (A.requires_grad() || B.requires_grad())) {
+        out.set_requires_grad(true);
+        GetImpl(out)->gradfn() = std::make_shared<MMBackward>(A, B);
+    }
+    return out;
+}
+
+MMBackward::MMBackward(const Tensor& a, const Tensor& b) : m_a(a), m_b(b) { set_name("MMBackward"); }
+
+void MMBackward::backward() {
+    NoGradGuard ng;
+    Tensor g = Engine::grad_in(this, 0);
+    if (wants_grad(m_a)) send(m_a, sum_to_shape(matmul(g, m_b.transpose(-1, -2)), m_a.shape()));
+    if (wants_grad(m_b)) {
+        if (m_b.ndim() == 2) {
+            // Shared weights: dB = A^T G over all rows of A as one product.
+            const size_t Kd = m_a.shape().back(), Nd = g.shape().back();
+            Tensor a2 = m_a.contiguous().reshape({m_a.numel() / Kd, Kd});
+            Tensor g2 = g.contiguous().reshape({g.numel() / Nd, Nd});
+            if (m_b.strides()[0] == 1 && m_b.shape()[0] > 1) {
+                // B is a transposed view (e.g. a tied embedding table): form
+                // dB^T = G^T A in the table's own layout and pass its transpose.
+                send(m_b, matmul(g2.transpose(0, 1), a2).transpose(0, 1));
+            } else {
+                send(m_b, matmul(a2.transpose(0, 1), g2));
+            }
+        } else {
+            send(m_b, sum_to_shape(matmul(m_a.transpose(-1, -2), g), m_b.shape()));
+        }
+    }
+}
+void MMBackward::release() { m_a = m_b = Tensor(); }
+void MMBackward::get_inputs(std::vector<Tensor>& out) const {
+    out.push_back(m_a);
+    out.push_back(m_b);
+}
+
+// ============================================================================
+// sum_to_shape
+// ============================================================================
+Tensor sum_to_shape(const Tensor& g, const std::vector<size_t>& shape) {
+    if (g.shape() == shape) return g;
+    if (shape.size() > g.ndim()) throw Error("sum_to_shape: target has higher rank");
+    const size_t pad = g.ndim() - shape.size();
+    std::vector<size_t> tshape(pad, 1);
+    tshape.insert(tshape.end(), shape.begin(), shape.end());
+    for (size_t d = 0; d < g.ndim(); ++d)
+        if (tshape[d] != g.shape()[d] && tshape[d] != 1) throw Error("sum_to_shape: shapes do not broadcast");
+    NoGradGuard ng;
+    Tensor gc = g.contiguous();
+    if (!g.device().is_cpu() && g.dtype() != DType::Float32)
+        throw Error("sum_to_shape: HIP reductions take Float32 gradients");
+    Tensor out(g.dtype(), shape, "sum_to_shape", g.device(), false);
+    if (g.device().is_cpu()) {
+        // cpu_sum_to_shape (broadcastops.h:22-48): walk the source in linear
+        // order and add each element to its destination.
+        std::vector<float> acc(out.numel(), 0.f);
+        const auto tst = Tensor::calculate_strides(tshape);
+        const char* src = static_cast<const char*>(gc.data_ptr());
+        const size_t n = gc.numel();
+        std::vector<size_t> idx(g.ndim(), 0);
+        for (size_t lin = 0; lin < n; ++lin) {
+            size_t dst = 0;
+            for (size_t d = 0; d < g.ndim(); ++d) dst += (tshape[d] == 1 ? 0 : idx[d]) * tst[d];
+            acc[dst] += ld_f(src, g.dtype(), (int64_t)lin);
+            for (int d = (int)g.ndim() - 1; d >= 0; --d) {
+                if (++idx[d] < g.shape()[d]) break;
+                idx[d] = 0;
+            }
+        }
+        char* po = static_cast<char*>(out.data_ptr());
+        for (size_t i = 0; i < acc.size(); ++i) st_f(po, out.dtype(), (int64_t)i, acc[i]);
+        return out;
+    }
+    // HIP: the reduced dimensions must be a leading block.
+    size_t k = 0;
+    while (k < g.ndim() && tshape[k] == 1) ++k;
+    for (size_t d = k; d < g.ndim(); ++d)
+        if (tshape[d] != g.shape()[d]) throw Error("sum_to_shape: HIP tensors reduce leading dimensions only");
+    const int64_t rows = (int64_t)prod(g.shape(), 0, k), cols = (int64_t)prod(g.shape(), k);
+    size_t wsb = 0;
+    status_check(inf_nn_workspace_bytes(INF_OP_COL_SUM, rows, cols, &wsb), "inf_nn_workspace_bytes");
+    Scratch ws(wsb, g.device());
+    DeviceGuard dg(g.device().index);
+    status_check(inf_col_sum(gc.data_ptr(), rows, cols, cols, static_cast<float*>(out.data_ptr()), 0, INF_F32, ws.ptr,
+                             wsb, detail::stream_of(g)),
+                 "inf_col_sum");
+    return out;
+}
+
+// ============================================================================
+// linear
+// ============================================================================
+Tensor linear(const Tensor& x, const Tensor& W, const Tensor& b) {
+    if (!x.defined() || !W.defined()) throw Error("linear: undefined input");
+    if (W.ndim() != 2) throw Error("linear: weights must be [in, out]");
+    if (x.ndim() < 1 || x.shape().back() != W.shape()[0]) throw Error("linear: input's last dimension must equal in");
+    detail::same_device(x, W, "linear");
+    if (x.dtype() != W.dtype()) throw Error("linear: dtype mismatch");
+    check_float(x, "linear");
+    const size_t in = W.shape()[0], outf = W.shape()[1];
+    if (b.defined()) {
+        if (b.ndim() != 1 || b.shape()[0] != outf) throw Error("linear: bias must be [out]");
+        detail::same_device(x, b, "linear");
+        if (b.dtype() != x.dtype()) throw Error("linear: bias dtype mismatch");
+    }
+    Tensor xc = x.contiguous(), Wc = W.contiguous(), bc = b.defined() ? b.contiguous() : Tensor();
+    const size_t rows = in ? xc.numel() / in : 0;
+    std::vector<size_t> oshape(x.shape().begin(), x.shape().end() - 1);
+    oshape.push_back(outf);
+    Tensor out(x.dtype(), oshape, "linear", x.device(), false);
+    if (out.numel()) {
+        if (x.device().is_cpu()) {
+            // matmul (cpu_matmul, k-ordered fp32 sums) then + bias, two roundings
+            const char* px = static_cast<const char*>(xc.data_ptr());
+            const char* pw = static_cast<const char*>(Wc.data_ptr());
+            const char* pbias = bc.defined() ? static_cast<const char*>(bc.data_ptr()) : nullptr;
+            char* po = static_cast<char*>(out.data_ptr());
+            const DType dt = x.dtype();
+            for (size_t r = 0; r < rows; ++r)
+                for (size_t n = 0; n < outf; ++n) {
+                    float s = 0.f;
+                    for (size_t k = 0; k < in; ++k)
+                        s += ld_f(px, dt, (int64_t)(r * in + k)) * ld_f(pw, dt, (int64_t)(k * outf + n));
+                    if (pbias) {
+                        st_f(po, dt, (int64_t)(r * outf + n), s);
+                        s = ld_f(po, dt, (int64_t)(r * outf + n)) + ld_f(pbias, dt, (int64_t)n);
+                    }
+                    st_f(po, dt, (int64_t)(r * outf + n), s);
+                }
+        } else if (in == 0) {
+            throw Error("linear: in_features must be > 0");
+        } else {
+            gemm_hip(x.device(), x.dtype(), false, false, (int64_t)rows, (int64_t)outf, (int64_t)in, 1.f,
+                     xc.data_ptr(), (int64_t)in, 0, Wc.data_ptr(), (int64_t)outf, 0, 0.f, out.data_ptr(),
+                     (int64_t)outf, 0, 1, bc.defined() ? bc.data_ptr() : nullptr);
+        }
+    }
+    if (grad_enabled && (x.requires_grad() || W.requires_grad() || (b.defined() && b.requires_grad()))) {
+        out.set_requires_grad(true);
+        GetImpl(out)->gradfn() = std::make_shared<LinearBackward>(xc, Wc, bc);
+    }
+    return out;
+}
+
+LinearBackward::LinearBackward(const Tensor& x, const Tensor& w, const Tensor& b) : m_x(x), m_w(w), m_b(b) {
+    set_name("LinearBackward");
+}
+
+void LinearBackward::backward() {
+    NoGradGuard ng;
+    Tensor g = Engine::grad_in(this, 0).contiguous();
+    const size_t in = m_w.shape()[0], outf = m_w.shape()[1];
+    const size_t rows = m_x.numel() / in;
+    Tensor g2 = g.reshape({rows, outf});
+    if (wants_grad(m_x)) {
+        Tensor dx;
+        if (m_x.device().is_cpu()) {
+            dx = matmul(g2, m_w.transpose(0, 1));
+        } else {
+            dx = Tensor(m_x.dtype(), {rows, in}, "linear_dx", m_x.device(), false);
+            gemm_hip(m_x.device(), m_x.dtype(), false, true, (int64_t)rows, (int64_t)in, (int64_t)outf, 1.f,
+                     g2.data_ptr(), (int64_t)outf, 0, m_w.data_ptr(), (int64_t)outf, 0, 0.f, dx.data_ptr(),
+                     (int64_t)in, 0, 1, nullptr);
+        }
+        send(m_x, dx.reshape(m_x.shape()));
+    }
+    if (wants_grad(m_w)) {
+        Tensor x2 = m_x.reshape({rows, in});
+        Tensor dw;
+        if (m_x.device().is_cpu()) {
+            dw = matmul(x2.transpose(0, 1), g2);
+        } else {
+            dw = Tensor(m_w.dtype(), {in, outf}, "linear_dw", m_w.device(), false);
+            gemm_hip(m_x.device(), m_x.dtype(), true, false, (int64_t)in, (int64_t)outf, (int64_t)rows, 1.f,
+                     x2.data_ptr(), (int64_t)in, 0, g2.data_ptr(), (int64_t)outf, 0, 0.f, dw.data_ptr(),
+                     (int64_t)outf, 0, 1, nullptr);
+        }
+        send(m_w, dw);
+    }
+    if (m_b.defined() && wants_grad(m_b)) send(m_b, sum_to_shape(g2, m_b.shape()));
+}
+void LinearBackward::release() { m_x = m_w = m_b = Tensor(); }
+void LinearBackward::get_inputs(std::vector<Tensor>& out) const {
+    out.push_back(m_x);
+    out.push_back(m_w);
+    if (m_b.defined()) out.push_back(m_b);
+}
+
+// ============================================================================
+// layer_norm
+// ============================================================================
+Tensor layer_norm(const Tensor& x, const Tensor& gamma, const Tensor& beta, float eps) {
+    if (!x.defined() || !gamma.defined() || !beta.defined()) throw Error("layer_norm: undefined input");
+    check_float(x, "layer_norm");
+    if (gamma.dtype() != DType::Float32 || beta.dtype() != DType::Float32)
+        throw Error("layer_norm: gamma and beta are Float32");
+    detail::same_device(x, gamma, "layer_norm");
+    detail::same_device(x, beta, "layer_norm");
+    const size_t dim = x.ndim() ? x.shape().back() : 0;
+    if (!dim || gamma.numel() != dim || beta.numel() != dim) throw Error("layer_norm: parameter size mismatch");
+    Tensor xc = x.contiguous(), gc = gamma.contiguous(), bc = beta.contiguous();
+    const size_t rows = xc.numel() / dim;
+    const bool req = x.requires_grad() || gamma.requires_grad() || beta.requires_grad();
+    Tensor out(x.dtype(), x.shape(), "layernorm", x.device(), false);
+    Tensor mean(DType::Float32, {rows}, "ln_mean", x.device(), false);
+    Tensor invstd(DType::Float32, {rows}, "ln_invstd", x.device(), false);
+    if (rows) {
+        if (x.device().is_cpu()) {
+            // cpu_layer_normalization (layernorm_kernels.h:48-87)
+            const char* px = static_cast<const char*>(xc.data_ptr());
+            char* po = static_cast<char*>(out.data_ptr());
+            const float* g = static_cast<const float*>(gc.data_ptr());
+            const float* bt = static_cast<const float*>(bc.data_ptr());
+            float* pm = static_cast<float*>(mean.data_ptr());
+            float* ps = static_cast<float*>(invstd.data_ptr());
+            for (size_t r = 0; r < rows; ++r) {
+                const int64_t base = (int64_t)(r * dim);
+                float mu = 0.f;
+                for (size_t i = 0; i < dim; ++i) mu += ld_f(px, x.dtype(), base + (int64_t)i);
+                mu /= (float)dim;
+                float var = 0.f;
+                for (size_t i = 0; i < dim; ++i) {
+                    const float d = ld_f(px, x.dtype(), base + (int64_t)i) - mu;
+                    var += d * d;
+                }
+                var /= (float)dim;
+                const float is = 1.0f / std::sqrt(var + eps);
+                pm[r] = mu;
+                ps[r] = is;
+                for (size_t i = 0; i < dim; ++i) {
+                    const float xh = (ld_f(px, x.dtype(), base + (int64_t)i) - mu) * is;
+                    st_f(po, x.dtype(), base + (int64_t)i, xh * g[i] + bt[i]);
+                }
+            }
+        } else {
+            DeviceGuard dg(x.device().index);
+            status_check(inf_layernorm_fwd(xc.data_ptr(), (int64_t)dim, out.data_ptr(), (int64_t)dim,
+                                           static_cast<const float*>(gc.data_ptr()),
+                                           static_cast<const float*>(bc.data_ptr()),
+                                           static_cast<float*>(mean.data_ptr()), static_cast<float*>(invstd.data_ptr()),
+                                           (int64_t)rows, (int64_t)dim, eps, detail::inf_dt(x.dtype(), "layer_norm"),
+                                           detail::stream_of(x)),
+                         "inf_layernorm_fwd");
+        }
+    }
+    if (grad_enabled && req) {
+        out.set_requires_grad(true);
+        GetImpl(out)->gradfn() = std::make_shared<LayerNormBackward>(xc, gc, bc, mean, invstd);
+    }
+    return out;
+}
+
+LayerNormBackward::LayerNormBackward(const Tensor& x, const Tensor& gamma, const Tensor& beta, const Tensor& mean,
+                                     const Tensor& invstd)
+    : m_x(x), m_gamma(gamma), m_beta(beta), m_mean(mean), m_invstd(invstd) {
+    set_name("LayerNormBackward");
+}
+
+void LayerNormBackward::backward() {
+    NoGradGuard ng;
+    Tensor g = Engine::grad_in(this, 0).contiguous();
+    const size_t dim = m_gamma.numel();
+    const size_t rows = m_x.numel() / dim;
+    Tensor gx(m_x.dtype(), m_x.shape(), "layernorm_grad_a", m_x.device(), false);
+    Tensor gg(DType::Float32, m_gamma.shape(), "layernorm_grad_gamma", m_x.device(), false);
+    Tensor gb(DType::Float32, m_beta.shape(), "layernorm_grad_beta", m_x.device(), false);
+    if (m_x.device().is_cpu()) {
+        // cpu_layernorm_backward (layernormbackward.h:47-97)
+        const char* px = static_cast<const char*>(m_x.data_ptr());
+        const char* pg = static_cast<const char*>(g.data_ptr());
+        char* pgx = static_cast<char*>(gx.data_ptr());
+        const float* gam = static_cast<const float*>(m_gamma.data_ptr());
+        const float* mu = static_cast<const float*>(m_mean.data_ptr());
+        const float* is = static_cast<const float*>(m_invstd.data_ptr());
+        float* dg = static_cast<float*>(gg.data_ptr());
+        float* db = static_cast<float*>(gb.data_ptr());
+        const DType dt = m_x.dtype();
+        for (size_t i = 0; i < dim; ++i) dg[i] = db[i] = 0.f;
+        for (size_t r = 0; r < rows; ++r) {
+            const int64_t base = (int64_t)(r * dim);
+            float s1 = 0.f, s2 = 0.f;
+            for (size_t i = 0; i < dim; ++i) {
+                const float xh = (ld_f(px, dt, base + (int64_t)i) - mu[r]) * is[r];
+                const float go = ld_f(pg, dt, base + (int64_t)i);
+                const float dxh = go * gam[i];
+                db[i] += go;
+                dg[i] += go * xh;
+                s1 += dxh;
+                s2 += dxh * xh;
+            }
+            const float fd = (float)dim;
+            for (size_t i = 0; i < dim; ++i) {
+                const float xh = (ld_f(px, dt, base + (int64_t)i) - mu[r]) * is[r];
+                const float dxh = ld_f(pg, dt, base + (int64_t)i) * gam[i];
+                st_f(pgx, dt, base + (int64_t)i, (is[r] / fd) * (fd * dxh - s1 - xh * s2));
+            }
+        }
+    } else {
+        size_t wsb = 0;
+        status_check(inf_nn_workspace_bytes(INF_OP_LAYERNORM_BWD, (int64_t)rows, (int64_t)dim, &wsb),
+                     "inf_nn_workspace_bytes");
+        Scratch ws(wsb, m_x.device());
+        DeviceGuard dg(m_x.device().index);
+        status_check(inf_layernorm_bwd(m_x.data_ptr(), (int64_t)dim, g.data_ptr(), (int64_t)dim,
+                                       static_cast<const float*>(m_gamma.data_ptr()),
+                                       static_cast<const float*>(m_mean.data_ptr()),
+                                       static_cast<const float*>(m_invstd.data_ptr()), gx.data_ptr(), (int64_t)dim,
+                                       static_cast<float*>(gg.data_ptr()), static_cast<float*>(gb.data_ptr()), 0,
+                                       (int64_t)rows, (int64_t)dim, detail::inf_dt(m_x.dtype(), "LayerNormBackward"),
+                                       ws.ptr, wsb, detail::stream_of(m_x)),
+                     "inf_layernorm_bwd");
+    }
+    if (wants_grad(m_x)) send(m_x, gx);
+    if (wants_grad(m_gamma)) send(m_gamma, gg);
+    if (wants_grad(m_beta)) send(m_beta, gb);
+}
+void LayerNormBackward::release() { m_x = m_gamma = m_beta = m_mean = m_invstd = Tensor(); }
+void LayerNormBackward::get_inputs(std::vector<Tensor>& out) const {
+    out.push_back(m_x);
+    out.push_back(m_gamma);
+    out.push_back(m_beta);
+}
+
+// ============================================================================
+// gelu
+// ============================================================================
+namespace {
+inline float gelu1(float x) {
+    const float a = 0.7978845608028654f, k = 0.044715f;
+    const float x3 = x * x * x;
+    return 0.5f * x * (1.0f + std::tanh(a * (x + k * x3)));
+}
+inline float gelu_grad1(float x) {
+    const float a = 0.7978845608028654f, k = 0.044715f;
+    const float x2 = x * x, x3 = x2 * x;
+    const float t = std::tanh(a * (x + k * x3));
+    const float sech2 = 1.0f - t * t;
+    return 0.5f * (1.0f + t) + 0.5f * x * sech2 * a * (1.0f + 3.0f * k * x2);
+}
+}  // namespace
+
+Tensor gelu(const Tensor& A) {
+    if (!A.defined()) throw Error("gelu: undefined input");
+    check_float(A, "gelu");
+    Tensor a = A.contiguous();
+    Tensor out(A.dtype(), A.shape(), "gelu", A.device(), false);
+    const size_t n = a.numel();
+    if (n) {
+        if (A.device().is_cpu()) {
+            const char* pa = static_cast<const char*>(a.data_ptr());
+            char* po = static_cast<char*>(out.data_ptr());
+            for (size_t i = 0; i < n; ++i) st_f(po, A.dtype(), (int64_t)i, gelu1(ld_f(pa, A.dtype(), (int64_t)i)));
+        } else {
+            DeviceGuard dg(A.device().index);
+            status_check(inf_gelu_fwd(a.data_ptr(), out.data_ptr(), (int64_t)n, detail::inf_dt(A.dtype(), "gelu"),
+                                      detail::stream_of(A)),
+                         "inf_gelu_fwd");
+        }
+    }
+    out.set_requires_grad(true);  // as the reference (gelu.cpp:29)
+    if (grad_enabled && A.requires_grad()) GetImpl(out)->gradfn() = std::make_shared<GeluBackward>(a);
+    return out;
+}
+
+GeluBackward::GeluBackward(const Tensor& x) : m_x(x) { set_name("GeluBackward"); }
+void GeluBackward::backward() {
+    NoGradGuard ng;
+    Tensor g = Engine::grad_in(this, 0).contiguous();
+    Tensor dx(m_x.dtype(), m_x.shape(), "gelu_grad", m_x.device(), false);
+    const size_t n = m_x.numel();
+    if (n) {
+        if (m_x.device().is_cpu()) {
+            const char* px = static_cast<const char*>(m_x.data_ptr());
+            const char* pg = static_cast<const char*>(g.data_ptr());
+            char* po = static_cast<char*>(dx.data_ptr());
+            for (size_t i = 0; i < n; ++i)
+                st_f(po, m_x.dtype(), (int64_t)i,
+                     ld_f(pg, m_x.dtype(), (int64_t)i) * gelu_grad1(ld_f(px, m_x.dtype(), (int64_t)i)));
+        } else {
+            DeviceGuard dg(m_x.device().index);
+            status_check(inf_gelu_bwd(m_x.data_ptr(), g.data_ptr(), dx.data_ptr(), (int64_t)n,
+                                      detail::inf_dt(m_x.dtype(), "GeluBackward"), detail::stream_of(m_x)),
+                         "inf_gelu_bwd");
+        }
+    }
+    send(m_x, dx);
+}
+void GeluBackward::release() { m_x = Tensor(); }
+void GeluBackward::get_inputs(std::vector<Tensor>& out) const { out.push_back(m_x); }
+
+// ============================================================================
+// embedding
+// ============================================================================
+Tensor embedding(const Tensor& ids, const Tensor& table) {
+    if (!ids.defined() || !table.defined()) throw Error("embedding: undefined input");
+    if (table.ndim() != 2) throw Error("embedding: table must be [vocab, dim]");
+    detail::same_device(ids, table, "embedding");
+    check_float(table, "embedding");
+    if (ids.dtype() != DType::Int32) throw Error("embedding: token ids must be Int32");
+    const size_t vocab = table.shape()[0], dim = table.shape()[1];
+    Tensor idc = ids.contiguous(), tc = table.contiguous();
+    std::vector<size_t> oshape = ids.shape();
+    oshape.push_back(dim);
+    Tensor out(table.dtype(), oshape, "embedding_out", table.device(), false);
+    const size_t n = idc.numel();
+    if (n) {
+        if (table.device().is_cpu()) {
+            // cpu_embedding (embedding_kernels.h:19-31); an id out of range throws
+            const int32_t* id = static_cast<const int32_t*>(idc.data_ptr());
+            const size_t esz = dtype_size(table.dtype());
+            for (size_t t = 0; t < n; ++t) {
+                if (id[t] < 0 || (size_t)id[t] >= vocab) throw Error("embedding: token id out of range");
+                std::memcpy(static_cast<char*>(out.data_ptr()) + t * dim * esz,
+                            static_cast<const char*>(tc.data_ptr()) + (size_t)id[t] * dim * esz, dim * esz);
+            }
+        } else {
+            DeviceGuard dg(table.device().index);
+            status_check(inf_embedding_fwd(static_cast<const int32_t*>(idc.data_ptr()), (int64_t)n, tc.data_ptr(),
+                                           (int64_t)vocab, (int64_t)dim, out.data_ptr(),
+                                           detail::inf_dt(table.dtype(), "embedding"), detail::stream_of(table)),
+                         "inf_embedding_fwd");
+        }
+    }
+    if (grad_enabled && table.requires_grad()) {
+        out.set_requires_grad(true);
+        GetImpl(out)->gradfn() = std::make_shared<EmbeddingBackward>(table, idc);
+    }
+    return out;
+}
+
+EmbeddingBackward::EmbeddingBackward(const Tensor& table, const Tensor& ids) : m_table(table), m_ids(ids) {
+    set_name("EmbeddingBackward");
+}
+void EmbeddingBackward::backward() {
+    NoGradGuard ng;
+    Tensor g = Engine::grad_in(this, 0).contiguous();
+    const size_t vocab = m_table.shape()[0], dim = m_table.shape()[1], n = m_ids.numel();
+    if (m_table.dtype() != DType::Float32) throw Error("EmbeddingBackward: Float32 tables only");
+    Tensor dt(DType::Float32, m_table.shape(), "EmbeddingBackward", m_table.device(), false);
+    if (m_table.device().is_cpu()) {
+        // scatter_add_embedding (broadcastops.cpp:120-166) into a zeroed gradient
+        float* o = static_cast<float*>(dt.data_ptr());
+        std::fill(o, o + vocab * dim, 0.f);
+        const int32_t* id = static_cast<const int32_t*>(m_ids.data_ptr());
+        const float* gp = static_cast<const float*>(g.data_ptr());
+        for (size_t t = 0; t < n; ++t)
+            for (size_t e = 0; e < dim; ++e) o[(size_t)id[t] * dim + e] += gp[t * dim + e];
+    } else {
+        DeviceGuard dg(m_table.device().index);
+        status_check(inf_embedding_bwd(static_cast<const int32_t*>(m_ids.data_ptr()), (int64_t)n,
+                                       static_cast<const float*>(g.data_ptr()), (int64_t)vocab, (int64_t)dim,
+                                       static_cast<float*>(dt.data_ptr()), 1, detail::stream_of(m_table)),
+                     "inf_embedding_bwd");
+    }
+    send(m_table, dt);
+}
+void EmbeddingBackward::release() { m_table = m_ids = Tensor(); }
+void EmbeddingBackward::get_inputs(std::vector<Tensor>& out) const { out.push_back(m_table); }
+
+// ============================================================================
+// cross_entropy
+// ============================================================================
+Tensor cross_entropy(const Tensor& logits, const Tensor& target) {
+    if (!logits.defined() || !target.defined()) throw Error("cross_entropy_loss: undefined input");
+    detail::same_device(logits, target, "cross_entropy_loss");
+    if (logits.ndim() < 2) throw Error("cross_entropy_loss requires logits rank >= 2");
+    if (target.ndim() != logits.ndim() - 1) throw Error("cross_entropy_loss requires target rank = logits rank - 1");
+    for (size_t i = 0; i < target.ndim(); ++i)
+        if (target.shape()[i] != logits.shape()[i]) throw Error("Shape mismatch on tensor parameters in cross_entropy_loss");
+    if (target.dtype() != DType::Int32) throw Error("cross_entropy_loss currently requires target dtype = Int32");
+    check_float(logits, "cross_entropy_loss");
+    Tensor lc = logits.contiguous(), tc = target.contiguous();
+    const size_t rows = tc.numel(), vocab = logits.shape().back();
+    Tensor out(DType::Float32, {1}, "cross_entropy_loss", logits.device(), false);
+    Tensor lse(DType::Float32, {rows}, "cross_entropy_lse", logits.device(), false);
+    if (logits.device().is_cpu()) {
+        // cpu_cross_entropy_loss (cpuops.h:707-749)
+        const char* pl = static_cast<const char*>(lc.data_ptr());
+        const int32_t* t = static_cast<const int32_t*>(tc.data_ptr());
+        float* pls = static_cast<float*>(lse.data_ptr());
+        float total = 0.f;
+        for (size_t r = 0; r < rows; ++r) {
+            if (t[r] < 0 || (size_t)t[r] >= vocab) throw Error("Target index out of bounds in cross_entropy_loss");
+            const int64_t base = (int64_t)(r * vocab);
+            float mx = ld_f(pl, logits.dtype(), base);
+            for (size_t v = 1; v < vocab; ++v) mx = std::max(mx, ld_f(pl, logits.dtype(), base + (int64_t)v));
+            float sum = 0.f;
+            for (size_t v = 0; v < vocab; ++v) sum += std::exp(ld_f(pl, logits.dtype(), base + (int64_t)v) - mx);
+            const float l = std::log(sum);
+            pls[r] = mx + l;
+            total += -(ld_f(pl, logits.dtype(), base + t[r]) - mx - l);
+        }
+        *static_cast<float*>(out.data_ptr()) = total / (float)rows;
+    } else {
+        size_t wsb = 0;
+        status_check(inf_nn_workspace_bytes(INF_OP_CROSS_ENTROPY, (int64_t)rows, (int64_t)vocab, &wsb),
+                     "inf_nn_workspace_bytes");
+        Scratch ws(wsb, logits.device());
+        DeviceGuard dg(logits.device().index);
+        status_check(inf_cross_entropy_fwd(lc.data_ptr(), (int64_t)vocab, static_cast<const int32_t*>(tc.data_ptr()),
+                                           static_cast<float*>(out.data_ptr()), static_cast<float*>(lse.data_ptr()),
+                                           (int64_t)rows, (int64_t)vocab,
+                                           detail::inf_dt(logits.dtype(), "cross_entropy_loss"), ws.ptr, wsb,
+                                           detail::stream_of(logits)),
+                     "inf_cross_entropy_fwd");
+    }
+    out.set_requires_grad(true);  // as the reference (crossentropyloss.cpp: Tensor(..., true))
+    if (grad_enabled && logits.requires_grad())
+        GetImpl(out)->gradfn() = std::make_shared<CrossEntropyLossBackward>(lc, tc, lse);
+    return out;
+}
+
+CrossEntropyLossBackward::CrossEntropyLossBackward(const Tensor& logits, const Tensor& target, const Tensor& lse)
+    : m_logits(logits), m_target(target), m_lse(lse) {
+    set_name("CrossEntropyLossBackward");
+}
+void CrossEntropyLossBackward::backward() {
+    NoGradGuard ng;
+    Tensor g = Engine::grad_in(this, 0);
+    if (g.dtype() != DType::Float32) throw Error("CrossEntropyLossBackward: Float32 upstream gradient expected");
+    const size_t rows = m_target.numel(), vocab = m_logits.shape().back();
+    Tensor grad(m_logits.dtype(), m_logits.shape(), "cross_entropy_grad_logits", m_logits.device(), false);
+    if (m_logits.device().is_cpu()) {
+        // cpu_cross_entropy_loss_backward (crossentropylossbackward.h:45-86)
+        const char* pl = static_cast<const char*>(m_logits.data_ptr());
+        const int32_t* t = static_cast<const int32_t*>(m_target.data_ptr());
+        char* po = static_cast<char*>(grad.data_ptr());
+        const DType dt = m_logits.dtype();
+        const float scale = *static_cast<const float*>(g.data_ptr()) / (float)rows;
+        for (size_t r = 0; r < rows; ++r) {
+            const int64_t base = (int64_t)(r * vocab);
+            float mx = ld_f(pl, dt, base);
+            for (size_t v = 1; v < vocab; ++v) mx = std::max(mx, ld_f(pl, dt, base + (int64_t)v));
+            float sum = 0.f;
+            for (size_t v = 0; v < vocab; ++v) sum += std::exp(ld_f(pl, dt, base + (int64_t)v) - mx);
+            for (size_t v = 0; v < vocab; ++v)
+                st_f(po, dt, base + (int64_t)v, std::exp(ld_f(pl, dt, base + (int64_t)v) - mx) / sum * scale);
+            st_f(po, dt, base + t[r], ld_f(po, dt, base + t[r]) - scale);
+        }
+    } else {
+        DeviceGuard dg(m_logits.device().index);
+        status_check(inf_cross_entropy_bwd(m_logits.data_ptr(), (int64_t)vocab,
+                                           static_cast<const int32_t*>(m_target.data_ptr()),
+                                           static_cast<const float*>(m_lse.data_ptr()),
+                                           static_cast<const float*>(g.data_ptr()), grad.data_ptr(), (int64_t)vocab,
+                                           (int64_t)rows, (int64_t)vocab,
+                                           detail::inf_dt(m_logits.dtype(), "CrossEntropyLossBackward"),
+                                           detail::stream_of(m_logits)),
+                     "inf_cross_entropy_bwd");
+    }
+    send(m_logits, grad);
+}
+void CrossEntropyLossBackward::release() { m_logits = m_target = m_lse = Tensor(); }
+void CrossEntropyLossBackward::get_inputs(std::vector<Tensor>& out) const { out.push_back(m_logits); }
+
+// ============================================================================
+// qkv_attention
+// ============================================================================
+namespace {
+struct QKVShape {
+    size_t B, T, C, H, D;
+};
+QKVShape qkv_shape(const Tensor& qkv, size_t heads) {
+    if (qkv.ndim() != 3) throw Error("qkv_attention: qkv must be [B, T, 3C]");
+    const size_t B = qkv.shape()[0], T = qkv.shape()[1], C3 = qkv.shape()[2];
+    if (C3 % 3 || heads == 0 || (C3 / 3) % heads) throw Error("qkv_attention: 3C must split into heads");
+    return {B, T, C3 / 3, heads, C3 / 3 / heads};
+}
+inf_strides head_view(const Tensor& t, size_t D) {
+    // [B, T, H*D]-shaped rows read as [B, H, T, D]
+    return inf_strides{(int64_t)t.strides()[0], (int64_t)D, (int64_t)t.strides()[1], 1};
+}
+}  // namespace
+
+Tensor qkv_attention(const Tensor& qkv, size_t num_heads, bool causal, float scale) {
+    if (!qkv.defined()) throw Error("qkv_attention: undefined input");
+    check_float(qkv, "qkv_attention");
+    const QKVShape s = qkv_shape(qkv, num_heads);
+    const float sc = std::isnan(scale) ? 1.0f / std::sqrt((float)s.D) : scale;
+    if (qkv.device().is_cpu()) {
+        // Compose the fused reference chain on views; autograd flows through them.
+        Tensor q = qkv.slice(2, 0, s.C - 1).unflatten(2, {s.H, s.D}).transpose(1, 2);
+        Tensor k = qkv.slice(2, s.C, 2 * s.C - 1).unflatten(2, {s.H, s.D}).transpose(1, 2);
+        Tensor v = qkv.slice(2, 2 * s.C, 3 * s.C - 1).unflatten(2, {s.H, s.D}).transpose(1, 2);
+        Tensor y = scaled_dot_product_attention(q, k, v, causal, sc);
+        return y.transpose(1, 2).contiguous().reshape({s.B, s.T, s.C});
+    }
+    Tensor in = qkv;
+    const size_t esz = dtype_size(qkv.dtype());
+    const auto& st = qkv.strides();
+    if (st[2] != 1 || st[0] % 4 || st[1] % 4 || reinterpret_cast<uintptr_t>(qkv.data_ptr()) % (4 * esz)) {
+        NoGradGuard ng;
+        in = detail::dense_copy(qkv);
+    }
+    Tensor y(qkv.dtype(), {s.B, s.T, s.C}, "attention_out", qkv.device(), false);
+    Tensor lse(DType::Float32, {s.B, s.H, s.T}, "attention_lse", qkv.device(), false);
+    if (s.B && s.T) {
+        const char* base = static_cast<const char*>(in.data_ptr());
+        const inf_strides sv = head_view(in, s.D), so = head_view(y, s.D);
+        DeviceGuard dg(qkv.device().index);
+        status_check(inf_attn_fwd(base, sv, base + s.C * esz, sv, base + 2 * s.C * esz, sv, y.data_ptr(), so,
+                                  static_cast<float*>(lse.data_ptr()), (int)s.B, (int)s.H, (int)s.T, (int)s.T,
+                                  (int)s.D, sc, causal ? 1 : 0, detail::inf_dt(qkv.dtype(), "qkv_attention"),
+                                  detail::stream_of(qkv)),
+                     "inf_attn_fwd");
+    }
+    if (grad_enabled && qkv.requires_grad()) {
+        y.set_requires_grad(true);
+        GetImpl(y)->gradfn() = std::make_shared<QKVAttentionBackward>(qkv, y, lse, num_heads, causal, sc);
+    }
+    return y;
+}
+
+QKVAttentionBackward::QKVAttentionBackward(const Tensor& qkv, const Tensor& y, const Tensor& lse, size_t num_heads,
+                                           bool causal, float scale)
+    : m_qkv(qkv),
+      m_y(make_view(y, y.shape(), y.strides(), y.offset(), "attention_saved")),
+      m_lse(lse),
+      m_heads(num_heads),
+      m_causal(causal),
+      m_scale(scale) {
+    set_name("QKVAttentionBackward");
+}
+
+void QKVAttentionBackward::backward() {
+    NoGradGuard ng;
+    Tensor g = Engine::grad_in(this, 0);
+    const QKVShape s = qkv_shape(m_qkv, m_heads);
+    const size_t esz = dtype_size(m_qkv.dtype());
+    Tensor in = m_qkv;
+    const auto& st = in.strides();
+    if (st[2] != 1 || st[0] % 4 || st[1] % 4 || reinterpret_cast<uintptr_t>(in.data_ptr()) % (4 * esz))
+        in = detail::dense_copy(in);
+    if (!g.is_contiguous()) g = detail::dense_copy(g);
+    Tensor dqkv(m_qkv.dtype(), {s.B, s.T, 3 * s.C}, "attention_dqkv", m_qkv.device(), false);
+    if (s.B && s.T) {
+        const inf_dtype dt = detail::inf_dt(m_qkv.dtype(), "QKVAttentionBackward");
+        size_t wsb = 0;
+        status_check(inf_attn_workspace_bytes(INF_OP_ATTN_BWD, (int)s.B, (int)s.H, (int)s.T, (int)s.T, (int)s.D, dt,
+                                              &wsb),
+                     "inf_attn_workspace_bytes");
+        Scratch ws(wsb, m_qkv.device());
+        const char* base = static_cast<const char*>(in.data_ptr());
+        char* dbase = static_cast<char*>(dqkv.data_ptr());
+        const inf_strides sv = head_view(in, s.D), sd = head_view(dqkv, s.D), so = head_view(m_y, s.D),
+                          sg = head_view(g, s.D);
+        DeviceGuard dg(m_qkv.device().index);
+        status_check(inf_attn_bwd(base, sv, base + s.C * esz, sv, base + 2 * s.C * esz, sv, m_y.data_ptr(), so,
+                                  g.data_ptr(), sg, static_cast<const float*>(m_lse.data_ptr()), dbase, sd,
+                                  dbase + s.C * esz, sd, dbase + 2 * s.C * esz, sd, ws.ptr, wsb, (int)s.B, (int)s.H,
+                                  (int)s.T, (int)s.T, (int)s.D, m_scale, m_causal ? 1 : 0, dt,
+                                  detail::stream_of(m_qkv)),
+                     "inf_attn_bwd");
+    }
+    send(m_qkv, dqkv);
+}
+void QKVAttentionBackward::release() { m_qkv = m_y = m_lse = Tensor(); }
+void QKVAttentionBackward::get_inputs(std::vector<Tensor>& out) const { out.push_back(m_qkv); }
+
+}  // namespace Inferno

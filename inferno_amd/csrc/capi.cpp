@@ -9,6 +9,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <string>
 
 #include "kernels.h"
 
@@ -51,9 +52,17 @@ int common_shape(int B, int H, int Tq, int Tk, int D, float scale, int dt) {
 }
 
 
+thread_local std::string t_detail;
+
 }  // namespace
 
+namespace inf {
+void set_error_detail(const std::string& msg) { t_detail = msg; }
+}  // namespace inf
+
 extern "C" {
+
+const char* inf_last_error_detail(void) { return t_detail.c_str(); }
 
 const char* inf_status_string(int status) {
     switch (status) {

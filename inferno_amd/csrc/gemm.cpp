@@ -14,12 +14,15 @@
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <cstdio>
 #include <cstring>
 #include <mutex>
 #include <unordered_map>
 #include <vector>
 
 #include "kernels.h"
+
+#include <string>
 
 namespace inf {
 
@@ -41,11 +44,14 @@ struct KeyHash {
     }
 };
 
+constexpr int kMaxAlgos = 16;
+
 struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
-    hipblasLtMatmulAlgo_t algo{};
-    size_t ws = 0;
+    hipblasLtMatmulAlgo_t algo[kMaxAlgos]{};
+    int n_algo = 0;
+    int cur = 0;  // the candidate in use: the first one that launched
 };
 
 std::mutex g_mu;
@@ -109,22 +115,25 @@ int make_plan(hipblasLtHandle_t h, const Key& k, Plan& p) {
     if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return 1;
     const uint64_t wsmax = k.ws;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax, sizeof(wsmax));
-    hipblasLtMatmulHeuristicResult_t res[4];
+    hipblasLtMatmulHeuristicResult_t res[kMaxAlgos];
     int n = 0;
     const hipblasStatus_t st =
-        hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 4, res, &n);
+        hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, kMaxAlgos, res, &n);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (st != HIPBLAS_STATUS_SUCCESS || n < 1) return 2;
-    p.algo = res[0].algo;
-    p.ws = res[0].workspaceSize;
-    return 0;
+    for (int i = 0; i < n && i < kMaxAlgos; ++i)
+        if (res[i].state == HIPBLAS_STATUS_SUCCESS) p.algo[p.n_algo++] = res[i].algo;
+    return p.n_algo ? 0 : 2;
 }
 
 }  // namespace
 
 int launch_gemm(const GemmArgs& g, hipStream_t s) {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        set_error_detail("inf_gemm: hipGetDevice failed");
+        return 1;
+    }
     Key k;
     std::memset(&k, 0, sizeof(k));  // padding bytes take part in hashing / comparison
     k.ta = g.ta;
@@ -144,14 +153,23 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
     k.batch = g.batch;
     k.ws = g.ws_bytes;
     std::lock_guard<std::mutex> lk(g_mu);
+    char shape[192];
+    std::snprintf(shape, sizeof(shape), "M=%lld N=%lld K=%lld ta=%d tb=%d lda=%lld ldb=%lld ldc=%lld batch=%lld bias=%d",
+                  (long long)g.M, (long long)g.N, (long long)g.K, g.ta, g.tb, (long long)g.lda, (long long)g.ldb,
+                  (long long)g.ldc, (long long)g.batch, g.bias != nullptr);
     hipblasLtHandle_t h = handle_for(dev);
-    if (!h) return 1;
+    if (!h) {
+        set_error_detail("inf_gemm: hipblasLtCreate failed");
+        return 1;
+    }
     auto it = g_plans->find(k);
     if (it == g_plans->end()) {
         Plan p;
         const int e = make_plan(h, k, p);
         if (e) {
             destroy(p);
+            set_error_detail(std::string("inf_gemm: ") + (e == 2 ? "no hipBLASLt algorithm" : "descriptor setup failed") +
+                             " for " + shape);
             return e == 2 ? 2 : 1;
         }
         it = g_plans->emplace(k, p).first;
@@ -159,13 +177,36 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
     Plan& p = it->second;
     if (g.bias) {
         const void* bp = g.bias;
-        if (hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof(bp)))
+        if (hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof(bp))) {
+            set_error_detail(std::string("inf_gemm: setting the bias pointer failed for ") + shape);
             return 1;
+        }
     }
+    // An error left pending by an earlier, unrelated HIP call would otherwise be
+    // reported by the library as its own failure.
+    const hipError_t pending = hipGetLastError();
     const float alpha = g.alpha, beta = g.beta;
-    const hipblasStatus_t st = hipblasLtMatmul(h, p.desc, &alpha, g.B, p.la, g.A, p.lb, &beta, g.C, p.lc, g.C, p.lc,
-                                               &p.algo, g.ws, g.ws_bytes, s);
-    return st == HIPBLAS_STATUS_SUCCESS ? 0 : 1;
+    // The heuristic's candidates in order, starting from the one in use: a
+    // candidate the installed library cannot launch (some builds return
+    // HIPBLAS_STATUS_INTERNAL_ERROR for a listed solution) is skipped for good.
+    hipblasStatus_t st = HIPBLAS_STATUS_NOT_SUPPORTED;
+    for (; p.cur < p.n_algo; ++p.cur) {
+        st = hipblasLtMatmul(h, p.desc, &alpha, g.B, p.la, g.A, p.lb, &beta, g.C, p.lc, g.C, p.lc, &p.algo[p.cur],
+                             g.ws, g.ws_bytes, s);
+        if (st == HIPBLAS_STATUS_SUCCESS) break;
+        (void)hipGetLastError();
+    }
+    if (st != HIPBLAS_STATUS_SUCCESS) {
+        p.cur = 0;  // all failed: start over on the next call
+        set_error_detail(std::string("inf_gemm: hipblasLtMatmul status ") + std::to_string((int)st) + " for " + shape +
+                         " with every one of " + std::to_string(p.n_algo) +
+                         " heuristic candidates; HIP error pending before the call: " + hipGetErrorString(pending));
+        return 1;
+    }
+    if (pending != hipSuccess)
+        set_error_detail(std::string("inf_gemm: cleared a pending HIP error before the call: ") +
+                         hipGetErrorString(pending));
+    return 0;
 }
 
 }  // namespace inf

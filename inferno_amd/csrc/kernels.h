@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+
 namespace inf {
 
 struct View4 {            // element strides of a [B,H,T,D] view, d stride 1
@@ -150,6 +152,9 @@ struct GemmArgs {         // row-major C = alpha * op(A) op(B) + beta * C (+ bia
 };
 // 0 = ok, 1 = library error, 2 = no algorithm for the problem
 int launch_gemm(const GemmArgs& g, hipStream_t s);
+
+// Thread-local text about the last failure inside the library (inf_last_error_detail).
+void set_error_detail(const std::string& msg);
 
 constexpr int kLnBwdMaxBlocks = 512;  // stage-1 workgroups of the LayerNorm backward
 constexpr int kLnBwdMaxDim = 2048;    // register path of the LayerNorm backward

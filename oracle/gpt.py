@@ -1,0 +1,149 @@
+"""Oracle for one GPT training step (forward, cross-entropy, backward, AdamW).
+
+TEST INFRASTRUCTURE ONLY (see the package docstring): the checker for the
+C++ GPT step (inferno_amd/app/gpt.cpp) on the HIP and CPU devices.
+
+The model is the reference application's GPTModel / TransformerBlock
+(InfernoApp/main.cpp:817-1033) with the output projection tied to the token
+embedding, and attention computed by the reference chain (oracle.attn_fwd /
+attn_bwd restate main.cpp:737-754 and its backward nodes).  The backward is
+written out by hand, layer by layer, from the reference's node formulas --
+MMBackward (dA = G B^T, dB = A^T G), AddBackward (identity; bias gradients
+summed over rows as sum_to_shape does), LayerNormBackward, GeluBackward,
+CrossEntropyLossBackward, EmbeddingBackward -- so it checks the C++ graph's
+wiring as well as its arithmetic.  Unlike the reference's own MHA (whose
+.contiguous() calls cut the graph, ops.cpp:1308), gradients flow through the
+attention into Wqkv and the LayerNorm before it, as in the fused module.
+
+Every 2-D product goes through oracle.matmul (the restated cpu_matmul, fp32
+sums in k order); each op's fp32 rounding points follow the oracle kernels.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle
+from oracle import nn as onn
+
+
+def positional_encoding(T: int, C: int) -> np.ndarray:
+    """main.cpp:26-43 in float arithmetic."""
+    pe = np.empty((T, C), np.float32)
+    for pos in range(T):
+        for i in range(C):
+            exponent = np.float32(2.0) * np.float32(i // 2) / np.float32(C)
+            angle = np.float32(pos) / np.power(np.float32(10000.0), exponent, dtype=np.float32)
+            pe[pos, i] = np.sin(angle, dtype=np.float32) if i % 2 == 0 else np.cos(angle, dtype=np.float32)
+    return pe
+
+
+def param_shapes(L: int, C: int, V: int) -> dict:
+    """State-dict names and shapes of the tied GPT (gpt.cpp's GPTModel)."""
+    out = {"tok_embedding.weight": (V, C), "ln1.beta": (C,), "ln1.gamma": (C,)}
+    for l in range(L):
+        p = f"block{l}."
+        out.update({
+            p + "attn.Wqkv.weights": (C, 3 * C), p + "attn.Wqkv.bias": (3 * C,),
+            p + "attn.W_out.weights": (C, C), p + "attn.W_out.bias": (C,),
+            p + "ln1.beta": (C,), p + "ln1.gamma": (C,), p + "ln2.beta": (C,), p + "ln2.gamma": (C,),
+            p + "ff1.weights": (C, 4 * C), p + "ff1.bias": (4 * C,),
+            p + "ff2.weights": (4 * C, C), p + "ff2.bias": (C,),
+        })
+    return out
+
+
+def init_params(L, C, V, seed=1234):
+    """Seeded parameters: weights N(0, 0.05^2), biases N(0, 0.01^2), LayerNorm gamma 1 + N(0, 0.1^2)."""
+    params = {}
+    for i, (name, shp) in enumerate(sorted(param_shapes(L, C, V).items())):
+        if name.endswith("gamma"):
+            params[name] = (1.0 + oracle.randn(seed + i, shp, 0.1)).astype(np.float32)
+        elif name.endswith("beta") or name.endswith("bias"):
+            params[name] = oracle.randn(seed + i, shp, 0.01)
+        else:
+            params[name] = oracle.randn(seed + i, shp, 0.05)
+    return params
+
+
+def _mm(a, b):
+    return oracle.matmul(np.ascontiguousarray(a, np.float32), np.ascontiguousarray(b, np.float32))
+
+
+def _linear(x2, W, b):
+    return (_mm(x2, W) + b).astype(np.float32)
+
+
+def gpt_loss(params, tokens, targets, L, C, H):
+    """The forward alone (the loss)."""
+    return gpt_step(params, tokens, targets, L, C, H, backward=False)
+
+
+def gpt_step(params, tokens, targets, L, C, H, step=1, lr=3e-4, backward=True):
+    """Returns (loss, grads, new_params) for one AdamW step from zero moments."""
+    P = {k: np.asarray(v, np.float32) for k, v in params.items()}
+    B, T = tokens.shape
+    V = P["tok_embedding.weight"].shape[0]
+    D = C // H
+    N = B * T
+    E = P["tok_embedding.weight"]
+    x = onn.embedding(tokens, E).reshape(N, C)
+    x = (x.reshape(B, T, C) + positional_encoding(T, C)).astype(np.float32).reshape(N, C)
+    cache = []
+    for l in range(L):
+        p = f"block{l}."
+        y1, m1, s1 = onn.layernorm(x, P[p + "ln1.gamma"], P[p + "ln1.beta"])
+        qkv = _linear(y1, P[p + "attn.Wqkv.weights"], P[p + "attn.Wqkv.bias"])
+        heads = [qkv[:, j * C:(j + 1) * C].reshape(B, T, H, D).transpose(0, 2, 1, 3) for j in range(3)]
+        q, k, v = (np.ascontiguousarray(t) for t in heads)
+        o, _ = oracle.attn_fwd(q, k, v)
+        ya = np.ascontiguousarray(o.transpose(0, 2, 1, 3)).reshape(N, C)
+        a = _linear(ya, P[p + "attn.W_out.weights"], P[p + "attn.W_out.bias"])
+        h = (x + a).astype(np.float32)
+        y2, m2, s2 = onn.layernorm(h, P[p + "ln2.gamma"], P[p + "ln2.beta"])
+        f1 = _linear(y2, P[p + "ff1.weights"], P[p + "ff1.bias"])
+        gl = onn.gelu(f1)
+        f2 = _linear(gl, P[p + "ff2.weights"], P[p + "ff2.bias"])
+        cache.append((x, y1, m1, s1, q, k, v, ya, h, y2, m2, s2, f1, gl))
+        x = (h + f2).astype(np.float32)
+    xf, mf, sf = onn.layernorm(x, P["ln1.gamma"], P["ln1.beta"])
+    logits = _mm(xf, E.T)
+    loss = onn.cross_entropy(logits, targets.reshape(-1))
+    if not backward:
+        return loss
+
+    G = {}
+    dlog = onn.cross_entropy_bwd(logits, targets.reshape(-1), 1.0)
+    dxf = _mm(dlog, E)
+    dE = _mm(dlog.T, xf)
+    dx, G["ln1.gamma"], G["ln1.beta"] = onn.layernorm_bwd(x, dxf, P["ln1.gamma"], mf, sf)
+    for l in reversed(range(L)):
+        p = f"block{l}."
+        (xl, y1, m1, s1, q, k, v, ya, h, y2, m2, s2, f1, gl) = cache[l]
+        df2 = dx
+        G[p + "ff2.weights"] = _mm(gl.T, df2)
+        G[p + "ff2.bias"] = onn.sum_rows(df2)
+        dgl = _mm(df2, P[p + "ff2.weights"].T)
+        df1 = onn.gelu_bwd(f1, dgl)
+        G[p + "ff1.weights"] = _mm(y2.T, df1)
+        G[p + "ff1.bias"] = onn.sum_rows(df1)
+        dy2 = _mm(df1, P[p + "ff1.weights"].T)
+        dh_ln, G[p + "ln2.gamma"], G[p + "ln2.beta"] = onn.layernorm_bwd(h, dy2, P[p + "ln2.gamma"], m2, s2)
+        dh = (dx + dh_ln).astype(np.float32)
+        G[p + "attn.W_out.weights"] = _mm(ya.T, dh)
+        G[p + "attn.W_out.bias"] = onn.sum_rows(dh)
+        dya = _mm(dh, P[p + "attn.W_out.weights"].T)
+        do = np.ascontiguousarray(dya.reshape(B, T, H, D).transpose(0, 2, 1, 3))
+        dq, dk, dv = oracle.attn_bwd(q, k, v, do)
+        dqkv = np.concatenate([t.transpose(0, 2, 1, 3).reshape(N, C) for t in (dq, dk, dv)], axis=1)
+        G[p + "attn.Wqkv.weights"] = _mm(y1.T, dqkv)
+        G[p + "attn.Wqkv.bias"] = onn.sum_rows(dqkv)
+        dy1 = _mm(dqkv, P[p + "attn.Wqkv.weights"].T)
+        dx_ln, G[p + "ln1.gamma"], G[p + "ln1.beta"] = onn.layernorm_bwd(xl, dy1, P[p + "ln1.gamma"], m1, s1)
+        dx = (dh + dx_ln).astype(np.float32)
+    G["tok_embedding.weight"] = (dE + onn.embedding_bwd(tokens.reshape(-1), dx, V)).astype(np.float32)
+
+    new = {}
+    for name, val in P.items():
+        z = np.zeros_like(val)
+        new[name], _, _ = onn.adamw(val, G[name], z, z, step, lr=lr)
+    return loss, G, new

@@ -1,0 +1,110 @@
+"""One GPT training step (forward, cross-entropy, backward, AdamW) through the
+C++ drop-in (inferno_amd/gpt step), against the oracle's hand-written step
+(oracle/gpt.py), on the CPU device (here) and the HIP device (-m gpu).
+
+The oracle step itself is pinned by a directional finite difference of its
+forward: (L(P + h u) - L(P - h u)) / 2h = <grad, u> for a random direction u
+over every parameter.
+
+Bar: max|x - ref| / max|ref| <= 1e-4 per tensor (fp32), for the loss, every
+parameter gradient and every updated parameter.
+"""
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import gpt as ogpt
+from oracle import nn as onn
+
+ROOT = Path(__file__).resolve().parents[1]
+APP = ROOT / "inferno_amd" / "gpt"
+TOL = 1e-4
+
+
+def make_case(tmp_path, L, C, H, T, V, B, seed=7):
+    params = ogpt.init_params(L, C, V)
+    rng = np.random.default_rng(seed)
+    seq = rng.integers(0, V, size=(B, T + 1), dtype=np.int32)
+    tokens, targets = np.ascontiguousarray(seq[:, :T]), np.ascontiguousarray(seq[:, 1:])
+    (tmp_path / "config.txt").write_text(f"{L} {C} {H} {T} {V} {B}\n")
+    tokens.tofile(tmp_path / "tokens.bin")
+    targets.tofile(tmp_path / "targets.bin")
+    for name, val in params.items():
+        np.ascontiguousarray(val, np.float32).tofile(tmp_path / f"{name}.bin")
+    return params, tokens, targets
+
+
+def run_app(tmp_path, device):
+    if not APP.exists():
+        pytest.skip("inferno_amd/gpt not built (run __graft_entry__.build())")
+    r = subprocess.run([str(APP), "step", str(tmp_path), device], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+def check_against_oracle(tmp_path, params, tokens, targets, L, C, H):
+    """Loss and gradients against the oracle step; the update against the
+    oracle's AdamW applied to the app's own gradients.
+
+    The update is checked that way because AdamW's first step is
+    g / (|g| + eps) ~ sign(g): where a gradient is zero up to rounding (the key
+    part of Wqkv's bias: a constant added to every key leaves the softmax
+    unchanged), the update follows rounding noise of either implementation.
+    """
+    loss, G, _ = ogpt.gpt_step(params, tokens, targets, L, C, H)
+    got_loss = float(np.fromfile(tmp_path / "loss.bin", np.float32)[0])
+    assert abs(got_loss - loss) <= TOL * abs(loss), (got_loss, loss)
+    bad = {}
+    for name in params:
+        g = np.fromfile(tmp_path / f"grad_{name}.bin", np.float32).reshape(params[name].shape)
+        p = np.fromfile(tmp_path / f"param_{name}.bin", np.float32).reshape(params[name].shape)
+        z = np.zeros_like(params[name])
+        want_p, _, _ = onn.adamw(params[name], g, z, z, 1)
+        eg, ep = oracle.rel_err(g, G[name]), oracle.rel_err(p, want_p)
+        if not (eg <= TOL and ep <= 1e-6):
+            bad[name] = (eg, ep)
+    assert not bad, bad
+
+
+def test_oracle_step_directional_derivative():
+    L, C, H, T, V, B = 1, 32, 2, 8, 48, 2
+    params = ogpt.init_params(L, C, V, seed=99)
+    rng = np.random.default_rng(3)
+    seq = rng.integers(0, V, size=(B, T + 1), dtype=np.int32)
+    tokens, targets = np.ascontiguousarray(seq[:, :T]), np.ascontiguousarray(seq[:, 1:])
+    _, G, _ = ogpt.gpt_step(params, tokens, targets, L, C, H)
+    u = {k: rng.standard_normal(v.shape).astype(np.float32) for k, v in params.items()}
+    h = 1e-3  # central difference of the fp32 forward: O(h^2) bias, ~1e-4 rounding noise
+
+    def dd(keys):
+        plus = {k: (params[k] + h * u[k]).astype(np.float32) if k in keys else params[k] for k in params}
+        minus = {k: (params[k] - h * u[k]).astype(np.float32) if k in keys else params[k] for k in params}
+        num = (ogpt.gpt_loss(plus, tokens, targets, L, C, H) - ogpt.gpt_loss(minus, tokens, targets, L, C, H)) / (2 * h)
+        ana = sum(float(np.sum(G[k].astype(np.float64) * u[k])) for k in keys)
+        return num, ana
+
+    num, ana = dd(set(params))
+    assert abs(num - ana) <= 1e-3 * abs(ana), (num, ana)
+    # every parameter group on its own: a dropped or mis-signed term moves its
+    # derivative by at least |a|, far above the 1e-3 noise floor used here
+    for k in params:
+        n_k, a_k = dd({k})
+        assert abs(n_k - a_k) <= 1e-3 + 0.02 * abs(a_k), (k, n_k, a_k)
+
+
+def test_gpt_step_cpu_matches_oracle(tmp_path):
+    L, C, H, T, V, B = 2, 32, 1, 8, 40, 2
+    params, tokens, targets = make_case(tmp_path, L, C, H, T, V, B)
+    run_app(tmp_path, "cpu")
+    check_against_oracle(tmp_path, params, tokens, targets, L, C, H)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("L,C,H,T,V,B", [(2, 64, 2, 64, 128, 2), (1, 128, 2, 33, 96, 3)])
+def test_gpt_step_hip_matches_oracle(tmp_path, L, C, H, T, V, B):
+    print(f"[case] gpt step hip L{L} C{C} H{H} T{T} V{V} B{B}", flush=True)
+    params, tokens, targets = make_case(tmp_path, L, C, H, T, V, B)
+    run_app(tmp_path, "hip")
+    check_against_oracle(tmp_path, params, tokens, targets, L, C, H)
