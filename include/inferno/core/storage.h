@@ -2,10 +2,11 @@
 //
 // Storage / CPUStorage follow the reference (src/inferno/storage/storage.h:19-64,
 // cpustorage.h:19-33).  HIPStorage replaces CUDAStorage (cudastorage.cpp:16-23):
-// it allocates with hipMallocAsync on the device's library stream (the runtime's
-// stream-ordered pool, so the per-op allocation the reference pays with
-// cudaMalloc becomes a pool hit) and frees with hipFreeAsync on the same
-// stream.  Allocation failures throw instead of being ignored.
+// freed blocks go to a per-device cache and are handed to the next allocation
+// of the same size class (every tensor on a device is used in order on that
+// device's library stream, so reuse needs no synchronisation); a miss allocates
+// with hipMallocAsync on that stream.  The reference pays a cudaMalloc per op
+// output instead.  Allocation failures throw instead of being ignored.
 #pragma once
 
 #include <cstddef>

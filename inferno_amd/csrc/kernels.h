@@ -157,6 +157,7 @@ int launch_gemm(const GemmArgs& g, hipStream_t s);
 void set_error_detail(const std::string& msg);
 
 constexpr int kLnBwdMaxBlocks = 512;  // stage-1 workgroups of the LayerNorm backward
+constexpr int kColChunk = 32;         // rows per partial of the column sum
 constexpr int kLnBwdMaxDim = 2048;    // register path of the LayerNorm backward
 int ln_bwd_blocks(int64_t rows);
 int col_sum_chunks(int64_t rows);     // partial rows the column sum needs

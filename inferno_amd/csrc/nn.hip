@@ -217,15 +217,16 @@ __global__ __launch_bounds__(256) void col_reduce_kernel(const float* __restrict
 }
 
 // Column sums of a dense [rows, cols] matrix in two stages: per-chunk partials
-// (chunk = 256 rows), then col_reduce over the chunks.
+// (chunk = kColChunk rows, so a [8192, 768] gradient runs 768 workgroups), then
+// col_reduce over the chunks.
 template <typename E>
 __global__ __launch_bounds__(256) void col_partial_kernel(const void* __restrict__ x, float* __restrict__ part,
                                                           int64_t rows, int64_t cols, int64_t ldx) {
     const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t r0 = (int64_t)blockIdx.y * 256;
+    const int64_t r0 = (int64_t)blockIdx.y * kColChunk;
     if (c >= cols) return;
     const typename E::T* p = (const typename E::T*)x;
-    const int64_t r1 = min(rows, r0 + 256);
+    const int64_t r1 = min(rows, r0 + kColChunk);
     float s = 0.f;
     for (int64_t r = r0; r < r1; ++r) s += E::ld(p + r * ldx + c);
     part[(int64_t)blockIdx.y * cols + c] = s;
@@ -515,7 +516,7 @@ int launch_ln_bwd(const LnBwdParams& p, int bf16, hipStream_t s) {
 
 int launch_col_sum(const void* x, float* out, float* part, int64_t rows, int64_t cols, int64_t ldx, int accumulate,
                    int bf16, hipStream_t s) {
-    const int64_t chunks = (rows + 255) / 256;
+    const int64_t chunks = col_sum_chunks(rows);
     const dim3 g1(blocks_for(cols, 256), (unsigned)chunks);
     if (bf16)
         hipLaunchKernelGGL(col_partial_kernel<BF16>, g1, dim3(256), 0, s, x, part, rows, cols, ldx);
@@ -526,7 +527,7 @@ int launch_col_sum(const void* x, float* out, float* part, int64_t rows, int64_t
     return (int)hipGetLastError();
 }
 
-int col_sum_chunks(int64_t rows) { return (int)((rows + 255) / 256); }
+int col_sum_chunks(int64_t rows) { return (int)((rows + kColChunk - 1) / kColChunk); }
 
 int launch_gelu_fwd(const void* x, void* y, int64_t n, int bf16, hipStream_t s) {
     const dim3 grid(blocks_for(n, 1024));
