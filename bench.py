@@ -77,7 +77,8 @@ def main():
     ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--cpu-heads", type=int, default=12, help="heads in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16 and config-4 lines")
+    ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16, config-3 and config-4 lines")
+    ap.add_argument("--gpt-steps", type=int, default=5, help="timed steps of the config-3 GPT line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 512 MiB device copy 5 times (HBM-counter calibration)")
     args = ap.parse_args()
@@ -195,6 +196,8 @@ def main():
             "c4_f32": bench_attn(ia, oracle, torch, np, dev, 1, 16, 8192, 128, 3.0, "f32", steps=5),
             "c4_bf16": bench_attn(ia, oracle, torch, np, dev, 1, 16, 8192, 128, 3.0, "bf16", steps=5),
         }
+        torch.cuda.empty_cache()
+        out["configs"]["c3_gpt"] = bench_gpt(args.gpt_steps)
 
     if args.cpu_heads > 0:
         out["cpu_baseline"] = cpu_baseline(B, H, T, D, args.cpu_heads)
@@ -236,6 +239,30 @@ def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10
         "bwd_tflops": round(2.5 * F / (bwd_ms * 1e-3) / 1e12, 2),
         "fwd_bwd_tflops": round(tot, 2), "peak_tflops": peak, "frac": round(tot / peak, 4),
     }
+
+
+def bench_gpt(steps, warmup=2):
+    """Config 3: the GPT training step on the C++ drop-in (inferno_amd/gpt, a child process).
+
+    12 layers, d_model 768, 12 heads, ctx 1024, GELU MLP 4x, LayerNorm,
+    vocab 8192, tied embedding; weights N(0, 0.02), tokens uniform in
+    [0, 8192), targets shifted by one; batch 8; AdamW lr 3e-4.  A step is
+    forward + cross-entropy + backward + AdamW + zero_grad; tokens/s counts the
+    8192 tokens of a step.  The attention share is the fused attention
+    forward + backward of one layer timed alone, times 12, over the step time.
+    """
+    import subprocess
+
+    app = ROOT / "inferno_amd" / "gpt"
+    r = subprocess.run([str(app), "bench", "--steps", str(steps), "--warmup", str(warmup)],
+                       capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError(f"inferno_amd/gpt bench failed ({r.returncode}): {r.stderr[-2000:]}")
+    line = [l for l in r.stdout.splitlines() if l.startswith("{")][-1]
+    d = json.loads(line)
+    d["unit"] = "tokens/s"
+    d["dtype"] = "f32"
+    return d
 
 
 def bench_decode(ia, oracle, torch, np, dev, reps=50):
