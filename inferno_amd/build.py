@@ -48,7 +48,7 @@ def _compile(src: Path, obj: Path) -> None:
 HOST_LIB = PKG / "libinferno.so"
 CPP = PKG / "cpp"
 CPP_SOURCES = ["dtype.cpp", "storage.cpp", "hipctx.cpp", "tensor.cpp", "engine.cpp", "softmax.cpp", "attention.cpp",
-               "nn_ops.cpp", "modules.cpp"]
+               "nn_ops.cpp", "modules.cpp", "checkpoint.cpp"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 CXX = os.environ.get("CXX", "g++")
 # -ffp-contract=off: the CPU-device branches keep the reference's separate

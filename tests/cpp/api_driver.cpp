@@ -18,6 +18,8 @@
 //       writes y.bin dx.bin.
 //   api_driver decode <dir> <B> <H> <Tk> <D> <f32|bf16> <cpu|hip>
 //       reads q.bin kc.bin vc.bin, writes o.bin.
+//   api_driver ckpt-save|ckpt-load <file> <cpu|hip>
+//       Checkpoint round trips of a small module tree (see cmd_ckpt).
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -320,6 +322,56 @@ static int cmd_decode(int argc, char** argv) {
     return 0;
 }
 
+// ---------------------------------------------------------------- checkpoint
+// A small module tree: Linear(4, 3) "fc", LayerNorm(3) "norm", Embedding(5, 4)
+// "emb" in Float32 and a BFloat16 Linear(2, 2) "half", values fixed by seed.
+struct CkptNet : Module {
+    Linear fc;
+    LayerNorm norm;
+    Embedding emb;
+    Linear half;
+    explicit CkptNet(const Device& d)
+        : fc(4, 3, d), norm(3, 1e-5f, d), emb(5, 4, d), half(2, 2, d, DType::BFloat16) {
+        register_module("fc", &fc);
+        register_module("norm", &norm);
+        register_module("emb", &emb);
+        register_module("half", &half);
+    }
+};
+
+static void print_state(const StateDict& sd) {
+    for (const auto& [name, t] : sd) {
+        std::cout << name << " " << dtype_name(t.dtype());
+        for (double v : t.to_host_double()) std::cout << " " << v;
+        std::cout << "\n";
+    }
+}
+
+//   api_driver ckpt-save <file> <cpu|hip>: seeded CkptNet on the device -> file; prints the state
+//   api_driver ckpt-load <file> <cpu|hip>: file -> Checkpoint::load -> load_into a fresh CkptNet
+//                                          on the device; prints the module's state
+static int cmd_ckpt(int argc, char** argv) {
+    if (argc < 4) throw Error("usage: api_driver ckpt-save|ckpt-load <file> <cpu|hip>");
+    const std::string mode = argv[1], path = argv[2];
+    const Device dev = parse_dev(argv[3]);
+    if (mode == "ckpt-save") {
+        RandomGenerator::initializeWithSeed(123);
+        CkptNet net(dev);
+        Checkpoint c;
+        c.set_state_dict(net.state_dict());
+        c.save(path);
+        print_state(net.state_dict());
+    } else {
+        RandomGenerator::initializeWithSeed(999);
+        CkptNet net(dev);
+        Checkpoint c;
+        Checkpoint loaded = c.load(path);
+        Checkpoint::load_into(net, loaded.state_dict());
+        print_state(net.state_dict());
+    }
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc < 2) {
         std::cerr << "usage: api_driver selftest|attn|softmax|decode ...\n";
@@ -331,6 +383,7 @@ int main(int argc, char** argv) {
         if (cmd == "attn") return cmd_attn(argc, argv);
         if (cmd == "softmax") return cmd_softmax(argc, argv);
         if (cmd == "decode") return cmd_decode(argc, argv);
+        if (cmd == "ckpt-save" || cmd == "ckpt-load") return cmd_ckpt(argc, argv);
         std::cerr << "unknown command " << cmd << "\n";
         return 2;
     } catch (const std::exception& e) {
