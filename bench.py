@@ -198,6 +198,7 @@ def main():
         }
         torch.cuda.empty_cache()
         out["configs"]["c3_gpt"] = bench_gpt(args.gpt_steps)
+        out["configs"]["gpt_generate"] = bench_generate()
 
     if args.cpu_heads > 0:
         out["cpu_baseline"] = cpu_baseline(B, H, T, D, args.cpu_heads)
@@ -262,6 +263,25 @@ def bench_gpt(steps, warmup=2):
     d = json.loads(line)
     d["unit"] = "tokens/s"
     d["dtype"] = "f32"
+    return d
+
+
+def bench_generate(batch=32, prompt=1024, new=64):
+    """Greedy generation on the config-3 model with one KV cache per layer (inferno_amd/gpt generate).
+
+    Prefill of a random prompt, then `new` tokens one at a time through the
+    single-query decode kernel (the inference loop around BASELINE config 5's
+    kernel); reports the per-token step time of the whole 12-layer model.
+    """
+    import subprocess
+
+    app = ROOT / "inferno_amd" / "gpt"
+    r = subprocess.run([str(app), "generate", "--batch", str(batch), "--prompt", str(prompt), "--new", str(new),
+                        "--ctx", str(prompt + new)], capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError(f"inferno_amd/gpt generate failed ({r.returncode}): {r.stderr[-2000:]}")
+    d = json.loads([l for l in r.stdout.splitlines() if l.startswith("{")][-1])
+    d.pop("first_tokens", None)
     return d
 
 

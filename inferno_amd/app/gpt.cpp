@@ -14,6 +14,15 @@
 //       lr 3e-4; times K training steps (forward, cross-entropy, backward,
 //       AdamW, zero_grad) on hip:0 and prints one JSON line with tokens/s and
 //       the attention share of the step time.
+//   gpt generate [--layers L] [--dmodel C] [--heads H] [--vocab V] [--ctx T]
+//                [--batch B] [--prompt P] [--new N]
+//       greedy generation with one KV cache per layer on hip:0 (prefill of a
+//       random P-token prompt, then N tokens one at a time through the
+//       single-query decode kernel); prints one JSON line with the prefill
+//       time and the per-token decode time.
+//   gpt decode-check <dir> <cpu|hip> [--prefill P]
+//       full causal forward of tokens.bin vs incremental decoding (prefill of P
+//       tokens, then one at a time); writes logits_full.bin and logits_inc.bin.
 //   gpt step <dir> <cpu|hip> [--untied]
 //       reads config.txt ("L C H T V B"), tokens.bin / targets.bin (int32 [B, T])
 //       and one <state-dict name>.bin (fp32) per parameter from <dir>; runs one
@@ -21,6 +30,7 @@
 //       param_<name>.bin (after it).
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -52,10 +62,12 @@ public:
                     device);
         register_buffer("pe", &pe);
     }
-    Tensor forward(Tensor& x) override {
-        // x [B, T, C] + pe[:T]
+    Tensor forward(Tensor& x) override { return forward_at(x, 0); }
+    // x [B, t, C] holding positions pos0 .. pos0 + t - 1
+    Tensor forward_at(const Tensor& x, size_t pos0) {
         const size_t T = x.shape()[1];
-        Tensor p = T == pe.shape()[0] ? pe : pe.slice(0, 0, T - 1);
+        if (pos0 + T > pe.shape()[0]) throw Error("PositionalEncoding: position beyond the context size");
+        Tensor p = (pos0 == 0 && T == pe.shape()[0]) ? pe : pe.slice(0, pos0, pos0 + T - 1);
         return x + p;
     }
     Tensor pe;
@@ -85,6 +97,14 @@ public:
         Tensor ff = feedforward2.forward(static_cast<const Tensor&>(n));
         return h + ff;
     }
+    // Inference on the next positions with this layer's KV cache.
+    Tensor forward_cached(Tensor& x, KVCache& cache) {
+        Tensor normed = layernorm1.forward(x);
+        Tensor h = x + attn.forward_cached(normed, cache);
+        Tensor normed2 = layernorm2.forward(h);
+        Tensor n = gelu(feedforward1.forward(static_cast<const Tensor&>(normed2)));
+        return h + feedforward2.forward(static_cast<const Tensor&>(n));
+    }
     MultiHeadAttention attn;
     LayerNorm layernorm1, layernorm2;
     Linear feedforward1, feedforward2;
@@ -98,6 +118,8 @@ public:
           pos_enc(context_size, embed_dim, device),
           layernorm1(embed_dim, 1e-5f, device, dtype),
           m_tied(tied) {
+        m_heads = nheads;
+        m_embed = embed_dim;
         register_module("tok_embedding", &emb1);
         register_module("pos_encoding", &pos_enc);
         blocks.reserve(nblocks);
@@ -119,6 +141,24 @@ public:
         if (m_tied) return matmul(x, emb1.weight().transpose(0, 1), "logits");
         return linear1->forward(static_cast<const Tensor&>(x));
     }
+    // One KV cache per block, for up to `capacity` positions.
+    std::vector<KVCache> make_caches(size_t B, size_t capacity, const Device& dev) {
+        std::vector<KVCache> c;
+        for (size_t i = 0; i < blocks.size(); ++i) c.emplace_back(B, m_heads, capacity, m_embed / m_heads, dev);
+        return c;
+    }
+    // Logits [B, t, V] of the next t tokens [B, t], appending to the caches.
+    Tensor forward_cached(Tensor& tokens, std::vector<KVCache>& caches) {
+        NoGradGuard ng;
+        const size_t pos0 = caches.empty() ? 0 : caches[0].length;
+        Tensor x = emb1.forward(tokens);
+        x = pos_enc.forward_at(x, pos0);
+        for (size_t i = 0; i < blocks.size(); ++i) x = blocks[i]->forward_cached(x, caches[i]);
+        x = layernorm1.forward(x);
+        if (m_tied) return matmul(x, emb1.weight().transpose(0, 1), "logits");
+        return linear1->forward(static_cast<const Tensor&>(x));
+    }
+    size_t m_heads = 0, m_embed = 0;
     Embedding emb1;
     PositionalEncoding pos_enc;
     std::vector<std::unique_ptr<TransformerBlock>> blocks;
@@ -196,6 +236,128 @@ static int run_step(const std::string& dir, const Device& dev, bool tied) {
     for (auto& [name, t] : sd) write_f32(dir + "/param_" + name + ".bin", t.to_host_float());
     sync(dev);
     std::cout << "step ok: loss " << loss.to_host_float()[0] << "\n";
+    return 0;
+}
+
+// ------------------------------------------------------------- decode-check
+// Full causal forward of tokens [B, T] vs incremental decoding: prefill of the
+// first P tokens, then one token at a time through the KV caches.  Writes
+// logits_full.bin and logits_inc.bin ([B, T, V] fp32).
+static void load_params(GPTModel& model, const std::string& dir) {
+    StateDict sd = model.state_dict();
+    std::vector<Tensor*> params = model.parameters();
+    for (auto& [name, t] : sd) {
+        Tensor* target = nullptr;
+        for (Tensor* p : params)
+            if (GetImpl(*p) == GetImpl(t)) target = p;
+        if (!target) continue;
+        auto raw = read_file(dir + "/" + name + ".bin");
+        std::vector<float> v(raw.size() / 4);
+        std::memcpy(v.data(), raw.data(), v.size() * 4);
+        set_param(*target, v);
+    }
+}
+
+static int run_decode_check(const std::string& dir, const Device& dev, size_t P) {
+    std::ifstream cf(dir + "/config.txt");
+    size_t L, C, H, T, V, B;
+    if (!(cf >> L >> C >> H >> T >> V >> B)) throw Error("bad config.txt");
+    GPTModel model(V, T, C, H, L, true, dev, DType::Float32);
+    load_params(model, dir);
+    auto tok = read_file(dir + "/tokens.bin");
+    std::vector<int32_t> tv(B * T);
+    std::memcpy(tv.data(), tok.data(), tv.size() * 4);
+    Tensor x(DType::Int32, tv, std::vector<size_t>{B, T}, "tokens", dev);
+    {
+        NoGradGuard ng;
+        write_f32(dir + "/logits_full.bin", model.forward(x).to_host_float());
+    }
+    auto caches = model.make_caches(B, T, dev);
+    std::vector<float> inc(B * T * V);
+    auto put = [&](const Tensor& logits, size_t pos0) {
+        const size_t t = logits.shape()[1];
+        auto h = logits.to_host_float();
+        for (size_t b = 0; b < B; ++b)
+            for (size_t i = 0; i < t; ++i)
+                std::memcpy(&inc[(b * T + pos0 + i) * V], &h[(b * t + i) * V], V * 4);
+    };
+    std::vector<int32_t> chunk(B * P);
+    for (size_t b = 0; b < B; ++b)
+        for (size_t i = 0; i < P; ++i) chunk[b * P + i] = tv[b * T + i];
+    Tensor xp(DType::Int32, chunk, std::vector<size_t>{B, P}, "prompt", dev);
+    put(model.forward_cached(xp, caches), 0);
+    for (size_t pos = P; pos < T; ++pos) {
+        std::vector<int32_t> one(B);
+        for (size_t b = 0; b < B; ++b) one[b] = tv[b * T + pos];
+        Tensor x1(DType::Int32, one, std::vector<size_t>{B, 1}, "next", dev);
+        put(model.forward_cached(x1, caches), pos);
+    }
+    write_f32(dir + "/logits_inc.bin", inc);
+    sync(dev);
+    std::cout << "decode-check ok\n";
+    return 0;
+}
+
+// ----------------------------------------------------------------- generate
+// Greedy generation with KV caches on hip:0: a random prompt of P tokens per
+// sequence, then N new tokens, each fed back (argmax on the host).
+static size_t arg(int argc, char** argv, const char* name, size_t def);
+static void init_normal(Module& m, float stddev, const Device& dev);
+
+static int run_generate(int argc, char** argv) {
+    const size_t L = arg(argc, argv, "--layers", 12), C = arg(argc, argv, "--dmodel", 768),
+                 H = arg(argc, argv, "--heads", 12), V = arg(argc, argv, "--vocab", 8192),
+                 B = arg(argc, argv, "--batch", 8), P = arg(argc, argv, "--prompt", 512),
+                 N = arg(argc, argv, "--new", 64), T = arg(argc, argv, "--ctx", 1024);
+    if (P + N > T) throw Error("generate: prompt + new tokens exceed the context size");
+    const Device dev = Device::hip(0);
+    RandomGenerator::initializeWithSeed(42);
+    GPTModel model(V, T, C, H, L, true, dev, DType::Float32);
+    init_normal(model, 0.02f, dev);
+    std::mt19937_64 rng(42);
+    std::uniform_int_distribution<int> tokd(0, (int)V - 1);
+    std::vector<int32_t> prompt(B * P);
+    for (auto& t : prompt) t = tokd(rng);
+    auto argmax_last = [&](const Tensor& logits) {
+        // only the last position's logits leave the device ([B, V])
+        const size_t t = logits.shape()[1];
+        auto h = logits.slice(1, t - 1, t - 1).to_host_float();
+        std::vector<int32_t> nxt(B);
+        for (size_t b = 0; b < B; ++b) {
+            const float* row = &h[b * V];
+            nxt[b] = (int32_t)(std::max_element(row, row + V) - row);
+        }
+        return nxt;
+    };
+    auto run_once = [&](double* prefill_ms, double* decode_ms, std::vector<int32_t>* out) {
+        auto caches = model.make_caches(B, T, dev);
+        Tensor xp(DType::Int32, prompt, std::vector<size_t>{B, P}, "prompt", dev);
+        sync(dev);
+        const auto t0 = std::chrono::steady_clock::now();
+        std::vector<int32_t> nxt = argmax_last(model.forward_cached(xp, caches));
+        const auto t1 = std::chrono::steady_clock::now();
+        out->clear();
+        for (size_t i = 0; i < N; ++i) {
+            out->insert(out->end(), nxt.begin(), nxt.end());
+            if (i + 1 == N) break;
+            Tensor x1(DType::Int32, nxt, std::vector<size_t>{B, 1}, "next", dev);
+            nxt = argmax_last(model.forward_cached(x1, caches));
+        }
+        const auto t2 = std::chrono::steady_clock::now();
+        *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+        *decode_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
+    };
+    double pm = 0, dm = 0;
+    std::vector<int32_t> gen;
+    run_once(&pm, &dm, &gen);  // warm-up (plans, caches)
+    run_once(&pm, &dm, &gen);
+    const double steps = (double)(N - 1);
+    std::printf(
+        "{\"workload\": \"GPT greedy generation L%zu C%zu H%zu V%zu B%zu prompt %zu new %zu, KV cache\", "
+        "\"prefill_ms\": %.3f, \"decode_ms_per_token\": %.4f, \"decode_tokens_per_s\": %.1f, "
+        "\"first_tokens\": [%d, %d, %d]}\n",
+        L, C, H, V, B, P, N, pm, dm / steps, (double)B * steps / (dm * 1e-3), gen[0], gen.size() > 1 ? gen[1] : 0,
+        gen.size() > 2 ? gen[2] : 0);
     return 0;
 }
 
@@ -328,11 +490,17 @@ static int run_bench(int argc, char** argv) {
 int main(int argc, char** argv) {
     try {
         if (argc >= 2 && std::strcmp(argv[1], "bench") == 0) return run_bench(argc, argv);
+        if (argc >= 2 && std::strcmp(argv[1], "generate") == 0) return run_generate(argc, argv);
+        if (argc >= 4 && std::strcmp(argv[1], "decode-check") == 0) {
+            const Device dev = std::strcmp(argv[3], "hip") == 0 ? Device::hip(0) : Device::cpu();
+            return run_decode_check(argv[2], dev, arg(argc, argv, "--prefill", 4));
+        }
         if (argc >= 4 && std::strcmp(argv[1], "step") == 0) {
             const Device dev = std::strcmp(argv[3], "hip") == 0 ? Device::hip(0) : Device::cpu();
             return run_step(argv[2], dev, !flag(argc, argv, "--untied"));
         }
-        std::cerr << "usage: gpt bench [options] | gpt step <dir> <cpu|hip> [--untied]\n";
+        std::cerr << "usage: gpt bench [options] | gpt step <dir> <cpu|hip> [--untied] | gpt decode-check <dir> "
+                     "<cpu|hip> [--prefill P] | gpt generate [options]\n";
         return 2;
     } catch (const std::exception& e) {
         std::cerr << "error: " << e.what() << "\n";

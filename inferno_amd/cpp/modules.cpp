@@ -19,6 +19,7 @@
 #include "inferno/modules/multiheadattention.h"
 #include "inferno/optim/adamw.h"
 #include "inferno/util/random.h"
+#include "inferno/functional/attention.h"
 
 namespace Inferno {
 
@@ -183,6 +184,57 @@ Tensor MultiHeadAttention::forward(Tensor& x) {
     if (x.shape()[2] != m_embed_dim) throw Error("MultiHeadAttention: embed_dim mismatch");
     Tensor qkv = Wqkv_layer.forward(static_cast<const Tensor&>(x));  // [B, T, 3C]
     Tensor y = qkv_attention(qkv, m_num_heads, true);                  // [B, T, C]
+    return W_out.forward(static_cast<const Tensor&>(y));
+}
+
+KVCache::KVCache(size_t B, size_t H, size_t capacity, size_t D, Device device, DType dtype)
+    : k(dtype, std::vector<size_t>{B, H, capacity, D}, "kv_cache_k", device, false),
+      v(dtype, std::vector<size_t>{B, H, capacity, D}, "kv_cache_v", device, false) {}
+
+namespace {
+// dst (a view) = src (a view of the same shape), element-wise through strides.
+void copy_view(const Tensor& src, Tensor& dst) {
+    if (src.shape() != dst.shape() || src.dtype() != dst.dtype()) throw Error("copy_view: shape or dtype mismatch");
+    const size_t esz = dtype_size(src.dtype());
+    if (src.device().is_cpu()) {
+        detail::copy_strided_host(static_cast<const char*>(src.data_ptr()), src.strides(),
+                                  static_cast<char*>(dst.data_ptr()), dst.strides(), src.shape(), esz);
+        return;
+    }
+    auto shape = detail::to_i64(src.shape());
+    auto ss = detail::to_i64(src.strides());
+    auto ds = detail::to_i64(dst.strides());
+    detail::DeviceGuard g(src.device().index);
+    detail::status_check(inf_copy_strided(src.data_ptr(), ss.data(), dst.data_ptr(), ds.data(), (int)src.ndim(),
+                                          shape.data(), (int)esz, detail::stream_of(src)),
+                         "inf_copy_strided");
+}
+}  // namespace
+
+Tensor MultiHeadAttention::forward_cached(const Tensor& x, KVCache& cache) {
+    NoGradGuard ng;
+    if (x.ndim() != 3 || x.shape()[2] != m_embed_dim) throw Error("MultiHeadAttention: expects [B, t, C]");
+    const size_t B = x.shape()[0], t = x.shape()[1], C = m_embed_dim, H = m_num_heads, D = m_head_dim;
+    if (!cache.k.defined() || cache.k.shape()[0] != B || cache.k.shape()[1] != H || cache.k.shape()[3] != D)
+        throw Error("MultiHeadAttention: KV cache shape does not match [B, H, capacity, D]");
+    if (cache.length + t > cache.capacity()) throw Error("MultiHeadAttention: KV cache is full");
+    if (cache.k.device() != x.device()) throw Error("MultiHeadAttention: KV cache is on another device");
+    Tensor qkv = Wqkv_layer.forward(x).contiguous();  // [B, t, 3C]
+    const std::vector<size_t> hs{B, H, t, D};
+    const std::vector<size_t> hst{t * 3 * C, D, 3 * C, 1};
+    Tensor q = make_view(qkv, hs, hst, qkv.offset(), "q");
+    Tensor knew = make_view(qkv, hs, hst, qkv.offset() + C, "k_new");
+    Tensor vnew = make_view(qkv, hs, hst, qkv.offset() + 2 * C, "v_new");
+    Tensor kdst = make_view(cache.k, hs, cache.k.strides(), cache.k.offset() + cache.length * D, "k_slot");
+    Tensor vdst = make_view(cache.v, hs, cache.v.strides(), cache.v.offset() + cache.length * D, "v_slot");
+    copy_view(knew, kdst);
+    copy_view(vnew, vdst);
+    cache.length += t;
+    const std::vector<size_t> all{B, H, cache.length, D};
+    Tensor kall = make_view(cache.k, all, cache.k.strides(), cache.k.offset(), "k_cache");
+    Tensor vall = make_view(cache.v, all, cache.v.strides(), cache.v.offset(), "v_cache");
+    Tensor y4 = t == 1 ? attention_decode(q, kall, vall) : scaled_dot_product_attention(q, kall, vall, true);
+    Tensor y = y4.transpose(1, 2).contiguous().reshape({B, t, C});
     return W_out.forward(static_cast<const Tensor&>(y));
 }
 
