@@ -13,11 +13,28 @@
 
 namespace Inferno {
 
+// Keys and values of one attention layer for incremental decoding: [B, H,
+// capacity, D] device buffers and the number of positions filled.  No
+// reference counterpart (the reference has no generation loop; see the
+// commented-out last-position select, InfernoApp/main.cpp:1173-1177).
+struct KVCache {
+    Tensor k, v;
+    size_t length = 0;
+    KVCache() = default;
+    KVCache(size_t B, size_t H, size_t capacity, size_t D, Device device, DType dtype = DType::Float32);
+    size_t capacity() const { return k.defined() ? k.shape()[2] : 0; }
+};
+
 class MultiHeadAttention : public Module {
 public:
     MultiHeadAttention(size_t embed_dim, size_t num_heads, Device device = Device::cpu(),
                        DType dtype = DType::Float32);
     Tensor forward(Tensor& x) override;  // x [B, T, C] -> [B, T, C]
+    // Inference with a cache: x [B, t, C] holds the next t positions; their keys
+    // and values are appended to `cache` and each attends causally to every
+    // cached position before it (t == 1: the single-query decode kernel; t > 1:
+    // the causal kernel with Tq = t < Tk).  No graph is recorded.
+    Tensor forward_cached(const Tensor& x, KVCache& cache);
     Linear& qkv_proj() { return Wqkv_layer; }
     Linear& out_proj() { return W_out; }
 
