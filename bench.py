@@ -117,10 +117,12 @@ def main():
     dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
     ws = torch.empty(max(ia.workspace_bytes(ia.OP_ATTN_BWD, B, H, T, T, D, ia.ops._dt(Q)), 1),
                      dtype=torch.uint8, device=dev)
+    fws = torch.empty(max(ia.workspace_bytes(ia.OP_ATTN_FWD, B, H, T, T, D, ia.ops._dt(Q)), 1),
+                      dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
 
     def step():
-        ia.attn_fwd(Q, K, V, out=O, lse=LSE, stream=stream)
+        ia.attn_fwd(Q, K, V, out=O, lse=LSE, workspace=fws, stream=stream)
         ia.attn_bwd(Q, K, V, O, dO, LSE, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
 
     for _ in range(args.warmup):
@@ -132,7 +134,7 @@ def main():
     t0 = time.perf_counter()
     for i in range(args.steps):
         ev[i][0].record(stream)
-        ia.attn_fwd(Q, K, V, out=O, lse=LSE, stream=stream)
+        ia.attn_fwd(Q, K, V, out=O, lse=LSE, workspace=fws, stream=stream)
         ev[i][1].record(stream)
         ia.attn_bwd(Q, K, V, O, dO, LSE, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
         ev[i][2].record(stream)
@@ -189,7 +191,7 @@ def main():
     if not args.no_decode:
         out["decode"] = bench_decode(ia, oracle, torch, np, dev)
     if not args.no_extras:
-        del Q, K, V, dO, O, dQ, dK, dV, ws
+        del Q, K, V, dO, O, dQ, dK, dV, ws, fws
         torch.cuda.empty_cache()
         out["configs"] = {
             "c2_bf16": bench_attn(ia, oracle, torch, np, dev, 8, 12, 1024, 64, 1.0, "bf16"),
@@ -216,12 +218,14 @@ def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10
     dQ, dK, dV = torch.empty_like(Q), torch.empty_like(K), torch.empty_like(V)
     ws = torch.empty(max(ia.workspace_bytes(ia.OP_ATTN_BWD, B, H, T, T, D, ia.ops._dt(Q)), 1),
                      dtype=torch.uint8, device=dev)
+    fws = torch.empty(max(ia.workspace_bytes(ia.OP_ATTN_FWD, B, H, T, T, D, ia.ops._dt(Q)), 1),
+                      dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     evs = []
     for i in range(warmup + steps):
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         e[0].record(stream)
-        ia.attn_fwd(Q, K, V, out=O, lse=LSE, stream=stream)
+        ia.attn_fwd(Q, K, V, out=O, lse=LSE, workspace=fws, stream=stream)
         e[1].record(stream)
         ia.attn_bwd(Q, K, V, O, dO, LSE, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
         e[2].record(stream)

@@ -69,7 +69,10 @@ const char* inf_last_error_detail(void);
 /* Library ABI version (major*10000 + minor*100 + patch). */
 int inf_version(void);
 
-/* Bytes of workspace an op needs for this shape (0 when none). */
+/* Bytes of workspace an op needs for this shape (0 when none) on the current
+ * device.  INF_OP_ATTN_FWD reports what a causal call needs (a non-causal
+ * forward needs none); the size depends on the device's CU count, so query it
+ * with the device that will run the call current. */
 int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dtype dt,
                              size_t* out_bytes);
 
@@ -80,10 +83,15 @@ int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dt
  * Replaces the chain matmul -> multiply -> triu/masked_fill -> Softmax ->
  * matmul of InfernoApp/main.cpp:737-754 (ops.cpp:437, ops.cpp:204,
  * ops.cpp:1235, softmax.cpp:22).  scale must be finite and > 0.
+ * workspace: inf_attn_workspace_bytes(INF_OP_ATTN_FWD, ...) bytes, 256-byte
+ * aligned, holding the partial results of query tiles whose key range is split
+ * across workgroups (may be NULL when that size is 0); its contents on entry
+ * do not matter.
  */
 int inf_attn_fwd(const void* q, inf_strides sq, const void* k, inf_strides sk, const void* v,
-                 inf_strides sv, void* o, inf_strides so, float* lse, int B, int H, int Tq,
-                 int Tk, int D, float scale, int causal, inf_dtype dt, void* stream);
+                 inf_strides sv, void* o, inf_strides so, float* lse, void* workspace,
+                 size_t ws_bytes, int B, int H, int Tq, int Tk, int D, float scale, int causal,
+                 inf_dtype dt, void* stream);
 
 /*
  * Fused causal attention backward (recompute from q, k, v, o, lse): writes

@@ -95,7 +95,7 @@ def lib() -> ctypes.CDLL:
         L.inf_version.restype = i32
         L.inf_attn_workspace_bytes.argtypes = [i32, i32, i32, i32, i32, i32, i32, ctypes.POINTER(ctypes.c_size_t)]
         L.inf_attn_workspace_bytes.restype = i32
-        L.inf_attn_fwd.argtypes = [vp, S, vp, S, vp, S, vp, S, vp, i32, i32, i32, i32, i32, f32, i32, i32, vp]
+        L.inf_attn_fwd.argtypes = [vp, S, vp, S, vp, S, vp, S, vp, vp, ctypes.c_size_t, i32, i32, i32, i32, i32, f32, i32, i32, vp]
         L.inf_attn_fwd.restype = i32
         L.inf_attn_bwd.argtypes = [vp, S, vp, S, vp, S, vp, S, vp, S, vp, vp, S, vp, S, vp, S, vp,
                                    ctypes.c_size_t, i32, i32, i32, i32, i32, f32, i32, i32, vp]

@@ -228,11 +228,18 @@ Tensor scaled_dot_product_attention_lse(const Tensor& q, const Tensor& k, const 
         } else {
             Tensor qa = abi_view(q), ka = abi_view(k), va = abi_view(v);
             detail::DeviceGuard g(q.device().index);
+            const inf_dtype dt = detail::inf_dt(q.dtype(), "scaled_dot_product_attention");
+            size_t ws_bytes = 0;
+            if (causal)
+                detail::status_check(inf_attn_workspace_bytes(INF_OP_ATTN_FWD, (int)s.B, (int)s.H, (int)s.Tq,
+                                                              (int)s.Tk, (int)s.D, dt, &ws_bytes),
+                                     "inf_attn_workspace_bytes");
+            Workspace ws(ws_bytes, q.device());
             detail::status_check(
                 inf_attn_fwd(qa.data_ptr(), strides_of(qa), ka.data_ptr(), strides_of(ka), va.data_ptr(), strides_of(va),
-                             out.data_ptr(), strides_of(out), static_cast<float*>(lse.data_ptr()), (int)s.B, (int)s.H,
-                             (int)s.Tq, (int)s.Tk, (int)s.D, sc, causal ? 1 : 0,
-                             detail::inf_dt(q.dtype(), "scaled_dot_product_attention"), detail::stream_of(q)),
+                             out.data_ptr(), strides_of(out), static_cast<float*>(lse.data_ptr()), ws.ptr, ws_bytes,
+                             (int)s.B, (int)s.H, (int)s.Tq, (int)s.Tk, (int)s.D, sc, causal ? 1 : 0, dt,
+                             detail::stream_of(q)),
                 "inf_attn_fwd");
         }
     }

@@ -822,10 +822,16 @@ Tensor qkv_attention(const Tensor& qkv, size_t num_heads, bool causal, float sca
         const char* base = static_cast<const char*>(in.data_ptr());
         const inf_strides sv = head_view(in, s.D), so = head_view(y, s.D);
         DeviceGuard dg(qkv.device().index);
+        const inf_dtype dt = detail::inf_dt(qkv.dtype(), "qkv_attention");
+        size_t wsb = 0;
+        if (causal)
+            status_check(inf_attn_workspace_bytes(INF_OP_ATTN_FWD, (int)s.B, (int)s.H, (int)s.T, (int)s.T, (int)s.D,
+                                                  dt, &wsb),
+                         "inf_attn_workspace_bytes");
+        Scratch ws(wsb, qkv.device());
         status_check(inf_attn_fwd(base, sv, base + s.C * esz, sv, base + 2 * s.C * esz, sv, y.data_ptr(), so,
-                                  static_cast<float*>(lse.data_ptr()), (int)s.B, (int)s.H, (int)s.T, (int)s.T,
-                                  (int)s.D, sc, causal ? 1 : 0, detail::inf_dt(qkv.dtype(), "qkv_attention"),
-                                  detail::stream_of(qkv)),
+                                  static_cast<float*>(lse.data_ptr()), ws.ptr, wsb, (int)s.B, (int)s.H, (int)s.T,
+                                  (int)s.T, (int)s.D, sc, causal ? 1 : 0, dt, detail::stream_of(qkv)),
                      "inf_attn_fwd");
     }
     if (grad_enabled && qkv.requires_grad()) {

@@ -28,10 +28,23 @@
 // -1e9f fill followed by exp((double)(-1e9 - max)) is.  The row
 // log-sum-exp (natural log) is stored for the backward pass.
 //
-// Scheduling: workgroup w takes query tile (n_qtiles - 1 - w / (B*H)) of head
-// w % (B*H), so the longest causal rows start first; when B*H is a multiple
-// of 8, all tiles of a head land on the same XCD (dispatch is round-robin
-// over the 8 XCDs), so a head's K/V is fetched into one L2.
+// Scheduling: dispatch group g = w / (B*H) of head w % (B*H).  Without a
+// split plan, group g is query tile n_qtiles - 1 - g, so the longest causal
+// rows start first; when B*H is a multiple of 8, all tiles of a head land on
+// the same XCD (dispatch is round-robin over the 8 XCDs), so a head's K/V is
+// fetched into one L2.  With a split plan (fwd_plan, causal shapes whose
+// heaviest query tiles would otherwise set the makespan), the heaviest query
+// tiles' key ranges are cut into chunks run by separate groups, the groups are
+// ordered heaviest first, and each chunk leaves (unnormalised O, row max, row
+// sum) in a workspace slot that attn_fwd_merge_kernel combines with the same
+// log-sum-exp weighting as the decode combine.
+#include <algorithm>
+#include <array>
+#include <functional>
+#include <map>
+#include <mutex>
+#include <vector>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -67,7 +80,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
 
     const int BH = p.B * p.H;
     const int w = blockIdx.x;
-    const int qtile = p.n_qtiles - 1 - w / BH;
+    int qtile, t_begin = 0, t_end = 0x7fffffff, slot = -1;
+    if (p.n_groups) {
+        const FwdGroup grp = p.groups[w / BH];
+        qtile = grp.qt;
+        t_begin = grp.t0;
+        t_end = grp.t1;
+        slot = grp.slot;
+    } else {
+        qtile = p.n_qtiles - 1 - w / BH;
+    }
     const int bh = w % BH;
     const int b = bh / p.H;
     const int h = bh % p.H;
@@ -100,7 +122,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
     // Keys this workgroup needs, and this wave's visible limit (exclusive).
     int kv_end = p.Tk;
     if (p.causal) kv_end = min(p.Tk, qtile * BM + BM + p.off);
-    const int n_tiles = (kv_end + BN - 1) / BN;
+    const int n_tiles = min((kv_end + BN - 1) / BN, t_end);
     const int wave_kend = p.causal ? min(kv_end, q0w + 32 + p.off) : kv_end;
 
     // K: chunk f -> (row f / C4, column chunk f % C4), row-major 16-byte loads.
@@ -139,12 +161,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
     float l_run = 0.f;        // this lane's partial sum of p (its half of the keys)
     const float c = p.c;
 
-    gload(0);
+    gload(t_begin);  // bounds-checked rows: safe even past the last tile
     sstore(0);
     __syncthreads();
 
-    for (int t = 0; t < n_tiles; ++t) {
-        const int buf = t & 1;
+    for (int t = t_begin; t < n_tiles; ++t) {
+        const int buf = (t - t_begin) & 1;
         const int k0 = t * BN;
         if (t + 1 < n_tiles) gload(t + 1);
 
@@ -186,8 +208,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
                 for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kb][r]);
             mloc = fmaxf(mloc, shfl_xor(mloc, 32));
             const float m_new = fmaxf(m_run, mloc);
-            const float alpha = fast_exp2((m_run - m_new) * c);  // m_run = -inf -> 0
-            const float mc = m_new * c;
+            // A row can see no key of a chunk that does not start at key 0:
+            // keep m = -inf, l = 0, O = 0 for it instead of exp2(NaN).
+            const bool row_dead = m_new == -INFINITY;
+            const float alpha = row_dead ? 1.f : fast_exp2((m_run - m_new) * c);  // m_run = -inf -> 0
+            const float mc = row_dead ? 0.f : m_new * c;
             float lsum = 0.f;
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
@@ -227,6 +252,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
 
     // ---- epilogue ---------------------------------------------------------------
     const float l_tot = l_run + shfl_xor(l_run, 32);
+    if (slot >= 0) {
+        // partial of a split query tile: unnormalised O, row max, row sum
+        if (qrow < p.Tq) {
+            const int r = wave * 32 + l32;
+            float* po = p.part + ((int64_t)slot * BH + bh) * (BM * D) + (int64_t)r * D;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    st4(po + db * 32 + 8 * j + 4 * g,
+                        f32x4{o[db][4 * j + 0], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]});
+            if (g == 0) {
+                float* pml = p.part + (int64_t)p.n_slots * BH * BM * D + (((int64_t)slot * BH + bh) * BM + r) * 2;
+                pml[0] = m_run;
+                pml[1] = l_tot;
+            }
+        }
+        return;
+    }
     const float inv = 1.f / l_tot;
     if (qrow < p.Tq) {
         E* dst = O + (int64_t)qrow * p.so.t;
@@ -245,11 +289,232 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
     }
 }
 
+// Combines the partial slots of each split query tile: per row
+// M = max_s m_s, w_s = exp2((m_s - M) c), O = sum_s w_s O_s / sum_s w_s l_s,
+// LSE = M * scale + ln(sum_s w_s l_s).  One thread per (row, 4 columns).
+template <int D, typename E>
+__global__ __launch_bounds__(256) void attn_fwd_merge_kernel(FwdParams p) {
+    constexpr int BM = kFwdBM;
+    constexpr int C4 = D / 4;
+    constexpr int TPT = BM * C4;  // threads per (split tile, head)
+    const int BH = p.B * p.H;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t unit = gid / TPT;  // (split tile, head)
+    if (unit >= (int64_t)p.n_split * BH) return;
+    const int si = (int)(unit / BH);
+    const int bh = (int)(unit % BH);
+    const int rem = (int)(gid % TPT);
+    const int r = rem / C4;
+    const int c4 = rem % C4;
+    const int qrow = p.split_qt[si] * BM + r;
+    if (qrow >= p.Tq) return;
+    const int s0 = p.split_slot0[si], ns = p.split_count[si];
+    const float* ml = p.part + (int64_t)p.n_slots * BH * BM * D;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, ml[(((int64_t)(s0 + s) * BH + bh) * BM + r) * 2]);
+    float L = 0.f;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < ns; ++s) {
+        const int64_t base = ((int64_t)(s0 + s) * BH + bh) * BM + r;
+        const float m = ml[base * 2];
+        if (m == -INFINITY) continue;
+        const float wgt = fast_exp2((m - M) * p.c);
+        L = fmaf(ml[base * 2 + 1], wgt, L);
+        const f32x4 v = *reinterpret_cast<const f32x4*>(p.part + base * D + 4 * c4);
+        acc[0] = fmaf(v[0], wgt, acc[0]);
+        acc[1] = fmaf(v[1], wgt, acc[1]);
+        acc[2] = fmaf(v[2], wgt, acc[2]);
+        acc[3] = fmaf(v[3], wgt, acc[3]);
+    }
+    const float inv = 1.f / L;
+    const int b = bh / p.H, h = bh % p.H;
+    E* dst = (E*)p.o + b * p.so.b + h * p.so.h + (int64_t)qrow * p.so.t + 4 * c4;
+    st4(dst, f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv});
+    if (c4 == 0 && p.lse) p.lse[(int64_t)bh * p.Tq + qrow] = M * p.scale + logf(L);
+}
+
 template <int D, typename E>
 static int launch_fwd_t(const FwdParams& p, hipStream_t s) {
-    const dim3 grid((unsigned)(p.n_qtiles * p.B * p.H));
+    const int BH = p.B * p.H;
+    const dim3 grid((unsigned)((p.n_groups ? p.n_groups : p.n_qtiles) * BH));
     hipLaunchKernelGGL((attn_fwd_kernel<D, E>), grid, dim3(256), 0, s, p);
+    if (p.n_split) {
+        const int64_t threads = (int64_t)p.n_split * BH * kFwdBM * (D / 4);
+        hipLaunchKernelGGL((attn_fwd_merge_kernel<D, E>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                           p);
+    }
     return (int)hipGetLastError();
+}
+
+// ---- split plan ----------------------------------------------------------------
+// Makespan of a dispatch order on the device: workgroup w goes to XCD w % 8,
+// and inside an XCD each workgroup starts on the slot that frees first (slots =
+// resident workgroups).  Costs are in key tiles plus a fixed per-workgroup
+// overhead (Q load, first K/V tile not hidden behind compute, epilogue).
+static double fwd_makespan(const int* cost, int n_groups, int BH, int slots_per_xcd, double overhead) {
+    double worst = 0.0;
+    std::vector<double> heap((size_t)slots_per_xcd);
+    for (int x = 0; x < 8; ++x) {
+        std::fill(heap.begin(), heap.end(), 0.0);  // min-heap of slot free times
+        int64_t w = 0;
+        for (int gi = 0; gi < n_groups; ++gi)
+            for (int i = 0; i < BH; ++i, ++w) {
+                if (w % 8 != x) continue;
+                std::pop_heap(heap.begin(), heap.end(), std::greater<double>());
+                heap.back() += cost[gi] + overhead;
+                std::push_heap(heap.begin(), heap.end(), std::greater<double>());
+            }
+        worst = std::max(worst, *std::max_element(heap.begin(), heap.end()));
+    }
+    return worst;
+}
+
+// Resident forward workgroups per XCD on the current device (8 XCDs).
+static int fwd_slots_per_xcd(int D) {
+    static std::mutex mu;
+    static std::map<std::pair<int, int>, int> cache;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        dev = -1;
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find({dev, D});
+    if (it != cache.end()) return it->second;
+    // MI355X: 256 CUs; LDS holds two D<=64 workgroups per CU, one at D = 128.
+    int cus = 256, per_cu = D >= 128 ? 1 : 2;
+    if (dev >= 0) {
+        int n = 0, occ = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
+        hipError_t e = hipErrorInvalidValue;
+        if (D == 32) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<32, float>, 256, 0);
+        if (D == 64) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<64, float>, 256, 0);
+        if (D == 128) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<128, float>, 256, 0);
+        if (e == hipSuccess && occ > 0) per_cu = occ;
+        (void)hipGetLastError();
+    }
+    const int slots = std::max(1, cus * per_cu / 8);
+    cache[{dev, D}] = slots;
+    return slots;
+}
+
+// Causal forward split plan.  Without a split the query tiles run heaviest
+// first, one workgroup per (tile, head).  When the whole grid fits in the
+// resident slots at once, the heaviest tile alone sets the kernel time (1.9x
+// to 3.2x measured at B1 H2 T8192 D128 and B1 H4 T2048 D128), so its key range
+// is cut.  With more workgroups than slots the tail balances itself (a
+// workgroup left alone on a CU runs faster), and at B8 H12 T1024 D64 a split
+// made the forward 4% slower, merge pass included: such grids never split.
+// Each candidate chunk length CH cuts every tile with more than CH key tiles
+// into ceil(n / CH) near-equal chunks; the candidate with the smallest
+// simulated makespan (plus the merge pass) wins if it beats the unsplit order
+// by more than 2%.
+static constexpr double kFwdOverhead = 0.35;  // per-workgroup fixed cost, in key tiles
+static constexpr double kFwdMergeCost = 0.5;  // merge kernel, in key tiles
+
+static void fwd_plan_compute(int B, int H, int Tq, int Tk, int D, int slots_per_xcd, FwdPlan* out) {
+    const int BM = kFwdBM, BN = D >= 128 ? FwdTile<128>::BN : FwdTile<64>::BN;
+    const int nq = (Tq + BM - 1) / BM;
+    const int BH = B * H;
+    const int off = Tk - Tq;
+    if ((int64_t)nq * BH > 8LL * slots_per_xcd) return;
+    std::vector<int> nt((size_t)nq);
+    int max_nt = 0;
+    for (int q = 0; q < nq; ++q) {
+        const int kend = std::min(Tk, (q + 1) * BM + off);
+        nt[(size_t)q] = std::max(0, (kend + BN - 1) / BN);
+        max_nt = std::max(max_nt, nt[(size_t)q]);
+    }
+    std::vector<int> cost;
+    for (int q = nq - 1; q >= 0; --q) cost.push_back(nt[(size_t)q]);
+    const double base = fwd_makespan(cost.data(), nq, BH, slots_per_xcd, kFwdOverhead);
+    double best = base * 0.98;
+    int best_ch = 0;
+    struct G { int n, qt, t0, t1; };
+    auto build = [&](int ch, std::vector<G>& g, int& n_split) {
+        g.clear();
+        n_split = 0;
+        for (int q = 0; q < nq; ++q) {
+            const int n = nt[(size_t)q];
+            if (n > ch) {
+                const int k = (n + ch - 1) / ch;
+                ++n_split;
+                for (int j = 0; j < k; ++j) {
+                    const int a = (int)((int64_t)n * j / k), b = (int)((int64_t)n * (j + 1) / k);
+                    g.push_back({b - a, q, a, b});
+                }
+            } else {
+                g.push_back({n, q, 0, n});
+            }
+        }
+        std::stable_sort(g.begin(), g.end(), [](const G& x, const G& y) {
+            return x.n != y.n ? x.n > y.n : x.qt > y.qt;
+        });
+    };
+    std::vector<G> g;
+    for (int ch = max_nt - 1; ch >= std::max(2, max_nt / 8); --ch) {
+        int n_split = 0;
+        build(ch, g, n_split);
+        if ((int)g.size() > kMaxFwdGroups || n_split > kMaxFwdGroups / 2) continue;
+        cost.resize(g.size());
+        for (size_t i = 0; i < g.size(); ++i) cost[i] = g[i].n;
+        const double ms = fwd_makespan(cost.data(), (int)g.size(), BH, slots_per_xcd, kFwdOverhead) + kFwdMergeCost;
+        if (ms < best) {
+            best = ms;
+            best_ch = ch;
+        }
+    }
+    if (!best_ch) return;
+    int n_split = 0;
+    build(best_ch, g, n_split);
+    // slots: consecutive per split tile, in query-tile order
+    std::vector<int> slot0((size_t)nq, -1), count((size_t)nq, 0);
+    for (const G& x : g)
+        if (x.t1 - x.t0 < nt[(size_t)x.qt]) ++count[(size_t)x.qt];
+    int ns = 0;
+    for (int q = 0; q < nq; ++q)
+        if (count[(size_t)q]) {
+            slot0[(size_t)q] = ns;
+            out->split_qt[out->n_split] = q;
+            out->split_slot0[out->n_split] = ns;
+            out->split_count[out->n_split] = count[(size_t)q];
+            ++out->n_split;
+            ns += count[(size_t)q];
+        }
+    std::vector<int> next((size_t)nq, 0);
+    for (const G& x : g) {
+        FwdGroup& o = out->groups[out->n_groups++];
+        o.qt = x.qt;
+        o.t0 = x.t0;
+        o.t1 = x.t1;
+        o.slot = count[(size_t)x.qt] ? slot0[(size_t)x.qt] + next[(size_t)x.qt]++ : -1;
+    }
+    out->n_slots = ns;
+}
+
+void fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan* out) {
+    *out = FwdPlan{};
+    if (bf16 || !causal || (D != 32 && D != 64 && D != 128)) return;
+    const int slots = fwd_slots_per_xcd(D);
+    static std::mutex mu;
+    static std::map<std::array<int, 5>, FwdPlan> cache;
+    const std::array<int, 5> key{B * H, Tq, Tk, D, slots};
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        auto it = cache.find(key);
+        if (it != cache.end()) {
+            *out = it->second;
+            return;
+        }
+    }
+    fwd_plan_compute(B, H, Tq, Tk, D, slots, out);
+    std::lock_guard<std::mutex> lk(mu);
+    if (cache.size() > 256) cache.clear();
+    cache[key] = *out;
+}
+
+size_t fwd_workspace_bytes(const FwdPlan& plan, int B, int H, int D) {
+    return (size_t)plan.n_slots * B * H * kFwdBM * (size_t)(D + 2) * sizeof(float);
 }
 
 int launch_attn_fwd(const FwdParams& p, int bf16, hipStream_t s) {

@@ -9,6 +9,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstring>
 #include <string>
 
 #include "kernels.h"
@@ -80,7 +81,7 @@ const char* inf_status_string(int status) {
     }
 }
 
-int inf_version(void) { return 100; }
+int inf_version(void) { return 200; }
 
 int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dtype dt,
                              size_t* out_bytes) {
@@ -91,7 +92,12 @@ int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dt
     if (st != INF_OK) return st;
     const size_t bh = (size_t)B * H;
     switch (op) {
-        case INF_OP_ATTN_FWD: *out_bytes = 0; return INF_OK;
+        case INF_OP_ATTN_FWD: {
+            inf::FwdPlan plan;
+            inf::fwd_plan(B, H, Tq, Tk, D, 1, dt == INF_BF16, &plan);
+            *out_bytes = round_up(inf::fwd_workspace_bytes(plan, B, H, D));
+            return INF_OK;
+        }
         case INF_OP_ATTN_BWD: {
             size_t n = round_up(bh * Tq * sizeof(float));                       // delta
             if (dt == INF_BF16) n += round_up(bh * Tq * (size_t)D * sizeof(float));  // dQ accumulator
@@ -109,8 +115,9 @@ int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dt
 }
 
 int inf_attn_fwd(const void* q, inf_strides sq, const void* k, inf_strides sk, const void* v,
-                 inf_strides sv, void* o, inf_strides so, float* lse, int B, int H, int Tq,
-                 int Tk, int D, float scale, int causal, inf_dtype dt, void* stream) {
+                 inf_strides sv, void* o, inf_strides so, float* lse, void* workspace,
+                 size_t ws_bytes, int B, int H, int Tq, int Tk, int D, float scale, int causal,
+                 inf_dtype dt, void* stream) {
     int st = common_shape(B, H, Tq, Tk, D, scale, dt);
     if (st != INF_OK) return st;
     if (causal && Tq > Tk) return INF_ERR_BAD_SHAPE;
@@ -126,6 +133,21 @@ int inf_attn_fwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     p.scale = scale;
     p.c = scale * 1.4426950408889634f;
     p.n_qtiles = (Tq + inf::kFwdBM - 1) / inf::kFwdBM;
+    inf::FwdPlan plan;
+    inf::fwd_plan(B, H, Tq, Tk, D, p.causal, dt == INF_BF16, &plan);
+    const size_t need = inf::fwd_workspace_bytes(plan, B, H, D);
+    if (need && (!workspace || ws_bytes < need)) return INF_ERR_WORKSPACE;
+    if (need && reinterpret_cast<uintptr_t>(workspace) % kAlign) return INF_ERR_ALIGNMENT;
+    if (plan.n_groups) {
+        p.n_groups = plan.n_groups;
+        p.n_slots = plan.n_slots;
+        p.n_split = plan.n_split;
+        p.part = static_cast<float*>(workspace);
+        std::memcpy(p.groups, plan.groups, sizeof(p.groups));
+        std::memcpy(p.split_qt, plan.split_qt, sizeof(p.split_qt));
+        std::memcpy(p.split_slot0, plan.split_slot0, sizeof(p.split_slot0));
+        std::memcpy(p.split_count, plan.split_count, sizeof(p.split_count));
+    }
     return hip_status(inf::launch_attn_fwd(p, dt == INF_BF16, (hipStream_t)stream));
 }
 

@@ -13,6 +13,16 @@ struct View4 {            // element strides of a [B,H,T,D] view, d stride 1
     int64_t b, h, t;
 };
 
+// Work split of the forward: dispatch group g (grid blocks [g*B*H, (g+1)*B*H),
+// one per head) runs query tile `qt` over key tiles [t0, t1).  slot < 0: the
+// group covers the tile's whole key range and writes O / LSE; slot >= 0: it
+// writes partials (unnormalised O, row max, row sum) to partial slot `slot`
+// and attn_fwd_merge_kernel combines the slots of that query tile.
+constexpr int kMaxFwdGroups = 96;
+struct FwdGroup {
+    int qt, t0, t1, slot;
+};
+
 struct FwdParams {
     const void* q;
     const void* k;
@@ -26,7 +36,24 @@ struct FwdParams {
     float scale;          // softmax scale
     float c;              // scale * log2(e)
     int n_qtiles;
+    int n_groups;         // 0: one group per query tile, heaviest first (no split)
+    int n_slots;          // partial slots in use
+    float* part;          // workspace: n_slots * B*H * kFwdBM * (D + 2) floats
+    int n_split;          // query tiles whose key range is split
+    FwdGroup groups[kMaxFwdGroups];
+    int split_qt[kMaxFwdGroups / 2], split_slot0[kMaxFwdGroups / 2], split_count[kMaxFwdGroups / 2];
 };
+
+// Split plan of the forward for a shape (fp32 kernels; bf16 never splits).
+struct FwdPlan {
+    int n_groups = 0, n_slots = 0;
+    FwdGroup groups[kMaxFwdGroups];
+    // per split query tile: first slot and number of slots
+    int n_split = 0;
+    int split_qt[kMaxFwdGroups / 2], split_slot0[kMaxFwdGroups / 2], split_count[kMaxFwdGroups / 2];
+};
+void fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan* out);
+size_t fwd_workspace_bytes(const FwdPlan& plan, int B, int H, int D);
 
 struct BwdParams {
     const void* q;

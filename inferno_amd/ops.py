@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import torch
 
-from . import INF_BF16, INF_F32, OP_ATTN_BWD, OP_ATTN_DECODE, InfernoError, Strides, default_scale, lib, workspace_bytes
+from . import INF_BF16, INF_F32, OP_ATTN_BWD, OP_ATTN_DECODE, OP_ATTN_FWD, InfernoError, Strides, default_scale, lib, workspace_bytes
 
 
 def _dt(t: torch.Tensor) -> int:
@@ -38,7 +38,7 @@ def _check(st: int, where: str) -> None:
         raise InfernoError(st, where)
 
 
-def attn_fwd(q, k, v, causal=True, scale=None, out=None, lse=None, stream=None):
+def attn_fwd(q, k, v, causal=True, scale=None, out=None, lse=None, workspace=None, stream=None):
     """O, LSE = causal attention forward of [B,H,T,D] views (fp32 or bf16)."""
     B, H, Tq, D = q.shape
     Tk = k.shape[2]
@@ -47,10 +47,15 @@ def attn_fwd(q, k, v, causal=True, scale=None, out=None, lse=None, stream=None):
         out = torch.empty((B, H, Tq, D), dtype=q.dtype, device=q.device)
     if lse is None:
         lse = torch.empty((B, H, Tq), dtype=torch.float32, device=q.device)
+    nbytes = workspace_bytes(OP_ATTN_FWD, B, H, Tq, Tk, D, _dt(q)) if causal else 0
+    if workspace is None and nbytes:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
     st = lib().inf_attn_fwd(
         q.data_ptr(), strides_of(q), k.data_ptr(), strides_of(k), v.data_ptr(), strides_of(v),
-        out.data_ptr(), strides_of(out), lse.data_ptr(), B, H, Tq, Tk, D, scale, int(bool(causal)),
-        _dt(q), _stream(stream),
+        out.data_ptr(), strides_of(out), lse.data_ptr(), ws_ptr, ws_len, B, H, Tq, Tk, D, scale,
+        int(bool(causal)), _dt(q), _stream(stream),
     )
     _check(st, "inf_attn_fwd")
     return out, lse

@@ -42,11 +42,12 @@ def dense(B, H, T, D):
 
 def fwd(**kw):
     a = dict(q=FAKE, sq=dense(1, 1, 8, 64), k=FAKE, sk=dense(1, 1, 8, 64), v=FAKE, sv=dense(1, 1, 8, 64),
-             o=FAKE, so=dense(1, 1, 8, 64), lse=FAKE, B=1, H=1, Tq=8, Tk=8, D=64, scale=0.125, causal=1,
-             dt=ia.INF_F32)
+             o=FAKE, so=dense(1, 1, 8, 64), lse=FAKE, ws=None, ws_bytes=0, B=1, H=1, Tq=8, Tk=8, D=64,
+             scale=0.125, causal=1, dt=ia.INF_F32)
     a.update(kw)
     return ia.lib().inf_attn_fwd(a["q"], a["sq"], a["k"], a["sk"], a["v"], a["sv"], a["o"], a["so"], a["lse"],
-                                 a["B"], a["H"], a["Tq"], a["Tk"], a["D"], a["scale"], a["causal"], a["dt"], None)
+                                 a["ws"], a["ws_bytes"], a["B"], a["H"], a["Tq"], a["Tk"], a["D"], a["scale"],
+                                 a["causal"], a["dt"], None)
 
 
 @pytest.mark.parametrize("kw,status", [
@@ -77,8 +78,25 @@ def test_bf16_alignment_is_8_bytes():
     assert fwd(q=FAKE + 4, dt=ia.INF_BF16) == 7
 
 
+def test_fwd_workspace():
+    # one small head: nothing to balance, no workspace
+    assert ia.workspace_bytes(ia.OP_ATTN_FWD, 1, 1, 8, 8, 64) == 0
+    assert ia.workspace_bytes(ia.OP_ATTN_FWD, 1, 1, 8, 8, 64, ia.INF_BF16) == 0
+    # a causal grid of few workgroups per CU splits its heaviest query tiles:
+    # whole (tile, head) partials of 128 rows x (D + 2) floats, 256-byte rounded
+    B, H, T, D = 4, 12, 1024, 64
+    ws = ia.workspace_bytes(ia.OP_ATTN_FWD, B, H, T, T, D)
+    assert ws > 0 and ws % 256 == 0
+    per_slot = B * H * 128 * (D + 2) * 4
+    assert ws >= 2 * per_slot and ws < per_slot * (T // 128) * 16
+    sq = dense(B, H, T, D)
+    args = dict(sq=sq, sk=sq, sv=sq, so=sq, B=B, H=H, Tq=T, Tk=T, D=D)
+    assert fwd(**args) == 6                                  # workspace missing
+    assert fwd(ws=FAKE, ws_bytes=ws - 256, **args) == 6      # too small
+    assert fwd(ws=FAKE + 16, ws_bytes=ws, **args) == 7       # misaligned
+
+
 def test_workspace_sizes():
-    assert ia.workspace_bytes(ia.OP_ATTN_FWD, 8, 12, 1024, 1024, 64) == 0
     ws = ia.workspace_bytes(ia.OP_ATTN_BWD, 8, 12, 1024, 1024, 64)
     assert ws >= 8 * 12 * 1024 * 4 and ws % 256 == 0
     wsb = ia.workspace_bytes(ia.OP_ATTN_BWD, 8, 12, 1024, 1024, 64, ia.INF_BF16)

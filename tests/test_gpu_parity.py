@@ -90,6 +90,30 @@ def test_fwd_bwd_bf16(ia, B, H, T, D):
         assert e <= TOL_BF16, f"{name} rel err {e:.3e}"
 
 
+@pytest.mark.parametrize("B,H,Tq,Tk,D", [
+    (1, 1, 1000, 1000, 64),
+    (1, 3, 777, 777, 64),
+    (1, 2, 1000, 1000, 32),
+    (1, 2, 1500, 1500, 128),
+    (1, 4, 900, 1024, 64),     # end-aligned causal: key j visible to query i iff j <= i + 124
+    (1, 2, 130, 1100, 64),     # short query block against a long cache
+])
+def test_fwd_split_plan_f32(ia, B, H, Tq, Tk, D):
+    """Few (tile, head) workgroups per CU: the forward splits the key range of its heaviest
+    query tiles across workgroups and merges the partials (the workspace is what they need)."""
+    print(f"[case] fwd split B{B} H{H} Tq{Tq} Tk{Tk} D{D}", flush=True)
+    assert ia.workspace_bytes(ia.OP_ATTN_FWD, B, H, Tq, Tk, D) > 0
+    q, k, v, _ = oracle.attn_inputs(B, H, Tq, D, seed=13, Tk=Tk)
+    o_r, lse_r = oracle.attn_fwd(q, k, v)
+    Q, K, V = dev(q), dev(k), dev(v)
+    ws = torch.full((ia.workspace_bytes(ia.OP_ATTN_FWD, B, H, Tq, Tk, D),), 0xFF, dtype=torch.uint8, device="cuda")
+    o, lse = ia.attn_fwd(Q, K, V, workspace=ws)  # NaN-filled workspace: contents on entry must not matter
+    torch.cuda.synchronize()
+    for name, x, r in (("O", host(o), o_r), ("LSE", host(lse), lse_r)):
+        e = oracle.rel_err(x, r)
+        assert e <= TOL_F32, f"{name} rel err {e:.3e}"
+
+
 def test_noncausal_f32(ia):
     print("[case] noncausal", flush=True)
     q, k, v, do = oracle.attn_inputs(1, 2, 96, 64, seed=7)
