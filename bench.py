@@ -72,8 +72,8 @@ def cpu_baseline(B, H, T, D, heads: int):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--cpu-heads", type=int, default=12, help="heads in the CPU-baseline sample (0 = skip)")
     ap.add_argument("--no-decode", action="store_true")
@@ -140,9 +140,16 @@ def main():
         ev[i][2].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    fwd_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
-    bwd_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+    fwd_all = np.array([e[0].elapsed_time(e[1]) for e in ev])
+    bwd_all = np.array([e[1].elapsed_time(e[2]) for e in ev])
+    step_all = np.array([e[0].elapsed_time(e[2]) for e in ev])
+    fwd_ms = float(np.mean(fwd_all))
+    bwd_ms = float(np.mean(bwd_all))
     ms_per_step = wall * 1e3 / args.steps
+
+    def pct(a):
+        return {"median_ms": round(float(np.median(a)), 4), "p10_ms": round(float(np.percentile(a, 10)), 4),
+                "p90_ms": round(float(np.percentile(a, 90)), 4)}
 
     F_fwd = flops_fwd(B, H, T, D)
     F_bwd = 2.5 * F_fwd
@@ -168,6 +175,7 @@ def main():
         "config": {"workload": "causal self-attention fwd+bwd, B=8 H=12 T=1024 D=64 (BASELINE config 2)",
                    "B": B, "H": H, "T": T, "D": D, "causal": True, "scale": ia.default_scale(D)},
         "frac_of_peak": round(value / peak, 4),
+        "timings": {"fwd": pct(fwd_all), "bwd": pct(bwd_all), "fwd+bwd": pct(step_all)},
         "roofline": {
             "bound": "mfma",
             "kernel": "bwd (bwd_pre + bwd_main; bwd_main dominates)",
