@@ -55,6 +55,9 @@ struct FwdTile {
     static constexpr int BN = (D >= 128) ? 32 : 64;  // keys per LDS tile
     static constexpr int KS = D + 4;                 // K row stride in LDS (floats)
     static constexpr int VTS = BN + 4;               // V^T row stride in LDS (floats)
+    // Software-pipelined loop (two score blocks live): fits two waves per
+    // SIMD up to D = 64; D = 128 keeps one score block.
+    static constexpr bool PIPE = D <= 64;
 };
 
 template <int D, typename E>
@@ -128,23 +131,40 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
     // K: chunk f -> (row f / C4, column chunk f % C4), row-major 16-byte loads.
     // V: chunk f -> (row f % 16 + 16 * (f / (16 * C4)), column chunk (f / 16) % C4).
     f32x4 kr[LPT], vr[LPT];
-    auto gload = [&](int t) {
+    // Rows at or past `lim` (<= Tk) load as zeros without touching memory.
+    auto gload_k = [&](int t, int lim) {
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
             const int f = tid + 256 * i;
             const int krow = t * BN + f / C4;
-            const int vrow = t * BN + (f & 15) + 16 * (f / (16 * C4));
             kr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            vr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (krow < p.Tk) kr[i] = ld4(K + (int64_t)krow * p.sk.t + 4 * (f % C4));
-            if (vrow < p.Tk) vr[i] = ld4(V + (int64_t)vrow * p.sv.t + 4 * ((f >> 4) % C4));
+            if (krow < lim) kr[i] = ld4(K + (int64_t)krow * p.sk.t + 4 * (f % C4));
         }
     };
-    auto sstore = [&](int buf) {
+    auto gload_v = [&](int t, int lim) {
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            const int f = tid + 256 * i;
+            const int vrow = t * BN + (f & 15) + 16 * (f / (16 * C4));
+            vr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (vrow < lim) vr[i] = ld4(V + (int64_t)vrow * p.sv.t + 4 * ((f >> 4) % C4));
+        }
+    };
+    auto gload = [&](int t) {
+        gload_k(t, p.Tk);
+        gload_v(t, p.Tk);
+    };
+    auto sstore_k = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
             const int f = tid + 256 * i;
             *reinterpret_cast<f32x4*>(&Ks[buf][f / C4][4 * (f % C4)]) = kr[i];
+        }
+    };
+    auto sstore_v = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            const int f = tid + 256 * i;
             const int vrow = (f & 15) + 16 * (f / (16 * C4));
             const int vc = 4 * ((f >> 4) % C4);
             Vt[buf][vc + 0][vrow] = vr[i][0];
@@ -152,6 +172,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
             Vt[buf][vc + 2][vrow] = vr[i][2];
             Vt[buf][vc + 3][vrow] = vr[i][3];
         }
+    };
+    auto sstore = [&](int buf) {
+        sstore_k(buf);
+        sstore_v(buf);
     };
 
     f32x16 o[NDB];
@@ -161,93 +185,131 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
     float l_run = 0.f;        // this lane's partial sum of p (its half of the keys)
     const float c = p.c;
 
-    gload(t_begin);  // bounds-checked rows: safe even past the last tile
-    sstore(0);
-    __syncthreads();
+    // S^T block of key tile in Ks[buf]: s[kb] reg 4j+cc holds key kb*32 + 8j + 4g + cc.
+    auto scores = [&](int buf, f32x16 (&s)[NKB]) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) s[kb] = f32x16{};
+#pragma unroll
+        for (int i = 0; i < HD; i += 4) {
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(&Ks[buf][kb * 32 + l32][g * HD + i]);
+                s[kb] = mfma32x32x2(a[0], qf[i + 0], s[kb]);
+                s[kb] = mfma32x32x2(a[1], qf[i + 1], s[kb]);
+                s[kb] = mfma32x32x2(a[2], qf[i + 2], s[kb]);
+                s[kb] = mfma32x32x2(a[3], qf[i + 3], s[kb]);
+            }
+        }
+    };
 
-    for (int t = t_begin; t < n_tiles; ++t) {
-        const int buf = (t - t_begin) & 1;
+    // Mask, online softmax and O^T += V^T P^T for key tile t (V^T in Vt[vbuf]).
+    auto softmax_pv = [&](f32x16 (&s)[NKB], int t, int vbuf) {
         const int k0 = t * BN;
-        if (t + 1 < n_tiles) gload(t + 1);
-
-        if (k0 < wave_kend) {
-            // ---- S^T = K Q^T --------------------------------------------------
-            f32x16 s[NKB];
-#pragma unroll
-            for (int kb = 0; kb < NKB; ++kb) s[kb] = f32x16{};
-#pragma unroll
-            for (int i = 0; i < HD; i += 4) {
-#pragma unroll
-                for (int kb = 0; kb < NKB; ++kb) {
-                    const f32x4 a =
-                        *reinterpret_cast<const f32x4*>(&Ks[buf][kb * 32 + l32][g * HD + i]);
-                    s[kb] = mfma32x32x2(a[0], qf[i + 0], s[kb]);
-                    s[kb] = mfma32x32x2(a[1], qf[i + 1], s[kb]);
-                    s[kb] = mfma32x32x2(a[2], qf[i + 2], s[kb]);
-                    s[kb] = mfma32x32x2(a[3], qf[i + 3], s[kb]);
-                }
-            }
-
-            // ---- mask, online softmax ------------------------------------------
-            const bool need_mask =
-                (k0 + BN > p.Tk) || (p.causal && (k0 + BN - 1 > q0w + p.off));
-            if (need_mask) {
-                const int lim = p.causal ? min(p.Tk - 1, qrow + p.off) : p.Tk - 1;
-#pragma unroll
-                for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                        if (key > lim) s[kb][r] = -INFINITY;
-                    }
-            }
-            float mloc = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kb][r]);
-            mloc = fmaxf(mloc, shfl_xor(mloc, 32));
-            const float m_new = fmaxf(m_run, mloc);
-            // A row can see no key of a chunk that does not start at key 0:
-            // keep m = -inf, l = 0, O = 0 for it instead of exp2(NaN).
-            const bool row_dead = m_new == -INFINITY;
-            const float alpha = row_dead ? 1.f : fast_exp2((m_run - m_new) * c);  // m_run = -inf -> 0
-            const float mc = row_dead ? 0.f : m_new * c;
-            float lsum = 0.f;
+        const bool need_mask = (k0 + BN > p.Tk) || (p.causal && (k0 + BN - 1 > q0w + p.off));
+        if (need_mask) {
+            const int lim = p.causal ? min(p.Tk - 1, qrow + p.off) : p.Tk - 1;
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float e = fast_exp2(fmaf(s[kb][r], c, -mc));
-                    s[kb][r] = e;
-                    lsum += e;
-                }
-            l_run = fmaf(l_run, alpha, lsum);
-            m_run = m_new;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-
-            // ---- O^T += V^T P^T --------------------------------------------------
-            // reg 4j+cc of s[kb] holds key kb*32 + 8j + 4g + cc
-#pragma unroll
-            for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    f32x4 va[NDB];
-#pragma unroll
-                    for (int db = 0; db < NDB; ++db)
-                        va[db] = *reinterpret_cast<const f32x4*>(
-                            &Vt[buf][db * 32 + l32][kb * 32 + 8 * j + 4 * g]);
-#pragma unroll
-                    for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-                        for (int db = 0; db < NDB; ++db)
-                            o[db] = mfma32x32x2(va[db][cc], s[kb][4 * j + cc], o[db]);
+                    const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (key > lim) s[kb][r] = -INFINITY;
                 }
         }
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kb][r]);
+        mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+        const float m_new = fmaxf(m_run, mloc);
+        // A row can see no key of a chunk that does not start at key 0:
+        // keep m = -inf, l = 0, O = 0 for it instead of exp2(NaN).
+        const bool row_dead = m_new == -INFINITY;
+        const float alpha = row_dead ? 1.f : fast_exp2((m_run - m_new) * c);  // m_run = -inf -> 0
+        const float mc = row_dead ? 0.f : m_new * c;
+        // row sum as four independent partial chains
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float e = fast_exp2(fmaf(s[kb][r], c, -mc));
+                s[kb][r] = e;
+                ls[r & 3] += e;
+            }
+        l_run = fmaf(l_run, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[db] *= alpha;
 
-        if (t + 1 < n_tiles) sstore(buf ^ 1);
+        // reg 4j+cc of s[kb] holds key kb*32 + 8j + 4g + cc
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f32x4 va[NDB];
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+                    va[db] = *reinterpret_cast<const f32x4*>(&Vt[vbuf][db * 32 + l32][kb * 32 + 8 * j + 4 * g]);
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db)
+                        o[db] = mfma32x32x2(va[db][cc], s[kb][4 * j + cc], o[db]);
+            }
+    };
+
+    if constexpr (FwdTile<D>::PIPE) {
+        // Software pipeline: S of tile t+1 is issued before the softmax of tile
+        // t, so the matrix pipe has independent work while the softmax runs.
+        // K runs one tile ahead of V: at the top of step t, Ks[i&1] and
+        // Ks[(i+1)&1] hold K_t (already consumed) and K_{t+1}, Vt[i&1] holds
+        // V_t (i = t - t_begin).  Step t writes K_{t+2} over K_t and V_{t+1}
+        // over V_{t-1}, both last read before the previous barrier.
+        gload(t_begin);  // bounds-checked rows: safe even past the last tile
+        sstore_k(0);
+        sstore_v(0);
+        gload_k(t_begin + 1, t_begin + 1 < n_tiles ? p.Tk : 0);
+        sstore_k(1);
         __syncthreads();
+        f32x16 sa[NKB], sb[NKB];
+        if (t_begin * BN < wave_kend) scores(0, sa);
+        __syncthreads();  // Ks[0] is overwritten at the end of the first step
+
+        // The prefetch and the stores run unconditionally (straight-line code
+        // keeps the loads overlapped); past the last tile they move zeros
+        // into buffers that are not read again.
+        auto step = [&](int t, f32x16 (&cur)[NKB], f32x16 (&nxt)[NKB]) {
+            const int i = t - t_begin;
+            const bool has_next = t + 1 < n_tiles;
+            gload_k(t + 2, t + 2 < n_tiles ? p.Tk : 0);
+            gload_v(t + 1, has_next ? p.Tk : 0);
+            if (has_next && (t + 1) * BN < wave_kend) scores((i + 1) & 1, nxt);
+            if (t * BN < wave_kend) softmax_pv(cur, t, i & 1);
+            sstore_k(i & 1);
+            sstore_v((i + 1) & 1);
+            __syncthreads();
+        };
+        for (int t = t_begin; t < n_tiles; t += 2) {
+            step(t, sa, sb);
+            if (t + 1 < n_tiles) step(t + 1, sb, sa);
+        }
+    } else {
+        gload(t_begin);  // bounds-checked rows: safe even past the last tile
+        sstore(0);
+        __syncthreads();
+        for (int t = t_begin; t < n_tiles; ++t) {
+            const int buf = (t - t_begin) & 1;
+            if (t + 1 < n_tiles) gload(t + 1);
+            if (t * BN < wave_kend) {
+                f32x16 s[NKB];
+                scores(buf, s);
+                softmax_pv(s, t, buf);
+            }
+            if (t + 1 < n_tiles) sstore(buf ^ 1);
+            __syncthreads();
+        }
     }
 
     // ---- epilogue ---------------------------------------------------------------
