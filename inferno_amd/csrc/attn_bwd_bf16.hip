@@ -132,11 +132,19 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
     q_begin = (q_begin / BQ) * BQ;
     const float c = p.c;
 
-    for (int q0 = q_begin; q0 < p.Tq; q0 += BQ) {
-        // ---- stage Q and dO, row-major and transposed --------------------------
+    // Q / dO staging, prefetched one query tile ahead in registers: tile q0's
+    // rows are loaded while tile q0 - BQ computes, and stored to LDS once the
+    // previous tile's S / dP / dV / dK phase is done with the staged copies
+    // (after the dS barrier), so each tile needs two barriers.
+    bf16x8 ra[QLPT], rb[QLPT];
+    float r_lse = 0.f, r_dl = 0.f;
+    // Rows at or past `lim` (<= Tq) load as zeros without touching memory;
+    // raw values only, so no arithmetic waits on the loads here.
+    auto gload_q = [&](int q0, int lim) {
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
             const int f = tid + 256 * i;
+            ra[i] = rb[i] = bf16x8{};
             if (f >= 2 * QTASK) continue;
             const int which = f / QTASK;  // 0: Q, 1: dO
             const int rem = f % QTASK;
@@ -144,27 +152,51 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
             const __bf16* src = which ? dO : Q;
             const int64_t st = which ? p.sdo.t : p.sq.t;
             const int r0 = q0 + 2 * qp;
-            const bf16x8 a = r0 < p.Tq ? *reinterpret_cast<const bf16x8*>(src + (int64_t)r0 * st + 8 * c8) : bf16x8{};
-            const bf16x8 bb = r0 + 1 < p.Tq ? *reinterpret_cast<const bf16x8*>(src + (int64_t)(r0 + 1) * st + 8 * c8)
-                                            : bf16x8{};
+            if (r0 < lim) ra[i] = *reinterpret_cast<const bf16x8*>(src + (int64_t)r0 * st + 8 * c8);
+            if (r0 + 1 < lim) rb[i] = *reinterpret_cast<const bf16x8*>(src + (int64_t)(r0 + 1) * st + 8 * c8);
+        }
+        r_lse = r_dl = 0.f;
+        if (tid < BQ && q0 + tid < lim) {
+            r_lse = LSE[q0 + tid];
+            r_dl = DL[q0 + tid];
+        }
+    };
+    auto sstore_q = [&]() {
+#pragma unroll
+        for (int i = 0; i < QLPT; ++i) {
+            const int f = tid + 256 * i;
+            if (f >= 2 * QTASK) continue;
+            const int which = f / QTASK;
+            const int rem = f % QTASK;
+            const int qp = rem % (BQ / 2), c8 = rem / (BQ / 2);
             __bf16(*rows)[QS] = which ? dOs : Qs;
             __bf16(*cols)[TS] = which ? dOTs : QTs;
-            *reinterpret_cast<bf16x8*>(&rows[2 * qp][8 * c8]) = a;
-            *reinterpret_cast<bf16x8*>(&rows[2 * qp + 1][8 * c8]) = bb;
+            *reinterpret_cast<bf16x8*>(&rows[2 * qp][8 * c8]) = ra[i];
+            *reinterpret_cast<bf16x8*>(&rows[2 * qp + 1][8 * c8]) = rb[i];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 bf16x2 pr;
-                pr[0] = a[e];
-                pr[1] = bb[e];
+                pr[0] = ra[i][e];
+                pr[1] = rb[i][e];
                 *reinterpret_cast<bf16x2*>(&cols[8 * c8 + e][2 * qp]) = pr;
             }
         }
         if (tid < BQ) {
-            const int qi = q0 + tid;
-            lse_s[tid] = (qi < p.Tq) ? LSE[qi] * kLog2e : 0.f;
-            dl_s[tid] = (qi < p.Tq) ? DL[qi] : 0.f;
+            lse_s[tid] = r_lse;  // natural-log LSE; scaled by log2(e) where it is read
+            dl_s[tid] = r_dl;
         }
-        __syncthreads();
+    };
+
+    gload_q(q_begin, p.Tq);
+    sstore_q();
+    __syncthreads();
+
+    // The prefetch and its store are straight-line (a row limit of 0 past the
+    // last tile): conditional blocks would make the compiler wait for every
+    // outstanding memory operation, the previous tile's dQ atomics included,
+    // at the top of each tile.
+    for (int q0 = q_begin; q0 < p.Tq; q0 += BQ) {
+        gload_q(q0 + BQ, q0 + BQ < p.Tq ? p.Tq : 0);
 
         const bool active = !p.causal || (q0 + BQ - 1 + p.off >= k0w);
         bf16x8 pb[2], dsb[2];
@@ -180,7 +212,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
             // P and dS; register r holds query row 8*(r/4) + 4*g + r%4 of the tile.
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]);
+                const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLog2e;
                 const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
 #pragma unroll
                 for (int cc = 0; cc < 4; ++cc) {
@@ -215,6 +247,9 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) dSs[8 * (r >> 2) + 4 * g + (r & 3)][wave * 32 + l32] = dsb[r >> 3][r & 7];
         __syncthreads();
+        // every wave is past its reads of the staged tile: stage the next one
+        // (zeros after the last tile, never read)
+        sstore_q();
 
         // ---- dQ tile (32 x D) += dS (32 x 128) K (128 x D), 16x16 blocks ---------
 #pragma unroll
