@@ -78,7 +78,8 @@ def test_fwd_bwd_f32(ia, B, H, T, D):
         assert e <= TOL_F32, f"{name} rel err {e:.3e}"
 
 
-@pytest.mark.parametrize("B,H,T,D", [(1, 4, 128, 32), (1, 2, 129, 64), (1, 1, 300, 128)])
+@pytest.mark.parametrize("B,H,T,D", [(1, 4, 128, 32), (1, 2, 129, 64), (1, 1, 300, 128), (2, 3, 333, 64),
+                                     (1, 2, 1000, 64), (1, 1, 700, 32)])
 def test_fwd_bwd_bf16(ia, B, H, T, D):
     print(f"[case] fwd_bwd_bf16 B{B} H{H} T{T} D{D}", flush=True)
     q, k, v, do = (bf16_round(x) for x in oracle.attn_inputs(B, H, T, D, seed=42))
