@@ -257,6 +257,26 @@ int inf_embedding_bwd(const int32_t* ids, int64_t n_tokens, const float* dout, i
 int inf_adamw_step(void* p, const void* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2, float eps,
                    float weight_decay, float bias_correction1, float bias_correction2, inf_dtype dt, void* stream);
 
+/* One parameter tensor of a multi-tensor AdamW step: p, g (dt), m, v (fp32),
+ * n elements; p and g 16-byte (fp32) / 8-byte (bf16) aligned, m and v 16-byte
+ * aligned, tensors disjoint. */
+typedef struct {
+    void* p;
+    const void* g;
+    float* m;
+    float* v;
+    int64_t n;
+} inf_adamw_tensor;
+
+/* The same update as inf_adamw_step (bit-identical per element) over a list of
+ * tensors in as few launches as the list allows (48 tensors per launch).
+ * Replaces the per-parameter loop of OptimizerAdamW::step
+ * (src/inferno/optim/adamw.cpp:18-64, one cuda_adamw_step_impl launch per
+ * parameter).  The table is read on the host during the call. */
+int inf_adamw_step_multi(const inf_adamw_tensor* tensors, int n_tensors, float lr, float beta1, float beta2,
+                         float eps, float weight_decay, float bias_correction1, float bias_correction2, inf_dtype dt,
+                         void* stream);
+
 /* out[c] = sum_r x[r * ldx + c] (or out[c] += when accumulate), fp32 result:
  * the bias gradient of Linear and the gradient of a broadcast operand.
  * Replaces cuda_sum_to_shape (src/inferno/cuda/cudaops.h:43) for reductions

@@ -56,6 +56,7 @@ EXPORTS = (
     "inf_embedding_fwd",
     "inf_embedding_bwd",
     "inf_adamw_step",
+    "inf_adamw_step_multi",
     "inf_col_sum",
     "inf_binary_bcast",
     "inf_last_error_detail",
@@ -66,6 +67,13 @@ class Strides(ctypes.Structure):
     """inf_strides: element strides of a [B, H, T, D] view."""
 
     _fields_ = [("b", ctypes.c_int64), ("h", ctypes.c_int64), ("t", ctypes.c_int64), ("d", ctypes.c_int64)]
+
+
+class AdamWTensor(ctypes.Structure):
+    """inf_adamw_tensor: one parameter tensor of a multi-tensor AdamW step."""
+
+    _fields_ = [("p", ctypes.c_void_p), ("g", ctypes.c_void_p), ("m", ctypes.c_void_p), ("v", ctypes.c_void_p),
+                ("n", ctypes.c_int64)]
 
 
 class InfernoError(RuntimeError):
@@ -128,6 +136,8 @@ def lib() -> ctypes.CDLL:
         L.inf_embedding_fwd.argtypes = [vp, i64, vp, i64, i64, vp, i32, vp]
         L.inf_embedding_bwd.argtypes = [vp, i64, vp, i64, i64, vp, i32, vp]
         L.inf_adamw_step.argtypes = [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, f32, i32, vp]
+        L.inf_adamw_step_multi.argtypes = [ctypes.POINTER(AdamWTensor), i32, f32, f32, f32, f32, f32, f32, f32, i32,
+                                           vp]
         L.inf_col_sum.argtypes = [vp, i64, i64, i64, vp, i32, i32, vp, sz, vp]
         L.inf_binary_bcast.argtypes = [i32, vp, vp, vp, i64, i64, i32, vp]
         for name in EXPORTS[11:-1]:
@@ -178,6 +188,7 @@ from .ops import (  # noqa: E402  (torch-facing helpers need lib())
 )
 from .nn import (  # noqa: E402
     adamw_step,
+    adamw_step_multi,
     col_sum,
     cross_entropy_bwd,
     cross_entropy_fwd,

@@ -7,7 +7,9 @@
 // InfernoApp/main.cpp:675-811); the compute goes through the ops of
 // inferno/core/ops.h.
 #include <cmath>
+#include <map>
 #include <random>
+#include <vector>
 
 #include "detail.h"
 #include "inferno/gradengine/engine.h"
@@ -247,6 +249,11 @@ void OptimizerAdamW::step() {
     m_step++;
     const float bc1 = 1.0f - std::pow(m_beta1, static_cast<float>(m_step));
     const float bc2 = 1.0f - std::pow(m_beta2, static_cast<float>(m_step));
+    // HIP parameters are updated together, one multi-tensor call per (device,
+    // dtype); `keep` holds the contiguous gradient copies until the calls are
+    // enqueued (later reuse of their blocks is stream-ordered after them).
+    std::map<std::pair<int, int>, std::vector<inf_adamw_tensor>> groups;
+    std::vector<Tensor> keep;
     for (Tensor* p : m_parameters) {
         if (p == nullptr || !p->grad()) continue;
         Tensor* grad = p->grad().get();
@@ -283,13 +290,20 @@ void OptimizerAdamW::step() {
                 vp[i] = vi;
             }
         } else {
-            detail::DeviceGuard dg(p->device().index);
-            detail::status_check(inf_adamw_step(p->data_ptr(), g.data_ptr(), static_cast<float*>(st.m.data_ptr()),
-                                                static_cast<float*>(st.v.data_ptr()), (int64_t)n, m_lr, m_beta1,
-                                                m_beta2, m_eps, m_weight_decay, bc1, bc2,
-                                                detail::inf_dt(p->dtype(), "OptimizerAdamW"), detail::stream_of(*p)),
-                                 "inf_adamw_step");
+            const int dt = (int)detail::inf_dt(p->dtype(), "OptimizerAdamW");
+            groups[{p->device().index, dt}].push_back(inf_adamw_tensor{p->data_ptr(), g.data_ptr(),
+                                                                       static_cast<float*>(st.m.data_ptr()),
+                                                                       static_cast<float*>(st.v.data_ptr()),
+                                                                       (int64_t)n});
+            keep.push_back(g);
         }
+    }
+    for (auto& [key, list] : groups) {
+        detail::DeviceGuard dg(key.first);
+        detail::status_check(inf_adamw_step_multi(list.data(), (int)list.size(), m_lr, m_beta1, m_beta2, m_eps,
+                                                  m_weight_decay, bc1, bc2, (inf_dtype)key.second,
+                                                  detail::stream_for(key.first)),
+                             "inf_adamw_step_multi");
     }
 }
 

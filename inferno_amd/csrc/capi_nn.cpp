@@ -7,6 +7,8 @@
 #include <cstdint>
 
 #include "inferno_hip.h"
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace {
@@ -205,6 +207,63 @@ int inf_adamw_step(void* p, const void* g, float* m, float* v, int64_t n, float 
     if (!(bias_correction1 > 0.f) || !(bias_correction2 > 0.f)) return INF_ERR_BAD_SCALE;
     inf::AdamWParams a{p, g, m, v, n, lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2};
     return hip_status(inf::launch_adamw(a, dt == INF_BF16, S(stream)));
+}
+
+int inf_adamw_step_multi(const inf_adamw_tensor* tensors, int n_tensors, float lr, float beta1, float beta2,
+                         float eps, float weight_decay, float bias_correction1, float bias_correction2, inf_dtype dt,
+                         void* stream) {
+    if (!dtype_ok(dt)) return INF_ERR_BAD_DTYPE;
+    if (n_tensors < 0) return INF_ERR_BAD_SHAPE;
+    if (n_tensors == 0) return INF_OK;
+    if (!tensors) return INF_ERR_NULL_POINTER;
+    if (!(bias_correction1 > 0.f) || !(bias_correction2 > 0.f)) return INF_ERR_BAD_SCALE;
+    const uintptr_t pa = dt == INF_BF16 ? 8 : 16;  // 4 elements of p / g per access
+    for (int i = 0; i < n_tensors; ++i) {
+        const inf_adamw_tensor& t = tensors[i];
+        if (t.n < 0) return INF_ERR_BAD_SHAPE;
+        if (t.n == 0) continue;
+        if (!t.p || !t.g || !t.m || !t.v) return INF_ERR_NULL_POINTER;
+        if (reinterpret_cast<uintptr_t>(t.p) % pa || reinterpret_cast<uintptr_t>(t.g) % pa ||
+            reinterpret_cast<uintptr_t>(t.m) % 16 || reinterpret_cast<uintptr_t>(t.v) % 16)
+            return INF_ERR_ALIGNMENT;
+        if (t.n > (int64_t)1 << 40) return INF_ERR_BAD_SHAPE;
+    }
+    // Launches of up to kAdamWMaxTensors tensors and < 2^31 workgroups each.
+    inf::AdamWMultiParams a{};
+    a.lr = lr; a.beta1 = beta1; a.beta2 = beta2; a.eps = eps; a.weight_decay = weight_decay;
+    a.bc1 = bias_correction1; a.bc2 = bias_correction2;
+    auto flush = [&]() -> int {
+        if (a.n_tensors == 0) return INF_OK;
+        const int st = hip_status(inf::launch_adamw_multi(a, dt == INF_BF16, S(stream)));
+        a.n_tensors = 0;
+        a.block0[0] = 0;
+        return st;
+    };
+    constexpr int64_t kMaxBlocks = (int64_t)1 << 30;
+    for (int i = 0; i < n_tensors; ++i) {
+        const inf_adamw_tensor& t = tensors[i];
+        if (t.n == 0) continue;
+        int64_t off = 0;
+        while (off < t.n) {  // a tensor larger than one launch's block budget is cut in pieces
+            const int64_t room = kMaxBlocks - a.block0[a.n_tensors];
+            int64_t take = std::min<int64_t>(t.n - off, room * 1024);
+            if (take <= 0 || a.n_tensors == inf::kAdamWMaxTensors) {
+                if (const int st = flush()) return st;
+                continue;
+            }
+            const int k = a.n_tensors;
+            const size_t esz = dt == INF_BF16 ? 2 : 4;
+            a.p[k] = static_cast<char*>(t.p) + off * esz;
+            a.g[k] = static_cast<const char*>(t.g) + off * esz;
+            a.m[k] = t.m + off;
+            a.v[k] = t.v + off;
+            a.n[k] = take;
+            a.block0[k + 1] = a.block0[k] + (int)((take + 1023) / 1024);
+            a.n_tensors = k + 1;
+            off += take;
+        }
+    }
+    return flush();
 }
 
 int inf_col_sum(const void* x, int64_t rows, int64_t cols, int64_t ldx, float* out, int accumulate, inf_dtype dt,

@@ -162,6 +162,21 @@ struct AdamWParams {
     float lr, beta1, beta2, eps, weight_decay, bc1, bc2;
 };
 
+// Multi-tensor AdamW: up to kAdamWMaxTensors tensors per launch, the table
+// passed by value in the kernel arguments; workgroup w updates elements
+// [1024 (w - block0[t]), +1024) of the tensor t with block0[t] <= w < block0[t+1].
+constexpr int kAdamWMaxTensors = 48;
+struct AdamWMultiParams {
+    float lr, beta1, beta2, eps, weight_decay, bc1, bc2;
+    int n_tensors;
+    void* p[kAdamWMaxTensors];
+    const void* g[kAdamWMaxTensors];
+    float* m[kAdamWMaxTensors];
+    float* v[kAdamWMaxTensors];
+    int64_t n[kAdamWMaxTensors];
+    int block0[kAdamWMaxTensors + 1];
+};
+
 struct GemmArgs {         // row-major C = alpha * op(A) op(B) + beta * C (+ bias[N] per row)
     int ta, tb, bf16;
     int64_t M, N, K;
@@ -200,6 +215,7 @@ int launch_ce_bwd(const CeParams& p, int bf16, hipStream_t s);
 int launch_embed_fwd(const EmbParams& p, int bf16, hipStream_t s);
 int launch_embed_bwd(const EmbParams& p, hipStream_t s);
 int launch_adamw(const AdamWParams& a, int bf16, hipStream_t s);
+int launch_adamw_multi(const AdamWMultiParams& a, int bf16, hipStream_t s);
 int launch_bcast(int op, const void* a, const void* b, void* out, int64_t n, int64_t nb, int vec, int bf16,
                  hipStream_t s);
 

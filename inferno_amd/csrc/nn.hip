@@ -197,16 +197,32 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(LnBwdParams p) {
 // out[c] (+)= sum_r in[r * cols + c] for r < rows: workgroup w owns columns
 // [16*w, 16*w + 16); thread (c = tid % 16, g = tid / 16) sums rows g, g+16, ...
 // and the 16 row groups are added in LDS in a fixed order.  Deterministic.
-__global__ __launch_bounds__(256) void col_reduce_kernel(const float* __restrict__ in, float* __restrict__ out,
+// Column sums of partial rows: 16 columns x 16 row groups per workgroup,
+// each thread summing its rows in four independent chains (rows r, r+16,
+// r+32, r+48 of each group of 64) so four loads are in flight; fixed order,
+// deterministic.  blockIdx.y selects one of two (in, out) pairs so LayerNorm's
+// dgamma and dbeta reduce in one launch.
+__global__ __launch_bounds__(256) void col_reduce_kernel(const float* __restrict__ in0, float* __restrict__ out0,
+                                                         const float* __restrict__ in1, float* __restrict__ out1,
                                                          int64_t rows, int64_t cols, int accumulate) {
     __shared__ float red[16][17];
+    const float* in = blockIdx.y ? in1 : in0;
+    float* out = blockIdx.y ? out1 : out0;
     const int cl = threadIdx.x & 15;
     const int g = threadIdx.x >> 4;
     const int64_t c = (int64_t)blockIdx.x * 16 + cl;
-    float s = 0.f;
-    if (c < cols)
-        for (int64_t r = g; r < rows; r += 16) s += in[r * cols + c];
-    red[g][cl] = s;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    if (c < cols) {
+        int64_t r = g;
+        for (; r + 48 < rows; r += 64) {
+            s0 += in[r * cols + c];
+            s1 += in[(r + 16) * cols + c];
+            s2 += in[(r + 32) * cols + c];
+            s3 += in[(r + 48) * cols + c];
+        }
+        for (; r < rows; r += 16) s0 += in[r * cols + c];
+    }
+    red[g][cl] = (s0 + s1) + (s2 + s3);
     __syncthreads();
     if (g == 0 && c < cols) {
         float t = 0.f;
@@ -228,7 +244,15 @@ __global__ __launch_bounds__(256) void col_partial_kernel(const void* __restrict
     const typename E::T* p = (const typename E::T*)x;
     const int64_t r1 = min(rows, r0 + kColChunk);
     float s = 0.f;
-    for (int64_t r = r0; r < r1; ++r) s += E::ld(p + r * ldx + c);
+    if (r1 - r0 == kColChunk) {  // full chunk: all loads issued before the sum
+        float v[kColChunk];
+#pragma unroll
+        for (int r = 0; r < kColChunk; ++r) v[r] = E::ld(p + (r0 + r) * ldx + c);
+#pragma unroll
+        for (int r = 0; r < kColChunk; ++r) s += v[r];
+    } else {
+        for (int64_t r = r0; r < r1; ++r) s += E::ld(p + r * ldx + c);
+    }
     part[(int64_t)blockIdx.y * cols + c] = s;
 }
 
@@ -402,6 +426,22 @@ __global__ __launch_bounds__(256) void embed_bwd_kernel(EmbParams p) {
 //   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2;
 //   upd = (m / bc1) / (sqrt(v / bc2) + eps) + wd * p;  p -= lr * upd.
 // ============================================================================
+// One AdamW element update (cpu_adamw_step_impl, adamw.h:67-111), shared by
+// the single- and multi-tensor kernels.  No FMA contraction: every product and
+// sum rounds separately, as in the reference's CPU loop, and the two kernels
+// cannot round differently.
+__device__ __forceinline__ void adamw_elem(float g, float& m, float& v, float& p, float lr, float b1, float b2,
+                                           float eps, float wd, float bc1, float bc2) {
+#pragma clang fp contract(off)
+    m = b1 * m + (1.0f - b1) * g;
+    v = b2 * v + (1.0f - b2) * g * g;
+    const float mhat = m / bc1;
+    const float vhat = v / bc2;
+    float upd = mhat / (sqrtf(vhat) + eps);
+    if (wd != 0.0f) upd += wd * p;
+    p -= lr * upd;
+}
+
 template <typename E>
 __global__ __launch_bounds__(256) void adamw_kernel(AdamWParams a) {
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
@@ -412,13 +452,7 @@ __global__ __launch_bounds__(256) void adamw_kernel(AdamWParams a) {
     auto one = [&](int64_t j) {
         const float g = E::ld(G + j);
         float mi = M[j], vi = Vv[j], pi = E::ld(P + j);
-        mi = a.beta1 * mi + (1.0f - a.beta1) * g;
-        vi = a.beta2 * vi + (1.0f - a.beta2) * g * g;
-        const float mhat = mi / a.bc1;
-        const float vhat = vi / a.bc2;
-        float upd = mhat / (sqrtf(vhat) + a.eps);
-        if (a.weight_decay != 0.0f) upd += a.weight_decay * pi;
-        pi -= a.lr * upd;
+        adamw_elem(g, mi, vi, pi, a.lr, a.beta1, a.beta2, a.eps, a.weight_decay, a.bc1, a.bc2);
         E::st(P + j, pi);
         M[j] = mi;
         Vv[j] = vi;
@@ -428,6 +462,47 @@ __global__ __launch_bounds__(256) void adamw_kernel(AdamWParams a) {
         for (int j = 0; j < 4; ++j) one(i + j);
     } else {
         for (int64_t j = i; j < a.n; ++j) one(j);
+    }
+}
+
+// Multi-tensor AdamW: 4 elements per thread with 16-byte (fp32) / 8-byte (bf16)
+// accesses; every tensor starts 16-byte aligned (checked on the host), so only
+// a tensor's last partial group of 4 goes element by element.
+template <typename E>
+__global__ __launch_bounds__(256) void adamw_multi_kernel(AdamWMultiParams a) {
+    const int w = blockIdx.x;
+    int t = 0;
+    while (t + 1 < a.n_tensors && a.block0[t + 1] <= w) ++t;  // wave-uniform, <= 48 steps
+    const int64_t n = a.n[t];
+    const int64_t i = ((int64_t)(w - a.block0[t]) * 256 + threadIdx.x) * 4;
+    typename E::T* P = (typename E::T*)a.p[t];
+    const typename E::T* G = (const typename E::T*)a.g[t];
+    float* M = a.m[t];
+    float* Vv = a.v[t];
+    if (i + 3 < n) {
+        const f32x4 g = ld4(G + i);
+        f32x4 p = ld4(P + i);
+        f32x4 m = *reinterpret_cast<const f32x4*>(M + i);
+        f32x4 v = *reinterpret_cast<const f32x4*>(Vv + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float mj = m[j], vj = v[j], pj = p[j];
+            adamw_elem(g[j], mj, vj, pj, a.lr, a.beta1, a.beta2, a.eps, a.weight_decay, a.bc1, a.bc2);
+            m[j] = mj;
+            v[j] = vj;
+            p[j] = pj;
+        }
+        st4(P + i, p);
+        *reinterpret_cast<f32x4*>(M + i) = m;
+        *reinterpret_cast<f32x4*>(Vv + i) = v;
+    } else {
+        for (int64_t j = i; j < n; ++j) {
+            float mj = M[j], vj = Vv[j], pj = E::ld(P + j);
+            adamw_elem(E::ld(G + j), mj, vj, pj, a.lr, a.beta1, a.beta2, a.eps, a.weight_decay, a.bc1, a.bc2);
+            E::st(P + j, pj);
+            M[j] = mj;
+            Vv[j] = vj;
+        }
     }
 }
 
@@ -502,11 +577,9 @@ static int ln_bwd_t(const LnBwdParams& p, hipStream_t s) {
         case 5: case 6: case 7: case 8: hipLaunchKernelGGL((ln_bwd_kernel<8, T>), grid, dim3(256), 0, s, p); break;
         default: return (int)hipErrorInvalidValue;  // dim <= kLnBwdMaxDim (checked by the caller)
     }
-    const dim3 rgrid(blocks_for(p.dim, 16));
-    hipLaunchKernelGGL(col_reduce_kernel, rgrid, dim3(256), 0, s, p.part, p.dgamma, (int64_t)nb, (int64_t)p.dim,
-                       p.accumulate);
-    hipLaunchKernelGGL(col_reduce_kernel, rgrid, dim3(256), 0, s, p.part + (int64_t)nb * p.dim, p.dbeta,
-                       (int64_t)nb, (int64_t)p.dim, p.accumulate);
+    const dim3 rgrid(blocks_for(p.dim, 16), 2);  // y: dgamma, dbeta
+    hipLaunchKernelGGL(col_reduce_kernel, rgrid, dim3(256), 0, s, p.part, p.dgamma, p.part + (int64_t)nb * p.dim,
+                       p.dbeta, (int64_t)nb, (int64_t)p.dim, p.accumulate);
     return (int)hipGetLastError();
 }
 
@@ -522,8 +595,8 @@ int launch_col_sum(const void* x, float* out, float* part, int64_t rows, int64_t
         hipLaunchKernelGGL(col_partial_kernel<BF16>, g1, dim3(256), 0, s, x, part, rows, cols, ldx);
     else
         hipLaunchKernelGGL(col_partial_kernel<F32>, g1, dim3(256), 0, s, x, part, rows, cols, ldx);
-    hipLaunchKernelGGL(col_reduce_kernel, dim3(blocks_for(cols, 16)), dim3(256), 0, s, part, out, chunks, cols,
-                       accumulate);
+    hipLaunchKernelGGL(col_reduce_kernel, dim3(blocks_for(cols, 16)), dim3(256), 0, s, part, out, part, out, chunks,
+                       cols, accumulate);
     return (int)hipGetLastError();
 }
 
@@ -587,6 +660,15 @@ int launch_adamw(const AdamWParams& a, int bf16, hipStream_t s) {
         hipLaunchKernelGGL(adamw_kernel<BF16>, grid, dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL(adamw_kernel<F32>, grid, dim3(256), 0, s, a);
+    return (int)hipGetLastError();
+}
+
+int launch_adamw_multi(const AdamWMultiParams& a, int bf16, hipStream_t s) {
+    const dim3 grid((unsigned)a.block0[a.n_tensors]);
+    if (bf16)
+        hipLaunchKernelGGL(adamw_multi_kernel<BF16>, grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(adamw_multi_kernel<F32>, grid, dim3(256), 0, s, a);
     return (int)hipGetLastError();
 }
 

@@ -136,6 +136,29 @@ def adamw_step(p, g, m, v, step, lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weigh
     _check(st, "inf_adamw_step")
 
 
+def adamw_step_multi(params, step, lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, stream=None):
+    """In-place AdamW update of a list of (p, g, m, v) tensors through one multi-tensor call."""
+    import ctypes
+
+    import numpy as np
+
+    from . import AdamWTensor
+
+    bc1 = float(np.float32(1.0) - np.power(np.float32(beta1), np.float32(step)))
+    bc2 = float(np.float32(1.0) - np.power(np.float32(beta2), np.float32(step)))
+    dts = {_dt(p) for p, _, _, _ in params}
+    if len(dts) > 1:
+        raise ValueError("adamw_step_multi: all parameters must share one dtype")
+    table = (AdamWTensor * max(len(params), 1))()
+    for i, (p, g, m, v) in enumerate(params):
+        table[i] = AdamWTensor(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.numel())
+    dt = dts.pop() if dts else 0
+    st = lib().inf_adamw_step_multi(ctypes.cast(table, ctypes.POINTER(AdamWTensor)), len(params), float(lr),
+                                    float(beta1), float(beta2), float(eps), float(weight_decay), bc1, bc2, dt,
+                                    _stream(stream))
+    _check(st, "inf_adamw_step_multi")
+
+
 def col_sum(x, out=None, accumulate=False, stream=None):
     rows, cols = x.shape
     out = torch.empty(cols, dtype=torch.float32, device=x.device) if out is None else out

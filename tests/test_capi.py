@@ -110,6 +110,27 @@ def test_workspace_sizes():
         ia.workspace_bytes(9, 1, 1, 8, 8, 64)
 
 
+def test_adamw_multi_validation():
+    L = ia.lib()
+    T = ia.AdamWTensor
+    args = (1e-3, 0.9, 0.95, 1e-8, 0.1, 0.1, 0.05)
+
+    def call(entries, dt=ia.INF_F32, bc=args):
+        table = (T * max(len(entries), 1))(*entries)
+        return L.inf_adamw_step_multi(ctypes.cast(table, ctypes.POINTER(T)), len(entries), *bc, dt, None)
+
+    ok = T(FAKE, FAKE, FAKE, FAKE, 10)
+    assert call([]) == 0                                            # nothing to do
+    assert L.inf_adamw_step_multi(None, 1, *args, ia.INF_F32, None) == 1
+    assert call([ok, T(FAKE, None, FAKE, FAKE, 10)]) == 1          # null gradient
+    assert call([ok, T(FAKE, FAKE, FAKE, FAKE, -1)]) == 2          # negative size
+    assert call([ok], dt=7) == 4
+    assert call([T(FAKE + 4, FAKE, FAKE, FAKE, 10)]) == 7          # fp32 p needs 16 bytes
+    assert call([T(FAKE, FAKE, FAKE + 8, FAKE, 10)]) == 7          # m needs 16 bytes
+    assert call([T(FAKE, FAKE + 4, FAKE, FAKE, 10)], dt=ia.INF_BF16) == 7  # bf16 g needs 8 bytes
+    assert call([ok], bc=args[:5] + (0.0, 0.05)) == 8              # bias correction must be > 0
+
+
 def test_bwd_validation():
     L = ia.lib()
     s = dense(1, 1, 8, 64)

@@ -168,6 +168,28 @@ def test_adamw_parity(ia, step):
     assert oracle.rel_err(host(Mm), mr) < TOL and oracle.rel_err(host(V), vr) < TOL
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_adamw_multi_matches_single(ia, bf16):
+    """The multi-tensor step equals the per-tensor step bit for bit: 60 tensors (two launches of
+    at most 48), sizes with ragged tails, one tensor larger than a 1024-element group."""
+    print(f"[case] adamw multi bf16={bf16}", flush=True)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    sizes = [1, 3, 4, 5, 1023, 1024, 1025, 768 * 2304 + 7] + [17 * (i + 1) for i in range(52)]
+    a, b = [], []
+    for i, n in enumerate(sizes):
+        p, g = rnd(100 + i, (n,), 0.02), rnd(200 + i, (n,), 0.01)
+        m, v = rnd(300 + i, (n,), 0.001), np.abs(rnd(400 + i, (n,), 1e-5))
+        a.append((dev(p).to(dt), dev(g).to(dt), dev(m), dev(v)))
+        b.append(tuple(t.clone() for t in a[-1]))
+    for step in (1, 2):
+        for P, G, M, V in a:
+            ia.adamw_step(P, G, M, V, step)
+        ia.adamw_step_multi(b, step)
+    torch.cuda.synchronize()
+    for (P, _, M, V), (P2, _, M2, V2) in zip(a, b):
+        assert torch.equal(P, P2) and torch.equal(M, M2) and torch.equal(V, V2)
+
+
 # ----------------------------------------------------------- reductions, bcast
 @pytest.mark.parametrize("rows,cols", [(8192, 768), (1, 5), (300, 3072)])
 def test_col_sum_parity(ia, rows, cols):
