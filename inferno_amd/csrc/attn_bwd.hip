@@ -155,28 +155,59 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
     q_begin = (q_begin / BQ) * BQ;
     const float c = p.c;
 
-    for (int q0 = q_begin; q0 < p.Tq; q0 += BQ) {
-        // ---- stage the query tile ----------------------------------------------
+    // Query-tile staging.  With PF (D <= 64, where the registers fit) the next
+    // tile's Q, dO, LSE and delta are loaded into registers while the current
+    // tile computes and stored to LDS right after the dS barrier, when every
+    // wave is done with the staged copies: two barriers per tile.  The
+    // prefetch is straight-line (a row limit of 0 past the last tile) and keeps
+    // raw values, so no wait for it lands inside the MFMA blocks.
+    constexpr bool PF = D <= 64;
+    f32x4 ra[QLPT], rd[QLPT];
+    float r_lse = 0.f, r_dl = 0.f;
+    auto gload_q = [&](int q0, int lim) {
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
             const int f = tid + 256 * i;
-            const int r = f / C4;
+            const int qi = q0 + f / C4;
             const int c4 = f % C4;
-            const int qi = q0 + r;
-            f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, d = a;
-            if (qi < p.Tq) {
-                a = ld4(Q + (int64_t)qi * p.sq.t + 4 * c4);
-                d = ld4(dO + (int64_t)qi * p.sdo.t + 4 * c4);
+            ra[i] = rd[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (qi < lim) {
+                ra[i] = ld4(Q + (int64_t)qi * p.sq.t + 4 * c4);
+                rd[i] = ld4(dO + (int64_t)qi * p.sdo.t + 4 * c4);
             }
-            *reinterpret_cast<f32x4*>(&Qs[r][4 * c4]) = a;
-            *reinterpret_cast<f32x4*>(&dOs[r][4 * c4]) = d;
+        }
+        r_lse = r_dl = 0.f;
+        if (tid < BQ && q0 + tid < lim) {
+            r_lse = LSE[q0 + tid];
+            r_dl = DL[q0 + tid];
+        }
+    };
+    auto sstore_q = [&]() {
+#pragma unroll
+        for (int i = 0; i < QLPT; ++i) {
+            const int f = tid + 256 * i;
+            *reinterpret_cast<f32x4*>(&Qs[f / C4][4 * (f % C4)]) = ra[i];
+            *reinterpret_cast<f32x4*>(&dOs[f / C4][4 * (f % C4)]) = rd[i];
         }
         if (tid < BQ) {
-            const int qi = q0 + tid;
-            lse_s[tid] = (qi < p.Tq) ? LSE[qi] * kLog2e : 0.f;
-            dl_s[tid] = (qi < p.Tq) ? DL[qi] : 0.f;
+            lse_s[tid] = r_lse;  // natural-log LSE; scaled by log2(e) where it is read
+            dl_s[tid] = r_dl;
         }
+    };
+    if constexpr (PF) {
+        gload_q(q_begin, p.Tq);
+        sstore_q();
         __syncthreads();
+    }
+
+    for (int q0 = q_begin; q0 < p.Tq; q0 += BQ) {
+        if constexpr (PF) {
+            gload_q(q0 + BQ, q0 + BQ < p.Tq ? p.Tq : 0);
+        } else {
+            gload_q(q0, p.Tq);
+            sstore_q();
+            __syncthreads();
+        }
 
         // Does any query of this tile see any key of this wave?
         const bool active = !p.causal || (q0 + BQ - 1 + p.off >= k0w);
@@ -199,7 +230,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
             // P and dS; reg r holds query row 8*(r/4) + 4*g + r%4 of the tile.
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]);
+                const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLog2e;
                 const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
 #pragma unroll
                 for (int cc = 0; cc < 4; ++cc) {
@@ -228,6 +259,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
 #pragma unroll
         for (int r = 0; r < 16; ++r) dSs[8 * (r >> 2) + 4 * g + (r & 3)][wave * 32 + l32] = ds[r];
         __syncthreads();
+        if constexpr (PF) sstore_q();  // the next tile (zeros after the last one, never read)
 
         // ---- dQ tile (32 x D) += dS (32 x 128) K (128 x D) ---------------------
 #pragma unroll
