@@ -46,6 +46,19 @@ Tensor cross_entropy(const Tensor& logits, const Tensor& target);
 // MultiHeadAttentionFast4::forward (main.cpp:712-764).
 Tensor qkv_attention(const Tensor& qkv, size_t num_heads, bool causal = true, float scale = NAN);
 
+// Upper triangle of the last two dimensions: element (..., r, c) kept when
+// c - r >= diagonal, else zero; any dtype, dense output, no gradient
+// (ops.cpp:1355-1398, cpu_triu cpuops.h:617-656).  Rank < 2 throws (the
+// reference logs an error and exits).
+Tensor triu(const Tensor& A, int diagonal);
+
+// value where mask != 0, input elsewhere; the integer mask (Int32, Int8 or Bool)
+// broadcasts from the right, size-1 dimensions repeating; value converted to
+// the input dtype as static_cast<AT>(value); dense output, no gradient
+// (ops.cpp:1235-1289, cpu_masked_fill cpuops.h:659-705).  A mask that does not
+// broadcast throws (the reference does not check it).
+Tensor masked_fill(const Tensor& input, const Tensor& mask, float value);
+
 // Sums g over the dimensions that broadcasting expanded, to `shape`
 // (sum_to_shape, src/inferno/core/broadcastops.cpp:19-106).  HIP tensors: the
 // expanded dimensions must be leading ones.

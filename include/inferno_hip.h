@@ -159,6 +159,25 @@ enum { INF_BIN_ADD = 0, INF_BIN_MUL = 1 };
 int inf_binary(int op, const void* a, const void* b, void* out, int64_t n, int a_scalar, int b_scalar,
                inf_dtype dt, void* stream);
 
+/* triu of a strided view into a dense output of `shape` (rank 2..8, element
+ * strides): element (..., r, c) is copied when c - r >= diagonal, else written
+ * as all-zero bits; elem_bytes 1, 2, 4 or 8 (the copy is bit-exact for any
+ * dtype).  Replaces cuda_triu (src/inferno/cuda/cudatri.cu:8-89) behind
+ * triu (src/inferno/core/ops.cpp:1355-1398). */
+int inf_triu(const void* a, const int64_t* a_strides, void* out, int rank, const int64_t* shape, int diagonal,
+             int elem_bytes, void* stream);
+
+/* out (dense, `shape`) = mask != 0 ? fill : in, for the strided view `in` and an
+ * integer mask (mask_bytes 1, 4 or 8) broadcast from the right: mask_rank <=
+ * rank and each mask dimension equal to the input's or 1 (size-1 dimensions
+ * repeat; anything else is INF_ERR_BAD_SHAPE).  fill_bits holds the fill
+ * value's bit pattern in the input's element type (elem_bytes 1, 2, 4 or 8).
+ * Replaces cuda_masked_fill (src/inferno/cuda/cudamaskedfill.cu:23-164) behind
+ * masked_fill (src/inferno/core/ops.cpp:1235-1289). */
+int inf_masked_fill(const void* in, const int64_t* in_strides, const void* mask, const int64_t* mask_shape,
+                    const int64_t* mask_strides, int mask_rank, int mask_bytes, void* out, int rank,
+                    const int64_t* shape, uint64_t fill_bits, int elem_bytes, void* stream);
+
 /* Strided copy: for every index tuple idx over `shape` (rank <= 8),
  * dst[sum_d idx_d * dst_strides[d]] = src[sum_d idx_d * src_strides[d]]
  * (element strides, elem_bytes 1, 2, 4 or 8).  With dense dst_strides this is

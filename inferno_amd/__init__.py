@@ -45,6 +45,8 @@ EXPORTS = (
     "inf_fill",
     "inf_binary",
     "inf_copy_strided",
+    "inf_triu",
+    "inf_masked_fill",
     "inf_nn_workspace_bytes",
     "inf_gemm",
     "inf_layernorm_fwd",
@@ -122,6 +124,10 @@ def lib() -> ctypes.CDLL:
         i64p = ctypes.POINTER(ctypes.c_int64)
         L.inf_copy_strided.argtypes = [vp, i64p, vp, i64p, i32, i64p, i32, vp]
         L.inf_copy_strided.restype = i32
+        L.inf_triu.argtypes = [vp, i64p, vp, i32, i64p, i32, i32, vp]
+        L.inf_triu.restype = i32
+        L.inf_masked_fill.argtypes = [vp, i64p, vp, i64p, i64p, i32, i32, vp, i32, i64p, ctypes.c_uint64, i32, vp]
+        L.inf_masked_fill.restype = i32
         sz = ctypes.c_size_t
         L.inf_nn_workspace_bytes.argtypes = [i32, i64, i64, ctypes.POINTER(sz)]
         L.inf_gemm.argtypes = [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64, f32, vp, i64, i64, i64,
@@ -182,9 +188,11 @@ from .ops import (  # noqa: E402  (torch-facing helpers need lib())
     attn_bwd,
     attn_decode,
     attn_fwd,
+    masked_fill,
     softmax_bwd,
     softmax_fwd,
     strides_of,
+    triu,
 )
 from .nn import (  # noqa: E402
     adamw_step,

@@ -47,7 +47,7 @@ def _compile(src: Path, obj: Path) -> None:
 # The C++ Tensor / autograd layer (host code only; g++ with the HIP runtime API headers).
 HOST_LIB = PKG / "libinferno.so"
 CPP = PKG / "cpp"
-CPP_SOURCES = ["dtype.cpp", "storage.cpp", "hipctx.cpp", "tensor.cpp", "engine.cpp", "softmax.cpp", "attention.cpp",
+CPP_SOURCES = ["dtype.cpp", "storage.cpp", "hipctx.cpp", "tensor.cpp", "engine.cpp", "softmax.cpp", "attention.cpp", "mask_ops.cpp",
                "nn_ops.cpp", "modules.cpp", "checkpoint.cpp"]
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 CXX = os.environ.get("CXX", "g++")

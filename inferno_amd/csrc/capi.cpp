@@ -272,6 +272,59 @@ int inf_binary(int op, const void* a, const void* b, void* out, int64_t n, int a
                                          dt == INF_BF16, (hipStream_t)stream));
 }
 
+int inf_triu(const void* a, const int64_t* a_strides, void* out, int rank, const int64_t* shape, int diagonal,
+             int elem_bytes, void* stream) {
+    if (rank < 2) return INF_ERR_BAD_SHAPE;
+    if (rank > inf::kMaxRank) return INF_ERR_UNSUPPORTED;
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) return INF_ERR_BAD_DTYPE;
+    if (!shape || !a_strides) return INF_ERR_NULL_POINTER;
+    inf::StridedCopy c{};
+    c.ndim = rank;
+    c.n = 1;
+    for (int d = 0; d < rank; ++d) {
+        if (shape[d] < 0) return INF_ERR_BAD_SHAPE;
+        if (a_strides[d] < 0) return INF_ERR_BAD_STRIDE;
+        c.shape[d] = shape[d];
+        c.sstride[d] = a_strides[d];
+        c.n *= shape[d];
+    }
+    if (c.n == 0) return INF_OK;
+    if (!a || !out) return INF_ERR_NULL_POINTER;
+    return hip_status(inf::launch_triu(a, out, c, diagonal, elem_bytes, (hipStream_t)stream));
+}
+
+int inf_masked_fill(const void* in, const int64_t* in_strides, const void* mask, const int64_t* mask_shape,
+                    const int64_t* mask_strides, int mask_rank, int mask_bytes, void* out, int rank,
+                    const int64_t* shape, uint64_t fill_bits, int elem_bytes, void* stream) {
+    if (rank < 0 || mask_rank < 0 || mask_rank > rank) return INF_ERR_BAD_SHAPE;
+    if (rank > inf::kMaxRank) return INF_ERR_UNSUPPORTED;
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) return INF_ERR_BAD_DTYPE;
+    if (mask_bytes != 1 && mask_bytes != 4 && mask_bytes != 8) return INF_ERR_BAD_DTYPE;
+    if ((rank > 0 && (!shape || !in_strides)) || (mask_rank > 0 && (!mask_shape || !mask_strides)))
+        return INF_ERR_NULL_POINTER;
+    inf::MaskedFill m{};
+    m.ndim = rank;
+    m.n = 1;
+    const int lead = rank - mask_rank;
+    for (int d = 0; d < rank; ++d) {
+        if (shape[d] < 0) return INF_ERR_BAD_SHAPE;
+        if (in_strides[d] < 0) return INF_ERR_BAD_STRIDE;
+        m.shape[d] = shape[d];
+        m.istride[d] = in_strides[d];
+        m.n *= shape[d];
+        if (d >= lead) {
+            const int64_t md = mask_shape[d - lead];
+            if (md != 1 && md != shape[d]) return INF_ERR_BAD_SHAPE;  // not broadcastable
+            if (mask_strides[d - lead] < 0) return INF_ERR_BAD_STRIDE;
+            m.mstride[d] = md == 1 ? 0 : mask_strides[d - lead];
+        }
+    }
+    if (m.n == 0) return INF_OK;
+    if (!in || !mask || !out) return INF_ERR_NULL_POINTER;
+    return hip_status(inf::launch_masked_fill(in, mask, out, m, elem_bytes, mask_bytes, fill_bits,
+                                              (hipStream_t)stream));
+}
+
 int inf_copy_strided(const void* src, const int64_t* src_strides, void* dst,
                      const int64_t* dst_strides, int ndim, const int64_t* shape, int elem_bytes,
                      void* stream) {

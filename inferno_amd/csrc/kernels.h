@@ -234,6 +234,20 @@ int launch_binary(int op, const void* a, const void* b, void* out, int64_t n, in
                   int bf16, hipStream_t s);
 int launch_copy_strided(const void* src, void* dst, const StridedCopy& c, int elem_bytes, hipStream_t s);
 
+// triu of a strided view into a dense output: StridedCopy's shape / sstride
+// describe the source (dstride unused).
+int launch_triu(const void* src, void* dst, const StridedCopy& c, int diagonal, int elem_bytes, hipStream_t s);
+
+struct MaskedFill {       // element strides; mstride is the mask's, padded on the left, 0 where it repeats
+    int ndim;
+    int64_t n;
+    int64_t shape[kMaxRank];
+    int64_t istride[kMaxRank];
+    int64_t mstride[kMaxRank];
+};
+int launch_masked_fill(const void* in, const void* mask, void* out, const MaskedFill& m, int elem_bytes,
+                       int mask_bytes, uint64_t fill_bits, hipStream_t s);
+
 // Tile shapes the host needs for grids and workspace sizing.
 constexpr int kFwdBM = 128;      // query rows per forward workgroup
 constexpr int kBwdBK = 128;      // keys per backward workgroup

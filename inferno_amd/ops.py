@@ -132,3 +132,32 @@ def softmax_bwd(y, dy, out=None, stream=None):
                                out.stride(0) if rows > 1 else cols, _dt(y), _stream(stream))
     _check(st, "inf_softmax_bwd")
     return out.reshape(y.shape)
+
+
+def _i64(vals):
+    import ctypes
+
+    return (ctypes.c_int64 * max(len(vals), 1))(*vals)
+
+
+def triu(a, diagonal, stream=None):
+    """Dense triu of any [..., R, C] view (any dtype; elements copied bit for bit)."""
+    out = torch.empty(a.shape, dtype=a.dtype, device=a.device)
+    st = lib().inf_triu(a.data_ptr(), _i64(a.stride()), out.data_ptr(), a.dim(), _i64(a.shape), int(diagonal),
+                        a.element_size(), _stream(stream))
+    _check(st, "inf_triu")
+    return out
+
+
+def masked_fill(x, mask, value, stream=None):
+    """Dense out = mask != 0 ? value : x, the integer mask broadcast from the right."""
+    import numpy as np
+
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    fill = torch.tensor([value], dtype=torch.float32).to(x.dtype)  # static_cast<AT>(value)
+    bits = int(np.frombuffer(fill.view(torch.uint8).numpy().tobytes() + bytes(8), dtype=np.uint64, count=1)[0])
+    st = lib().inf_masked_fill(x.data_ptr(), _i64(x.stride()), mask.data_ptr(), _i64(mask.shape),
+                               _i64(mask.stride()), mask.dim(), mask.element_size(), out.data_ptr(), x.dim(),
+                               _i64(x.shape), bits, x.element_size(), _stream(stream))
+    _check(st, "inf_masked_fill")
+    return out

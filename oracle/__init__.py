@@ -109,6 +109,22 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
     return out
 
 
+def triu_ones(rows: int, cols: int, diagonal: int) -> np.ndarray:
+    """triu(ones[rows, cols], diagonal) as Int32 (cpu_triu, cpuops.h:617-656)."""
+    out = np.empty((rows, cols), dtype=np.int32)
+    lib().orc_triu_ones_i32(out, rows, cols, int(diagonal))
+    return out
+
+
+def masked_fill(x: np.ndarray, mask: np.ndarray, fill: float) -> np.ndarray:
+    """(mask != 0) ? fill : x for a [rows, cols] fp32 x and Int32 mask (cpu_masked_fill)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    mask = np.ascontiguousarray(mask, dtype=np.int32)
+    out = np.empty_like(x)
+    lib().orc_masked_fill_f32(x, mask, np.float32(fill), out, x.shape[0], x.shape[1])
+    return out
+
+
 def bf16_to_f32(b: np.ndarray) -> np.ndarray:
     b = np.ascontiguousarray(b, dtype=np.uint16)
     out = np.empty(b.shape, dtype=np.float32)

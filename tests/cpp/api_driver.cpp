@@ -20,6 +20,14 @@
 //       reads q.bin kc.bin vc.bin, writes o.bin.
 //   api_driver ckpt-save|ckpt-load <file> <cpu|hip>
 //       Checkpoint round trips of a small module tree (see cmd_ckpt).
+//   api_driver mask <dir> <cpu|hip>
+//       triu / masked_fill cases on index-pattern inputs (see cmd_mask); writes
+//       each result's raw bytes to <dir>/<case>.bin.
+//   api_driver chain <dir> <B> <H> <T> <D> <cpu|hip>
+//       the reference's unfused attention chain (InfernoApp/main.cpp:732-754)
+//       on q.bin k.bin v.bin: kt = k^T contiguous, S = matmul(q, kt) * scale,
+//       masked_fill(S, triu(ones[1,1,T,T] Int32, 1), -1e9f), Softmax, matmul with
+//       v; writes y.bin and the mask's raw bytes mask.bin.
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -372,6 +380,76 @@ static int cmd_ckpt(int argc, char** argv) {
     return 0;
 }
 
+static void write_raw(const std::string& path, const Tensor& t) {
+    const Tensor h = t.to(Device::cpu());
+    if (!h.is_contiguous()) throw Error("write_raw: expected a dense tensor");
+    std::ofstream f(path, std::ios::binary);
+    f.write(static_cast<const char*>(h.data_ptr()), (std::streamsize)(h.numel() * dtype_size(h.dtype())));
+}
+
+// Index-pattern input: element i = i * step + base, converted to dt.
+static Tensor pattern(DType dt, const std::vector<size_t>& shape, float step, float base, Device dev) {
+    size_t n = 1;
+    for (size_t d : shape) n *= d;
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; ++i) v[i] = (float)i * step + base;
+    return Tensor(dt, v, shape, "pattern", dev);
+}
+
+static int cmd_mask(int argc, char** argv) {
+    if (argc < 4) throw Error("usage: mask <dir> <cpu|hip>");
+    const std::string dir = argv[2];
+    const Device dev = parse_dev(argv[3]);
+    const Tensor a = pattern(DType::Float32, {2, 3, 5, 7}, 0.5f, -10.f, dev);
+    const Tensor at = a.transpose(2, 3);  // [2, 3, 7, 5], a strided view
+    for (int dg : {-2, 0, 1, 3}) {
+        write_raw(dir + "/triu_f32_" + std::to_string(dg + 2) + ".bin", triu(a, dg));
+        write_raw(dir + "/triu_f32t_" + std::to_string(dg + 2) + ".bin", triu(at, dg));
+    }
+    const Tensor ones(DType::Int32, std::vector<int>(6 * 9, 1), {1, 1, 6, 9}, "ones", dev);
+    const Tensor causal = triu(ones, 1);
+    write_raw(dir + "/triu_i32.bin", causal);
+    write_raw(dir + "/triu_bf16.bin", triu(pattern(DType::BFloat16, {4, 6}, 0.25f, -3.f, dev), -1));
+    const Tensor m57 = triu(Tensor(DType::Int32, std::vector<int>(5 * 7, 1), {5, 7}, "ones57", dev), 1);
+    write_raw(dir + "/mf_f32.bin", masked_fill(a, m57, -1e9f));
+    const Tensor m75 = triu(Tensor(DType::Int32, std::vector<int>(7 * 5, 1), {7, 5}, "ones75", dev), 0);
+    write_raw(dir + "/mf_f32t.bin", masked_fill(at, m75, 2.5f));
+    write_raw(dir + "/mf_i8.bin", masked_fill(a, pattern(DType::Int8, {1, 7}, 1.f, -3.f, dev), 7.f));
+    write_raw(dir + "/mf_bool.bin", masked_fill(a, pattern(DType::Bool, {3, 1, 1}, 1.f, 0.f, dev), -1.f));
+    std::vector<int> every3(2 * 5 * 7);
+    for (size_t i = 0; i < every3.size(); ++i) every3[i] = i % 3 == 0 ? 1 : 0;
+    write_raw(dir + "/mf_bf16.bin", masked_fill(pattern(DType::BFloat16, {2, 3, 5, 7}, 0.25f, -7.f, dev),
+                                                Tensor(DType::Int32, every3, {2, 1, 5, 7}, "every3", dev), -1e9f));
+    write_raw(dir + "/mf_i32.bin",
+              masked_fill(pattern(DType::Int32, {4, 6}, 3.f, -20.f, dev), pattern(DType::Bool, {6}, 1.f, -2.f, dev),
+                          -3.7f));
+    return 0;
+}
+
+static int cmd_chain(int argc, char** argv) {
+    if (argc < 8) throw Error("usage: chain <dir> B H T D cpu|hip");
+    const std::string dir = argv[2];
+    const size_t B = std::stoul(argv[3]), H = std::stoul(argv[4]), T = std::stoul(argv[5]), D = std::stoul(argv[6]);
+    const Device dev = parse_dev(argv[7]);
+    const size_t n = B * H * T * D;
+    NoGradGuard ng;
+    const Tensor q(DType::Float32, read_f32(dir + "/q.bin", n), {B, H, T, D}, "q", dev);
+    const Tensor k(DType::Float32, read_f32(dir + "/k.bin", n), {B, H, T, D}, "k", dev);
+    const Tensor v(DType::Float32, read_f32(dir + "/v.bin", n), {B, H, T, D}, "v", dev);
+    const Tensor kt = k.transpose(-1, -2).contiguous();
+    Tensor scores = matmul(q, kt, "QK ^ T");
+    const float scale = 1.0f / std::sqrt(static_cast<float>(D));
+    scores = scores * scale;
+    const Tensor ones(DType::Int32, std::vector<int>(T * T, 1), {1, 1, T, T}, "causal_mask_ones", dev);
+    const Tensor mask = triu(ones, 1);
+    scores = masked_fill(scores, mask, -1e9f);
+    const Tensor attn = Softmax(scores, -1).contiguous();
+    const Tensor y = matmul(attn, v, "attn@V");
+    write_raw(dir + "/y.bin", y);
+    write_raw(dir + "/mask.bin", mask);
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc < 2) {
         std::cerr << "usage: api_driver selftest|attn|softmax|decode ...\n";
@@ -384,6 +462,8 @@ int main(int argc, char** argv) {
         if (cmd == "softmax") return cmd_softmax(argc, argv);
         if (cmd == "decode") return cmd_decode(argc, argv);
         if (cmd == "ckpt-save" || cmd == "ckpt-load") return cmd_ckpt(argc, argv);
+        if (cmd == "mask") return cmd_mask(argc, argv);
+        if (cmd == "chain") return cmd_chain(argc, argv);
         std::cerr << "unknown command " << cmd << "\n";
         return 2;
     } catch (const std::exception& e) {

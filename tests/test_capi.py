@@ -131,6 +131,29 @@ def test_adamw_multi_validation():
     assert call([ok], bc=args[:5] + (0.0, 0.05)) == 8              # bias correction must be > 0
 
 
+def test_triu_masked_fill_validation():
+    L = ia.lib()
+    i64 = lambda *v: (ctypes.c_int64 * len(v))(*v)  # noqa: E731
+    sh, st = i64(3, 4), i64(4, 1)
+    assert L.inf_triu(FAKE, st, FAKE, 1, i64(4), 0, 4, None) == 2       # rank < 2
+    assert L.inf_triu(FAKE, st, FAKE, 2, sh, 0, 3, None) == 4           # element size
+    assert L.inf_triu(FAKE, i64(4, -1), FAKE, 2, sh, 0, 4, None) == 3   # negative stride
+    assert L.inf_triu(None, st, FAKE, 2, sh, 0, 4, None) == 1
+    assert L.inf_triu(None, st, None, 2, i64(0, 4), 0, 4, None) == 0     # empty: nothing to do
+    ms, mst = i64(1, 4), i64(4, 1)
+    args = lambda **k: dict(dict(inp=FAKE, ist=st, mask=FAKE, msh=ms, mst=mst, mrank=2, mbytes=4, out=FAKE,  # noqa
+                                 rank=2, shape=sh, fill=0, eb=4), **k)
+    call = lambda a: L.inf_masked_fill(a["inp"], a["ist"], a["mask"], a["msh"], a["mst"], a["mrank"],  # noqa
+                                       a["mbytes"], a["out"], a["rank"], a["shape"], a["fill"], a["eb"], None)
+    assert call(args(msh=i64(2, 4))) == 2            # mask dim 2 vs input 3: does not broadcast
+    assert call(args(mrank=3, msh=i64(1, 1, 4), mst=i64(4, 4, 1))) == 2  # mask rank > input rank
+    assert call(args(mbytes=2)) == 4                 # mask element size
+    assert call(args(eb=5)) == 4
+    assert call(args(mst=i64(4, -1))) == 3
+    assert call(args(mask=None)) == 1
+    assert call(args(shape=i64(3, 0), msh=i64(1, 0))) == 0  # empty
+
+
 def test_bwd_validation():
     L = ia.lib()
     s = dense(1, 1, 8, 64)

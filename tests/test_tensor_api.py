@@ -111,8 +111,98 @@ def test_error_paths_cpu(tmp_path):
     assert r.returncode == 3 and "cannot read" in r.stderr
 
 
+def pattern(shape, step, base):
+    n = int(np.prod(shape))
+    return (np.arange(n, dtype=np.float32) * np.float32(step) + np.float32(base)).reshape(shape)
+
+
+def mask_expected():
+    """Expected bytes of every `api_driver mask` case: np.triu / np.where on the driver's inputs."""
+    a = pattern((2, 3, 5, 7), 0.5, -10.0)
+    at = np.swapaxes(a, 2, 3)
+    exp = {}
+    for dg in (-2, 0, 1, 3):
+        exp[f"triu_f32_{dg + 2}"] = np.triu(a, dg)
+        exp[f"triu_f32t_{dg + 2}"] = np.triu(at, dg)
+    exp["triu_i32"] = np.triu(np.ones((1, 1, 6, 9), np.int32), 1)
+    exp["triu_bf16"] = np.triu(oracle.round_bf16(pattern((4, 6), 0.25, -3.0)), -1)
+    m57 = np.triu(np.ones((5, 7), np.int32), 1)
+    exp["mf_f32"] = np.where(m57 != 0, np.float32(-1e9), a)
+    exp["mf_f32t"] = np.where(np.triu(np.ones((7, 5), np.int32), 0) != 0, np.float32(2.5), at)
+    m_i8 = pattern((1, 7), 1.0, -3.0).astype(np.int8)
+    exp["mf_i8"] = np.where(m_i8 != 0, np.float32(7.0), a)
+    m_bool = pattern((3, 1, 1), 1.0, 0.0) != 0
+    exp["mf_bool"] = np.where(m_bool, np.float32(-1.0), a)
+    every3 = (np.arange(70) % 3 == 0).astype(np.int32).reshape(2, 1, 5, 7)
+    xb = oracle.round_bf16(pattern((2, 3, 5, 7), 0.25, -7.0))
+    fill_b = oracle.round_bf16(np.array([-1e9], np.float32))[0]
+    exp["mf_bf16"] = np.where(every3 != 0, fill_b, xb)
+    xi = pattern((4, 6), 3.0, -20.0).astype(np.int32)
+    exp["mf_i32"] = np.where(pattern((6,), 1.0, -2.0) != 0, np.int32(-3), xi)  # static_cast<int>(-3.7f)
+    return {k: np.ascontiguousarray(v).tobytes() for k, v in exp.items()}
+
+
+def test_mask_ops_cpu_match_numpy(tmp_path):
+    """triu / masked_fill (ops.cpp:1235-1398) on CPU tensors: dtypes f32, bf16, i32; strided views;
+    Int32 / Int8 / Bool masks broadcast from the right -- against np.triu and np.where."""
+    r = run("mask", tmp_path, "cpu")
+    assert r.returncode == 0, r.stdout + r.stderr
+    for name, want in mask_expected().items():
+        assert (tmp_path / f"{name}.bin").read_bytes() == want, name
+
+
+def test_mask_ops_pin_against_oracle():
+    """The causal mask and the -1e9 fill equal the oracle's restatement (itself pinned bit for bit to
+    the reference's cpu_triu / cpu_masked_fill in tests/test_oracle.py)."""
+    T = 9
+    assert np.array_equal(np.triu(np.ones((T, T), np.int32), 1), oracle.triu_ones(T, T, 1))
+    s = oracle.randn(3, (T, T))
+    assert np.array_equal(bits(np.where(np.triu(np.ones((T, T)), 1) != 0, np.float32(-1e9), s)),
+                          bits(oracle.masked_fill(s, oracle.triu_ones(T, T, 1), -1e9)))
+
+
+@pytest.mark.parametrize("B,H,T,D", [(1, 2, 33, 16), (2, 1, 64, 8)])
+def test_reference_chain_cpu_bitwise(tmp_path, B, H, T, D):
+    """The reference's unfused attention chain (main.cpp:732-754: transpose, contiguous, matmul,
+    * scale, triu, masked_fill, Softmax, matmul) through this API equals the oracle bit for bit."""
+    q, k, v, _ = oracle.attn_inputs(B, H, T, D, seed=9)
+    write(tmp_path, q=q, k=k, v=v)
+    r = run("chain", tmp_path, B, H, T, D, "cpu")
+    assert r.returncode == 0, r.stdout + r.stderr
+    o_r, _ = oracle.attn_fwd(q, k, v)
+    assert np.array_equal(bits(read(tmp_path, "y", (B, H, T, D))), bits(o_r))
+    assert (tmp_path / "mask.bin").read_bytes() == np.triu(np.ones((T, T), np.int32), 1).tobytes()
+
+
 # ------------------------------------------------------------------ HIP device
 gpu = pytest.mark.gpu
+
+
+@gpu
+def test_mask_ops_hip_equal_cpu(tmp_path):
+    if not have_gpu():
+        pytest.skip("no GPU")
+    print("[case] api_driver mask hip", flush=True)
+    r = run("mask", tmp_path, "hip")
+    assert r.returncode == 0, r.stdout + r.stderr
+    for name, want in mask_expected().items():
+        assert (tmp_path / f"{name}.bin").read_bytes() == want, name
+
+
+@gpu
+def test_reference_chain_hip(tmp_path):
+    """The unfused chain on HIP tensors: the causal mask bit-exact, y within the fp32 bar."""
+    if not have_gpu():
+        pytest.skip("no GPU")
+    print("[case] api_driver chain hip", flush=True)
+    B, H, T, D = 2, 3, 130, 64
+    q, k, v, _ = oracle.attn_inputs(B, H, T, D, seed=9)
+    write(tmp_path, q=q, k=k, v=v)
+    r = run("chain", tmp_path, B, H, T, D, "hip")
+    assert r.returncode == 0, r.stdout + r.stderr
+    o_r, _ = oracle.attn_fwd(q, k, v)
+    assert oracle.rel_err(read(tmp_path, "y", (B, H, T, D)), o_r) <= 1e-4
+    assert (tmp_path / "mask.bin").read_bytes() == np.triu(np.ones((T, T), np.int32), 1).tobytes()
 
 
 @gpu
