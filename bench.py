@@ -184,8 +184,8 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(bwd_tf / peak, 4),
             # HBM bytes per bwd_main launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-            # (x2.00 / x1.00 copy-kernel calibration): 125.7 MB read + 163.6 MB written.
-            "traffic": 289.3e6,
+            # (x2.00 / x1.00 copy-kernel calibration): 191.0 MB read + 163.6 MB written.
+            "traffic": 354.6e6,
             "algorithmic_flop_per_launch": F_bwd,
             "avg_launch_ms": round(bwd_ms, 4),
         },
