@@ -18,7 +18,10 @@ namespace Inferno {
 // reference counterpart (the reference has no generation loop; see the
 // commented-out last-position select, InfernoApp/main.cpp:1173-1177).
 struct KVCache {
-    Tensor k, v;
+    // k and v are the two halves of one [2, B, H, capacity, D] buffer `kv`, so
+    // appending a step's keys and values is one strided copy.  A cache built
+    // from separate k / v tensors (kv undefined) is appended with two copies.
+    Tensor kv, k, v;
     size_t length = 0;
     KVCache() = default;
     KVCache(size_t B, size_t H, size_t capacity, size_t D, Device device, DType dtype = DType::Float32);

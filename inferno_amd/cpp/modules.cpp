@@ -190,8 +190,12 @@ Tensor MultiHeadAttention::forward(Tensor& x) {
 }
 
 KVCache::KVCache(size_t B, size_t H, size_t capacity, size_t D, Device device, DType dtype)
-    : k(dtype, std::vector<size_t>{B, H, capacity, D}, "kv_cache_k", device, false),
-      v(dtype, std::vector<size_t>{B, H, capacity, D}, "kv_cache_v", device, false) {}
+    : kv(dtype, std::vector<size_t>{2, B, H, capacity, D}, "kv_cache", device, false) {
+    const std::vector<size_t> shape{B, H, capacity, D};
+    const auto st = Tensor::calculate_strides(shape);
+    k = make_view(kv, shape, st, kv.offset(), "kv_cache_k");
+    v = make_view(kv, shape, st, kv.offset() + B * H * capacity * D, "kv_cache_v");
+}
 
 namespace {
 // dst (a view) = src (a view of the same shape), element-wise through strides.
@@ -227,16 +231,32 @@ Tensor MultiHeadAttention::forward_cached(const Tensor& x, KVCache& cache) {
     Tensor q = make_view(qkv, hs, hst, qkv.offset(), "q");
     Tensor knew = make_view(qkv, hs, hst, qkv.offset() + C, "k_new");
     Tensor vnew = make_view(qkv, hs, hst, qkv.offset() + 2 * C, "v_new");
-    Tensor kdst = make_view(cache.k, hs, cache.k.strides(), cache.k.offset() + cache.length * D, "k_slot");
-    Tensor vdst = make_view(cache.v, hs, cache.v.strides(), cache.v.offset() + cache.length * D, "v_slot");
-    copy_view(knew, kdst);
-    copy_view(vnew, vdst);
+    const bool joint = cache.kv.defined() && cache.kv.ndim() == 5 && cache.kv.strides()[0] > 0 &&
+                       GetImpl(cache.k)->storage() == GetImpl(cache.kv)->storage() &&
+                       GetImpl(cache.v)->storage() == GetImpl(cache.kv)->storage() &&
+                       cache.k.offset() == cache.kv.offset() &&
+                       cache.v.offset() == cache.kv.offset() + cache.kv.strides()[0] &&
+                       cache.k.strides() == std::vector<size_t>(cache.kv.strides().begin() + 1, cache.kv.strides().end());
+    if (joint) {
+        // keys and values of the step in one copy: source [2, B, H, t, D] out of
+        // qkv (k at column C, v at 2C), destination slots of both cache halves
+        Tensor kvnew = make_view(qkv, {2, B, H, t, D}, {C, t * 3 * C, D, 3 * C, 1}, qkv.offset() + C, "kv_new");
+        Tensor kvdst = make_view(cache.kv, {2, B, H, t, D}, cache.kv.strides(), cache.kv.offset() + cache.length * D,
+                                 "kv_slot");
+        copy_view(kvnew, kvdst);
+    } else {
+        Tensor kdst = make_view(cache.k, hs, cache.k.strides(), cache.k.offset() + cache.length * D, "k_slot");
+        Tensor vdst = make_view(cache.v, hs, cache.v.strides(), cache.v.offset() + cache.length * D, "v_slot");
+        copy_view(knew, kdst);
+        copy_view(vnew, vdst);
+    }
     cache.length += t;
     const std::vector<size_t> all{B, H, cache.length, D};
     Tensor kall = make_view(cache.k, all, cache.k.strides(), cache.k.offset(), "k_cache");
     Tensor vall = make_view(cache.v, all, cache.v.strides(), cache.v.offset(), "v_cache");
     Tensor y4 = t == 1 ? attention_decode(q, kall, vall) : scaled_dot_product_attention(q, kall, vall, true);
-    Tensor y = y4.transpose(1, 2).contiguous().reshape({B, t, C});
+    // [B, H, t, D] -> [B, t, C]; at t = 1 the dense [B, H, 1, D] already has that layout
+    Tensor y = t == 1 ? y4.reshape({B, 1, C}) : y4.transpose(1, 2).contiguous().reshape({B, t, C});
     return W_out.forward(static_cast<const Tensor&>(y));
 }
 
