@@ -59,6 +59,12 @@ Tensor triu(const Tensor& A, int diagonal);
 // broadcast throws (the reference does not check it).
 Tensor masked_fill(const Tensor& input, const Tensor& mask, float value);
 
+// Index of the largest element along the last dimension -- the first one on
+// ties, as std::max_element picks -- as Int32 [...] for x [..., n]; no
+// gradient.  No counterpart in the reference (it has no generation loop): the
+// greedy next-token pick, so only the indices leave the device.
+Tensor argmax(const Tensor& x);
+
 // Sums g over the dimensions that broadcasting expanded, to `shape`
 // (sum_to_shape, src/inferno/core/broadcastops.cpp:19-106).  HIP tensors: the
 // expanded dimensions must be leading ones.

@@ -310,6 +310,12 @@ int inf_col_sum(const void* x, int64_t rows, int64_t cols, int64_t ldx, float* o
 int inf_binary_bcast(int op, const void* a, const void* b, void* out, int64_t n, int64_t nb, inf_dtype dt,
                      void* stream);
 
+/* out[r] = the column index of the largest element of row r of x [rows, cols]
+ * (row stride ld elements), the first one on ties -- std::max_element's pick.
+ * No counterpart in the reference, which has no generation loop: the greedy
+ * next-token choice, so only rows int32 values leave the device. */
+int inf_argmax_rows(const void* x, int64_t rows, int64_t cols, int64_t ld, int32_t* out, inf_dtype dt, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,7 @@ EXPORTS = (
     "inf_adamw_step_multi",
     "inf_col_sum",
     "inf_binary_bcast",
+    "inf_argmax_rows",
     "inf_last_error_detail",
 )
 
@@ -146,6 +147,7 @@ def lib() -> ctypes.CDLL:
                                            vp]
         L.inf_col_sum.argtypes = [vp, i64, i64, i64, vp, i32, i32, vp, sz, vp]
         L.inf_binary_bcast.argtypes = [i32, vp, vp, vp, i64, i64, i32, vp]
+        L.inf_argmax_rows.argtypes = [vp, i64, i64, i64, vp, i32, vp]
         for name in EXPORTS[11:-1]:
             getattr(L, name).restype = i32
         L.inf_last_error_detail.argtypes = []
@@ -197,6 +199,7 @@ from .ops import (  # noqa: E402  (torch-facing helpers need lib())
 from .nn import (  # noqa: E402
     adamw_step,
     adamw_step_multi,
+    argmax_rows,
     col_sum,
     cross_entropy_bwd,
     cross_entropy_fwd,

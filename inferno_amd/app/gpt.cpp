@@ -319,14 +319,11 @@ static int run_generate(int argc, char** argv) {
     std::vector<int32_t> prompt(B * P);
     for (auto& t : prompt) t = tokd(rng);
     auto argmax_last = [&](const Tensor& logits) {
-        // only the last position's logits leave the device ([B, V])
+        // the greedy pick of the last position on the device; B indices leave it
         const size_t t = logits.shape()[1];
-        auto h = logits.slice(1, t - 1, t - 1).to_host_float();
+        const std::vector<double> h = argmax(logits.slice(1, t - 1, t - 1)).to_host_double();
         std::vector<int32_t> nxt(B);
-        for (size_t b = 0; b < B; ++b) {
-            const float* row = &h[b * V];
-            nxt[b] = (int32_t)(std::max_element(row, row + V) - row);
-        }
+        for (size_t b = 0; b < B; ++b) nxt[b] = (int32_t)h[b];
         return nxt;
     };
     auto run_once = [&](double* prefill_ms, double* decode_ms, std::vector<int32_t>* out) {

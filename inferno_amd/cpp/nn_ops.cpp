@@ -261,6 +261,58 @@ void MMBackward::get_inputs(std::vector<Tensor>& out) const {
 // ============================================================================
 // sum_to_shape
 // ============================================================================
+Tensor argmax(const Tensor& x) {
+    if (x.ndim() < 1 || x.shape().back() == 0) throw Error("argmax: needs a non-empty last dimension");
+    if (x.strides().back() != 1 && x.shape().back() > 1) throw Error("argmax: the last dimension must be dense");
+    const std::vector<size_t> oshape(x.shape().begin(), x.shape().end() - 1);
+    Tensor out(DType::Int32, oshape, "argmax", x.device(), false);
+    const size_t cols = x.shape().back();
+    const size_t rows = out.numel();
+    // Rows of x as one strided sequence: the leading dimensions other than
+    // size-1 ones must collapse into one stride; otherwise work on a dense copy.
+    Tensor src = x;
+    size_t ld = cols;
+    {
+        std::vector<std::pair<size_t, size_t>> lead;  // (size, stride) of the non-trivial leading dims
+        for (size_t d = 0; d + 1 < x.ndim(); ++d)
+            if (x.shape()[d] != 1) lead.emplace_back(x.shape()[d], x.strides()[d]);
+        bool ok = true;
+        for (size_t i = 0; i + 1 < lead.size(); ++i)
+            if (lead[i].second != lead[i + 1].second * lead[i + 1].first) ok = false;
+        if (!lead.empty()) ld = lead.back().second;
+        if (!ok || ld < cols) {
+            NoGradGuard ng;
+            src = detail::dense_copy(x);
+            ld = cols;
+        }
+    }
+    if (rows == 0) return out;
+    if (x.device().is_cpu()) {
+        const char* p = static_cast<const char*>(src.data_ptr());
+        const size_t esz = dtype_size(x.dtype());
+        int32_t* o = static_cast<int32_t*>(out.data_ptr());
+        for (size_t r = 0; r < rows; ++r) {
+            size_t best = 0;
+            double bv = detail::load_elem(p + (r * ld) * esz, x.dtype());
+            for (size_t c = 1; c < cols; ++c) {
+                const double v = detail::load_elem(p + (r * ld + c) * esz, x.dtype());
+                if (bv < v) {
+                    bv = v;
+                    best = c;
+                }
+            }
+            o[r] = (int32_t)best;
+        }
+        return out;
+    }
+    DeviceGuard dg(x.device().index);
+    status_check(inf_argmax_rows(src.data_ptr(), (int64_t)rows, (int64_t)cols, (int64_t)ld,
+                                 static_cast<int32_t*>(out.data_ptr()), detail::inf_dt(x.dtype(), "argmax"),
+                                 detail::stream_of(x)),
+                 "inf_argmax_rows");
+    return out;
+}
+
 Tensor sum_to_shape(const Tensor& g, const std::vector<size_t>& shape) {
     if (g.shape() == shape) return g;
     if (shape.size() > g.ndim()) throw Error("sum_to_shape: target has higher rank");

@@ -216,6 +216,7 @@ int launch_embed_fwd(const EmbParams& p, int bf16, hipStream_t s);
 int launch_embed_bwd(const EmbParams& p, hipStream_t s);
 int launch_adamw(const AdamWParams& a, int bf16, hipStream_t s);
 int launch_adamw_multi(const AdamWMultiParams& a, int bf16, hipStream_t s);
+int launch_argmax_rows(const void* x, int64_t rows, int64_t cols, int64_t ld, int32_t* out, int bf16, hipStream_t s);
 int launch_bcast(int op, const void* a, const void* b, void* out, int64_t n, int64_t nb, int vec, int bf16,
                  hipStream_t s);
 

@@ -531,6 +531,38 @@ __global__ __launch_bounds__(256) void bcast_kernel(const void* __restrict__ a, 
 }
 
 // ============================================================================
+// Row argmax (the greedy next-token pick): one wave per row; lanes scan columns
+// lane, lane + 64, ... keeping (value, first index), then a wave reduction in
+// which the larger value wins and equal values keep the smaller index.
+// ============================================================================
+template <typename E>
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
+                                                          int64_t ld, int32_t* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const typename E::T* p = (const typename E::T*)x + row * ld;
+    float best = -INFINITY;
+    int idx = -1;
+    for (int64_t c = lane; c < cols; c += 64) {
+        const float v = E::ld(p + c);
+        if (idx < 0 || v > best) {
+            best = v;
+            idx = (int)c;
+        }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ob = shfl_xor(best, m);
+        const int oi = __shfl_xor(idx, m, 64);
+        const bool take = oi >= 0 && (idx < 0 || ob > best || (ob == best && oi < idx));
+        best = take ? ob : best;
+        idx = take ? oi : idx;
+    }
+    if (lane == 0) out[row] = idx;
+}
+
+// ============================================================================
 // launchers
 // ============================================================================
 namespace {
@@ -669,6 +701,16 @@ int launch_adamw_multi(const AdamWMultiParams& a, int bf16, hipStream_t s) {
         hipLaunchKernelGGL(adamw_multi_kernel<BF16>, grid, dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL(adamw_multi_kernel<F32>, grid, dim3(256), 0, s, a);
+    return (int)hipGetLastError();
+}
+
+int launch_argmax_rows(const void* x, int64_t rows, int64_t cols, int64_t ld, int32_t* out, int bf16,
+                       hipStream_t s) {
+    const dim3 grid(blocks_for(rows, 4));
+    if (bf16)
+        hipLaunchKernelGGL(argmax_rows_kernel<BF16>, grid, dim3(256), 0, s, x, rows, cols, ld, out);
+    else
+        hipLaunchKernelGGL(argmax_rows_kernel<F32>, grid, dim3(256), 0, s, x, rows, cols, ld, out);
     return (int)hipGetLastError();
 }
 

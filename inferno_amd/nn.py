@@ -180,3 +180,12 @@ def binary_bcast(op, a, b, stream=None):
 __all__ = ["gemm", "layernorm_fwd", "layernorm_bwd", "gelu_fwd", "gelu_bwd", "cross_entropy_fwd",
            "cross_entropy_bwd", "embedding_fwd", "embedding_bwd", "adamw_step", "col_sum", "binary_bcast",
            "INF_F32"]
+
+
+def argmax_rows(x, stream=None):
+    """Int32 index of each row's largest element (first on ties) of a [rows, cols] tensor."""
+    rows, cols = x.shape
+    out = torch.empty(rows, dtype=torch.int32, device=x.device)
+    st = lib().inf_argmax_rows(x.data_ptr(), rows, cols, x.stride(0), out.data_ptr(), _dt(x), _stream(stream))
+    _check(st, "inf_argmax_rows")
+    return out

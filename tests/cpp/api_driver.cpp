@@ -225,6 +225,18 @@ static int selftest(Device dev) {
         }
         check(threw, "device_mismatch_throws");
     });
+    run_case("argmax", [&] {
+        // rows: plain, all equal (first index), a tie at 1 and 3, the maximum last
+        Tensor x(DType::Float32, std::vector<float>{0, 5, 2, 1, 7, 7, 7, 7, 1, 9, 0, 9, -4, -3, -2, -1},
+                 {2, 2, 4}, "x", dev);
+        auto got = argmax(x).to_host_double();
+        check(got == std::vector<double>{1, 0, 1, 3}, "argmax_rows_first_on_ties");
+        // a [2, 1, 4] slice with strided rows (the last position of each sequence)
+        auto last = argmax(x.slice(1, 1, 1)).to_host_double();
+        check(last == std::vector<double>{0, 3}, "argmax_strided_rows");
+        check(argmax(x).dtype() == DType::Int32 && argmax(x).shape() == std::vector<size_t>{2, 2},
+              "argmax_shape_dtype");
+    });
     std::cout << (g_fail ? "SELFTEST FAILED " : "SELFTEST OK ") << g_fail << "\n";
     return g_fail;
 }

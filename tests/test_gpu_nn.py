@@ -190,6 +190,27 @@ def test_adamw_multi_matches_single(ia, bf16):
         assert torch.equal(P, P2) and torch.equal(M, M2) and torch.equal(V, V2)
 
 
+@pytest.mark.parametrize("rows,cols,dt", [(32, 8192, "f32"), (5, 1, "f32"), (3, 1000, "bf16"), (7, 65, "f32")])
+def test_argmax_rows(ia, rows, cols, dt):
+    """Row argmax = numpy's argmax (first index on ties): random rows, plus rows of ties and a
+    maximum in the last column; bf16 values compared after rounding."""
+    print(f"[case] argmax {rows}x{cols} {dt}", flush=True)
+    x = rnd(31, (rows, cols))
+    x[0, :] = 1.0                      # all equal: index 0
+    if cols > 3:
+        x[1, 2] = x[1, 3] = 50.0       # tie: first of the two
+        x[2 % rows, -1] = 60.0         # maximum in the last column
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    X = dev(x).to(tdt)
+    got = host(ia.argmax_rows(X)).astype(np.int64)
+    want = np.argmax(X.float().cpu().numpy(), axis=1)
+    assert np.array_equal(got, want)
+    # a strided row view (every other row of a wider buffer)
+    W = torch.zeros((2 * rows, cols + 3), dtype=tdt, device="cuda")
+    W[::2, :cols] = X
+    assert np.array_equal(host(ia.argmax_rows(W[::2, :cols])).astype(np.int64), want)
+
+
 # ----------------------------------------------------------- reductions, bcast
 @pytest.mark.parametrize("rows,cols", [(8192, 768), (1, 5), (300, 3072)])
 def test_col_sum_parity(ia, rows, cols):
