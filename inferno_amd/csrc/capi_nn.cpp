@@ -296,7 +296,7 @@ int inf_binary_bcast(int op, const void* a, const void* b, void* out, int64_t n,
 
 int inf_argmax_rows(const void* x, int64_t rows, int64_t cols, int64_t ld, int32_t* out, inf_dtype dt, void* stream) {
     if (!dtype_ok(dt)) return INF_ERR_BAD_DTYPE;
-    if (rows < 0 || cols < 1 || cols > INT32_MAX) return INF_ERR_BAD_SHAPE;
+    if (rows < 0 || rows > INT32_MAX || cols < 1 || cols > INT32_MAX) return INF_ERR_BAD_SHAPE;
     if (ld < cols) return INF_ERR_BAD_STRIDE;
     if (rows == 0) return INF_OK;
     if (!x || !out) return INF_ERR_NULL_POINTER;

@@ -531,35 +531,66 @@ __global__ __launch_bounds__(256) void bcast_kernel(const void* __restrict__ a, 
 }
 
 // ============================================================================
-// Row argmax (the greedy next-token pick): one wave per row; lanes scan columns
-// lane, lane + 64, ... keeping (value, first index), then a wave reduction in
-// which the larger value wins and equal values keep the smaller index.
+// Row argmax (the greedy next-token pick): one workgroup per row; threads scan
+// 4-column groups t, t + 256, ... (16-byte loads when the row allows, several
+// in flight) keeping (value, first index); then wave and workgroup reductions
+// in which the larger value wins and equal values keep the smaller index.
 // ============================================================================
+__device__ __forceinline__ void argmax_merge(float& best, int& idx, float ob, int oi) {
+    const bool take = oi >= 0 && (idx < 0 || ob > best || (ob == best && oi < idx));
+    best = take ? ob : best;
+    idx = take ? oi : idx;
+}
+
 template <typename E>
-__global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict__ x, int64_t rows, int64_t cols,
-                                                          int64_t ld, int32_t* __restrict__ out) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const typename E::T* p = (const typename E::T*)x + row * ld;
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict__ x, int64_t cols, int64_t ld,
+                                                          int vec, int32_t* __restrict__ out) {
+    __shared__ float sb[4];
+    __shared__ int si[4];
+    const int tid = threadIdx.x;
+    const typename E::T* p = (const typename E::T*)x + (int64_t)blockIdx.x * ld;
     float best = -INFINITY;
     int idx = -1;
-    for (int64_t c = lane; c < cols; c += 64) {
-        const float v = E::ld(p + c);
-        if (idx < 0 || v > best) {
-            best = v;
-            idx = (int)c;
+    if (vec) {
+        constexpr int U = 4;  // 4-column groups per thread per step
+        for (int64_t c0 = 4 * (int64_t)tid; c0 < cols; c0 += 4 * 256 * U) {
+            f32x4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t c = c0 + 4 * 256 * u;
+                v[u] = c < cols ? ld4(p + c) : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t c = c0 + 4 * 256 * u + j;
+                    if (c < cols && (idx < 0 || v[u][j] > best)) {
+                        best = v[u][j];
+                        idx = (int)c;
+                    }
+                }
+        }
+    } else {
+        for (int64_t c = tid; c < cols; c += 256) {
+            const float v = E::ld(p + c);
+            if (idx < 0 || v > best) {
+                best = v;
+                idx = (int)c;
+            }
         }
     }
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ob = shfl_xor(best, m);
-        const int oi = __shfl_xor(idx, m, 64);
-        const bool take = oi >= 0 && (idx < 0 || ob > best || (ob == best && oi < idx));
-        best = take ? ob : best;
-        idx = take ? oi : idx;
+    for (int m = 32; m >= 1; m >>= 1) argmax_merge(best, idx, shfl_xor(best, m), __shfl_xor(idx, m, 64));
+    if ((tid & 63) == 0) {
+        sb[tid >> 6] = best;
+        si[tid >> 6] = idx;
     }
-    if (lane == 0) out[row] = idx;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w) argmax_merge(best, idx, sb[w], si[w]);
+        out[blockIdx.x] = idx;
+    }
 }
 
 // ============================================================================
@@ -706,11 +737,13 @@ int launch_adamw_multi(const AdamWMultiParams& a, int bf16, hipStream_t s) {
 
 int launch_argmax_rows(const void* x, int64_t rows, int64_t cols, int64_t ld, int32_t* out, int bf16,
                        hipStream_t s) {
-    const dim3 grid(blocks_for(rows, 4));
+    const size_t align = bf16 ? 8 : 16;
+    const int vec = cols % 4 == 0 && ld % 4 == 0 && reinterpret_cast<uintptr_t>(x) % align == 0;
+    const dim3 grid((unsigned)rows);
     if (bf16)
-        hipLaunchKernelGGL(argmax_rows_kernel<BF16>, grid, dim3(256), 0, s, x, rows, cols, ld, out);
+        hipLaunchKernelGGL(argmax_rows_kernel<BF16>, grid, dim3(256), 0, s, x, cols, ld, vec, out);
     else
-        hipLaunchKernelGGL(argmax_rows_kernel<F32>, grid, dim3(256), 0, s, x, rows, cols, ld, out);
+        hipLaunchKernelGGL(argmax_rows_kernel<F32>, grid, dim3(256), 0, s, x, cols, ld, vec, out);
     return (int)hipGetLastError();
 }
 
