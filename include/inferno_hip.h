@@ -37,7 +37,9 @@ extern "C" {
 
 typedef enum { INF_F32 = 0, INF_BF16 = 1 } inf_dtype;
 
-/* Element strides of a [B, H, T, D] view (d must be 1). */
+/* Element strides of a [B, H, T, D] view: d must be 1, all >= 0, and
+ * t <= 2^22 (tiles are addressed with 32-bit byte offsets); otherwise the
+ * attention entry points return INF_ERR_BAD_STRIDE. */
 typedef struct {
     int64_t b, h, t, d;
 } inf_strides;

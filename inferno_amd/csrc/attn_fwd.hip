@@ -58,6 +58,21 @@ struct FwdTile {
     // Software-pipelined loop (two score blocks live): fits two waves per
     // SIMD up to D = 64; D = 128 keeps one score block.
     static constexpr bool PIPE = D <= 64;
+    // V chunk f of a tile: row and first column (elements) within the tile.
+    static constexpr int vrow(int f) { return (f & 15) + 16 * (f / (16 * (D / 4))); }
+    static constexpr int vcol(int f) { return 4 * ((f >> 4) % (D / 4)); }
+    // Chunk tid + 256 i sits at (row, column) of chunk tid plus that of chunk
+    // 256 i, for K and V, for every thread and load of a tile.
+    static constexpr bool chunks_split() {
+        constexpr int C4 = D / 4, LPT = BN * C4 / 256;
+        for (int i = 0; i < LPT; ++i)
+            for (int tid = 0; tid < 256; ++tid) {
+                const int f = tid + 256 * i;
+                if (f / C4 != tid / C4 + 256 * i / C4 || f % C4 != tid % C4) return false;
+                if (vrow(f) != vrow(tid) + vrow(256 * i) || vcol(f) != vcol(tid) + vcol(256 * i)) return false;
+            }
+        return true;
+    }
 };
 
 template <int D, typename E>
@@ -130,25 +145,27 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
 
     // K: chunk f -> (row f / C4, column chunk f % C4), row-major 16-byte loads.
     // V: chunk f -> (row f % 16 + 16 * (f / (16 * C4)), column chunk (f / 16) % C4).
+    // Loads go through a buffer resource per tile: each chunk's offset is a
+    // per-thread part (chunk tid) plus a uniform part (chunk 256 i), and rows
+    // at or past `lim` (<= Tk) are outside the resource and read as zeros, so
+    // a load costs no address arithmetic, compare or branch.
+    static_assert(FwdTile<D>::chunks_split(), "chunk offsets must split into thread + load parts");
+    static_assert(sizeof(E) == 4, "fp32 storage (bf16 has its own kernel)");
     f32x4 kr[LPT], vr[LPT];
-    // Rows at or past `lim` (<= Tk) load as zeros without touching memory.
+    const uint32_t k_voff = (uint32_t)(((int64_t)(tid / C4) * p.sk.t + 4 * (tid % C4)) * 4);
+    const uint32_t v_voff = (uint32_t)(((int64_t)FwdTile<D>::vrow(tid) * p.sv.t + FwdTile<D>::vcol(tid)) * 4);
     auto gload_k = [&](int t, int lim) {
+        const auto rs = row_rsrc((const float*)K, p.sk.t, t * BN, min(lim - t * BN, BN), D);
 #pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int f = tid + 256 * i;
-            const int krow = t * BN + f / C4;
-            kr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (krow < lim) kr[i] = ld4(K + (int64_t)krow * p.sk.t + 4 * (f % C4));
-        }
+        for (int i = 0; i < LPT; ++i)
+            kr[i] = buffer_ld4(rs, k_voff, (uint32_t)(((int64_t)(256 * i / C4) * p.sk.t) * 4));
     };
     auto gload_v = [&](int t, int lim) {
+        const auto rs = row_rsrc((const float*)V, p.sv.t, t * BN, min(lim - t * BN, BN), D);
 #pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int f = tid + 256 * i;
-            const int vrow = t * BN + (f & 15) + 16 * (f / (16 * C4));
-            vr[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (vrow < lim) vr[i] = ld4(V + (int64_t)vrow * p.sv.t + 4 * ((f >> 4) % C4));
-        }
+        for (int i = 0; i < LPT; ++i)
+            vr[i] = buffer_ld4(rs, v_voff,
+                               (uint32_t)(((int64_t)FwdTile<D>::vrow(256 * i) * p.sv.t + FwdTile<D>::vcol(256 * i)) * 4));
     };
     auto gload = [&](int t) {
         gload_k(t, p.Tk);

@@ -26,11 +26,16 @@ bool dtype_ok(int dt) { return dt == INF_F32 || dt == INF_BF16; }
 
 bool head_dim_ok(int D) { return D == 32 || D == 64 || D == 128; }
 
-// A [B,H,T,D] view: unit d stride, non-negative strides, rows aligned for
-// 4-element vector access (16 B fp32, 8 B bf16).
+// Row stride limit: the kernels address a tile of up to 128 rows through a
+// buffer resource with 32-bit byte offsets, so 128 * stride * 4 B < 2^31.
+constexpr int64_t kMaxRowStride = int64_t(1) << 22;
+
+// A [B,H,T,D] view: unit d stride, non-negative strides at most
+// kMaxRowStride along t, rows aligned for 4-element vector access (16 B fp32,
+// 8 B bf16).
 int check_view(const void* p, const inf_strides& s, inf_dtype dt) {
     if (!p) return INF_ERR_NULL_POINTER;
-    if (s.d != 1 || s.b < 0 || s.h < 0 || s.t < 0) return INF_ERR_BAD_STRIDE;
+    if (s.d != 1 || s.b < 0 || s.h < 0 || s.t < 0 || s.t > kMaxRowStride) return INF_ERR_BAD_STRIDE;
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
     const uintptr_t need = (uintptr_t)(4 * elem_bytes(dt));
     if (a % need) return INF_ERR_ALIGNMENT;
@@ -70,7 +75,7 @@ const char* inf_status_string(int status) {
         case INF_OK: return "ok";
         case INF_ERR_NULL_POINTER: return "null pointer argument";
         case INF_ERR_BAD_SHAPE: return "invalid shape";
-        case INF_ERR_BAD_STRIDE: return "invalid stride (head-dim stride must be 1, strides >= 0)";
+        case INF_ERR_BAD_STRIDE: return "invalid stride (head-dim stride must be 1, strides >= 0, row stride <= 2^22)";
         case INF_ERR_BAD_DTYPE: return "unsupported dtype";
         case INF_ERR_UNSUPPORTED: return "unsupported configuration (head dim must be 32, 64 or 128)";
         case INF_ERR_WORKSPACE: return "workspace missing or too small";

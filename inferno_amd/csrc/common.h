@@ -105,6 +105,25 @@ struct BF16 {
 
 // Load 4 consecutive elements as fp32 (16-byte load for fp32, 8-byte for bf16).
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+
+// Raw buffer resource over `bytes` bytes from `base` (gfx9 dword 3: raw
+// addressing, no swizzle).  A load whose offset falls at or past `bytes`
+// returns zeros without a memory access.  The base and size are wave-uniform,
+// so the descriptor lives in SGPRs.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 16-byte load at byte offset voff (per lane) + soff (uniform).
+__device__ __forceinline__ f32x4 buffer_ld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+// Resource over rows [row0, row0 + rows) of a row-major fp32 matrix with
+// row stride `st` elements and `cols` used columns (rows <= 0: empty).
+// Offsets must stay below 2^31 bytes: the caller bounds rows * st * 4.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const float* base, int64_t st, int row0, int rows, int cols) {
+    const uint32_t bytes = rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * st + cols) * 4) : 0u;
+    return buffer_rsrc(base + (int64_t)row0 * st, bytes);
+}
 __device__ __forceinline__ f32x4 ld4(const uint16_t* p) {
     u16x4 h = *reinterpret_cast<const u16x4*>(p);
     f32x4 r;
