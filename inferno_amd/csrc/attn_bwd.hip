@@ -27,6 +27,8 @@
 // bf16 inputs use the bf16-MFMA main kernel (attn_bwd_bf16.hip) between the
 // same pre kernel and a final bwd_cvt that turns the fp32 dQ accumulator into
 // bf16 dq.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -161,26 +163,28 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
     // wave is done with the staged copies: two barriers per tile.  The
     // prefetch is straight-line (a row limit of 0 past the last tile) and keeps
     // raw values, so no wait for it lands inside the MFMA blocks.
+    // The loads go through buffer resources over rows [q0, lim): chunk
+    // tid + 256 i sits 256 i / C4 rows below chunk tid, and rows past the
+    // resource read as zeros, so a load needs no address arithmetic or branch.
     constexpr bool PF = D <= 64;
+    static_assert(256 % C4 == 0, "chunk rows must split into thread + load parts");
+    static_assert(sizeof(E) == 4, "fp32 storage (bf16 has its own kernel)");
     f32x4 ra[QLPT], rd[QLPT];
     float r_lse = 0.f, r_dl = 0.f;
+    const uint32_t q_voff = (uint32_t)(((int64_t)(tid / C4) * p.sq.t + 4 * (tid % C4)) * 4);
+    const uint32_t do_voff = (uint32_t)(((int64_t)(tid / C4) * p.sdo.t + 4 * (tid % C4)) * 4);
     auto gload_q = [&](int q0, int lim) {
+        const int rows = min(lim - q0, BQ);
+        const auto rq = row_rsrc((const float*)Q, p.sq.t, q0, rows, D);
+        const auto rdo = row_rsrc((const float*)dO, p.sdo.t, q0, rows, D);
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
-            const int f = tid + 256 * i;
-            const int qi = q0 + f / C4;
-            const int c4 = f % C4;
-            ra[i] = rd[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (qi < lim) {
-                ra[i] = ld4(Q + (int64_t)qi * p.sq.t + 4 * c4);
-                rd[i] = ld4(dO + (int64_t)qi * p.sdo.t + 4 * c4);
-            }
+            ra[i] = buffer_ld4(rq, q_voff, (uint32_t)((int64_t)(256 * i / C4) * p.sq.t * 4));
+            rd[i] = buffer_ld4(rdo, do_voff, (uint32_t)((int64_t)(256 * i / C4) * p.sdo.t * 4));
         }
-        r_lse = r_dl = 0.f;
-        if (tid < BQ && q0 + tid < lim) {
-            r_lse = LSE[q0 + tid];
-            r_dl = DL[q0 + tid];
-        }
+        // lanes past the tile's rows (all but the first BQ threads) read zeros
+        r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
+        r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
     };
     auto sstore_q = [&]() {
 #pragma unroll
@@ -211,15 +215,15 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
 
         // Does any query of this tile see any key of this wave?
         const bool active = !p.causal || (q0 + BQ - 1 + p.off >= k0w);
-        f32x16 ds = f32x16{};
+        f32x16 ds;
         if (active && k0w < p.Tk) {
-            f32x16 s = f32x16{}, dp = f32x16{};
+            f32x16 s, dp;
 #pragma unroll
             for (int i = 0; i < HD; i += 4) {
                 const f32x4 qa = *reinterpret_cast<const f32x4*>(&Qs[l32][g * HD + i]);
                 const f32x4 da = *reinterpret_cast<const f32x4*>(&dOs[l32][g * HD + i]);
-                s = mfma32x32x2(qa[0], kf[i + 0], s);
-                dp = mfma32x32x2(da[0], vf[i + 0], dp);
+                s = mfma32x32x2(qa[0], kf[i + 0], i == 0 ? f32x16{} : s);  // zero accumulator as an operand
+                dp = mfma32x32x2(da[0], vf[i + 0], i == 0 ? f32x16{} : dp);
                 s = mfma32x32x2(qa[1], kf[i + 1], s);
                 dp = mfma32x32x2(da[1], vf[i + 1], dp);
                 s = mfma32x32x2(qa[2], kf[i + 2], s);
@@ -228,20 +232,32 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
                 dp = mfma32x32x2(da[3], vf[i + 3], dp);
             }
             // P and dS; reg r holds query row 8*(r/4) + 4*g + r%4 of the tile.
+            // Only tiles that cross the causal diagonal or the end of the
+            // queries / keys evaluate the visibility test.
+            auto p_ds = [&](auto masked) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLog2e;
-                const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLog2e;
+                    const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
 #pragma unroll
-                for (int cc = 0; cc < 4; ++cc) {
-                    const int r = 4 * j + cc;
-                    const int qi = q0 + 8 * j + 4 * g + cc;
-                    const bool vis = (qi < p.Tq) && (key < p.Tk) && (!p.causal || key <= qi + p.off);
-                    const float pr = vis ? fast_exp2(fmaf(s[r], c, -L[cc])) : 0.f;
-                    s[r] = pr;
-                    ds[r] = pr * (dp[r] - Dl[cc]);
+                    for (int cc = 0; cc < 4; ++cc) {
+                        const int r = 4 * j + cc;
+                        float pr = fast_exp2(fmaf(s[r], c, -L[cc]));
+                        if constexpr (decltype(masked)::value) {
+                            const int qi = q0 + 8 * j + 4 * g + cc;
+                            const bool vis = (qi < p.Tq) && (key < p.Tk) && (!p.causal || key <= qi + p.off);
+                            pr = vis ? pr : 0.f;
+                        }
+                        s[r] = pr;
+                        ds[r] = pr * (dp[r] - Dl[cc]);
+                    }
                 }
-            }
+            };
+            const bool need_mask = q0 + BQ > p.Tq || k0w + 32 > p.Tk || (p.causal && k0w + 31 > q0 + p.off);
+            if (need_mask)
+                p_ds(std::true_type{});
+            else
+                p_ds(std::false_type{});
             // dV^T += dO^T P ; dK^T += Q^T dS
 #pragma unroll
             for (int kk = 0; kk < 16; ++kk) {
@@ -254,6 +270,8 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
                     dk_acc[db] = mfma32x32x2(aq, ds[kk], dk_acc[db]);
                 }
             }
+        } else {
+            ds = f32x16{};
         }
         // dS block of this wave -> LDS (rows = queries, columns = the 128 keys)
 #pragma unroll
@@ -262,26 +280,28 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
         if constexpr (PF) sstore_q();  // the next tile (zeros after the last one, never read)
 
         // ---- dQ tile (32 x D) += dS (32 x 128) K (128 x D) ---------------------
+        // fp32 atomics through a buffer resource over the tile's rows: rows
+        // past Tq fall outside it and the hardware drops those adds.
+        const auto rdq = row_rsrc(dQa, p.sacc.t, q0, min(p.Tq - q0, BQ), D);
 #pragma unroll
         for (int bi = 0; bi < DQB; ++bi) {
             const int blk = wave * DQB + bi;
             const int qh = blk & 1;
             const int dc = blk >> 1;
-            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            f32x4 acc;
 #pragma unroll
             for (int kk = 0; kk < 32; kk += 4) {
                 const f32x4 a = *reinterpret_cast<const f32x4*>(&dSs[16 * qh + l16][g4 * 32 + kk]);
                 const f32x4 bb = *reinterpret_cast<const f32x4*>(&Kts[16 * dc + l16][g4 * 32 + kk]);
-                acc = mfma16x16x4(a[0], bb[0], acc);
+                acc = mfma16x16x4(a[0], bb[0], kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc);
                 acc = mfma16x16x4(a[1], bb[1], acc);
                 acc = mfma16x16x4(a[2], bb[2], acc);
                 acc = mfma16x16x4(a[3], bb[3], acc);
             }
+            const uint32_t voff = (uint32_t)(((int64_t)(16 * qh + 4 * g4) * p.sacc.t + 16 * dc + l16) * 4);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int qi = q0 + 16 * qh + 4 * g4 + r;
-                if (qi < p.Tq) unsafeAtomicAdd(dQa + (int64_t)qi * p.sacc.t + 16 * dc + l16, acc[r] * p.scale);
-            }
+            for (int r = 0; r < 4; ++r)
+                buffer_atomic_add(rdq, acc[r] * p.scale, voff, (uint32_t)((int64_t)r * p.sacc.t * 4));
         }
         __syncthreads();
     }

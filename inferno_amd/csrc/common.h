@@ -117,6 +117,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 __device__ __forceinline__ f32x4 buffer_ld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
+__device__ __forceinline__ float buffer_ld1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+// fp32 atomic add at byte offset voff + soff (dropped outside the resource).
+__device__ __forceinline__ void buffer_atomic_add(__amdgpu_buffer_rsrc_t r, float v, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, (int)voff, (int)soff, 0);
+}
 // Resource over rows [row0, row0 + rows) of a row-major fp32 matrix with
 // row stride `st` elements and `cols` used columns (rows <= 0: empty).
 // Offsets must stay below 2^31 bytes: the caller bounds rows * st * 4.
