@@ -20,6 +20,8 @@
 //                               workgroup; v_mfma_f32_16x16x32_bf16 tiles
 // Transposed staging writes dwords that pack two rows' elements, so the LDS
 // stores stay 32-bit.  Softmax statistics, P and dS are computed in fp32.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -138,28 +140,33 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
     // (after the dS barrier), so each tile needs two barriers.
     bf16x8 ra[QLPT], rb[QLPT];
     float r_lse = 0.f, r_dl = 0.f;
-    // Rows at or past `lim` (<= Tq) load as zeros without touching memory;
-    // raw values only, so no arithmetic waits on the loads here.
+    // Loads through buffer resources over rows [q0, lim) (<= Tq): rows past
+    // them read as zeros, with no address arithmetic or branch per load; raw
+    // values only, so no arithmetic waits on the loads here.  Whether chunk f
+    // is of Q or dO is uniform over each wave for every head dim (QTASK is a
+    // multiple of 64), which keeps the selected resource in SGPRs.
+    static_assert(QTASK % 64 == 0 && 256 % QTASK == 0 || QTASK % 256 == 0, "Q / dO split must be wave-uniform");
     auto gload_q = [&](int q0, int lim) {
+        const int rows = min(lim - q0, BQ);
+        const auto rq = row_rsrc(Q, p.sq.t, q0, rows, D);
+        const auto rdo = row_rsrc(dO, p.sdo.t, q0, rows, D);
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
             const int f = tid + 256 * i;
             ra[i] = rb[i] = bf16x8{};
             if (f >= 2 * QTASK) continue;
-            const int which = f / QTASK;  // 0: Q, 1: dO
+            const int which = __builtin_amdgcn_readfirstlane(f / QTASK);  // 0: Q, 1: dO
             const int rem = f % QTASK;
             const int qp = rem % (BQ / 2), c8 = rem / (BQ / 2);
-            const __bf16* src = which ? dO : Q;
             const int64_t st = which ? p.sdo.t : p.sq.t;
-            const int r0 = q0 + 2 * qp;
-            if (r0 < lim) ra[i] = *reinterpret_cast<const bf16x8*>(src + (int64_t)r0 * st + 8 * c8);
-            if (r0 + 1 < lim) rb[i] = *reinterpret_cast<const bf16x8*>(src + (int64_t)(r0 + 1) * st + 8 * c8);
+            const auto rs = which ? rdo : rq;
+            const uint32_t voff = (uint32_t)(((int64_t)(2 * qp) * st + 8 * c8) * 2);
+            ra[i] = buffer_ld8bf(rs, voff, 0);
+            rb[i] = buffer_ld8bf(rs, voff, (uint32_t)(st * 2));
         }
-        r_lse = r_dl = 0.f;
-        if (tid < BQ && q0 + tid < lim) {
-            r_lse = LSE[q0 + tid];
-            r_dl = DL[q0 + tid];
-        }
+        // lanes past the tile's rows (all but the first BQ threads) read zeros
+        r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
+        r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
     };
     auto sstore_q = [&]() {
 #pragma unroll
@@ -201,29 +208,41 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
         const bool active = !p.causal || (q0 + BQ - 1 + p.off >= k0w);
         bf16x8 pb[2], dsb[2];
         if (active && k0w < p.Tk) {
-            f32x16 s = f32x16{}, dp = f32x16{};
+            f32x16 s, dp;
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk) {
                 const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&Qs[l32][16 * kk + 8 * g]);
                 const bf16x8 da = *reinterpret_cast<const bf16x8*>(&dOs[l32][16 * kk + 8 * g]);
-                s = mfma32x32x16bf16(qa, kf[kk], s);
-                dp = mfma32x32x16bf16(da, vf[kk], dp);
+                s = mfma32x32x16bf16(qa, kf[kk], kk == 0 ? f32x16{} : s);  // zero accumulator as an operand
+                dp = mfma32x32x16bf16(da, vf[kk], kk == 0 ? f32x16{} : dp);
             }
-            // P and dS; register r holds query row 8*(r/4) + 4*g + r%4 of the tile.
+            // P and dS; register r holds query row 8*(r/4) + 4*g + r%4 of the
+            // tile.  Only tiles that cross the causal diagonal or the end of
+            // the queries / keys evaluate the visibility test.
+            auto p_ds = [&](auto masked) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLog2e;
-                const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLog2e;
+                    const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
 #pragma unroll
-                for (int cc = 0; cc < 4; ++cc) {
-                    const int r = 4 * j + cc;
-                    const int qi = q0 + 8 * j + 4 * g + cc;
-                    const bool vis = (qi < p.Tq) && (key < p.Tk) && (!p.causal || key <= qi + p.off);
-                    const float pr = vis ? fast_exp2(fmaf(s[r], c, -L[cc])) : 0.f;
-                    pb[r >> 3][r & 7] = (__bf16)pr;
-                    dsb[r >> 3][r & 7] = (__bf16)(pr * (dp[r] - Dl[cc]));
+                    for (int cc = 0; cc < 4; ++cc) {
+                        const int r = 4 * j + cc;
+                        float pr = fast_exp2(fmaf(s[r], c, -L[cc]));
+                        if constexpr (decltype(masked)::value) {
+                            const int qi = q0 + 8 * j + 4 * g + cc;
+                            const bool vis = (qi < p.Tq) && (key < p.Tk) && (!p.causal || key <= qi + p.off);
+                            pr = vis ? pr : 0.f;
+                        }
+                        pb[r >> 3][r & 7] = (__bf16)pr;
+                        dsb[r >> 3][r & 7] = (__bf16)(pr * (dp[r] - Dl[cc]));
+                    }
                 }
-            }
+            };
+            const bool need_mask = q0 + BQ > p.Tq || k0w + 32 > p.Tk || (p.causal && k0w + 31 > q0 + p.off);
+            if (need_mask)
+                p_ds(std::true_type{});
+            else
+                p_ds(std::false_type{});
             // dV^T += dO^T P ; dK^T += Q^T dS  (reduce over the 32 queries, 16 per MFMA)
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
@@ -252,23 +271,25 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
         sstore_q();
 
         // ---- dQ tile (32 x D) += dS (32 x 128) K (128 x D), 16x16 blocks ---------
+        // fp32 atomics through a buffer resource over the tile's rows: rows
+        // past Tq fall outside it and the hardware drops those adds.
+        const auto rdq = row_rsrc(dQa, p.sacc.t, q0, min(p.Tq - q0, BQ), D);
 #pragma unroll
         for (int bi = 0; bi < DQB; ++bi) {
             const int blk = wave * DQB + bi;
             const int qh = blk & 1;
             const int dc = blk >> 1;
-            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            f32x4 acc;
 #pragma unroll
             for (int kk = 0; kk < BK / 32; ++kk) {
                 const bf16x8 a = *reinterpret_cast<const bf16x8*>(&dSs[16 * qh + l16][32 * kk + 8 * g4]);
                 const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&KTs[16 * dc + l16][32 * kk + 8 * g4]);
-                acc = mfma16x16x32bf16(a, bb, acc);
+                acc = mfma16x16x32bf16(a, bb, kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc);
             }
+            const uint32_t voff = (uint32_t)(((int64_t)(16 * qh + 4 * g4) * p.sacc.t + 16 * dc + l16) * 4);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int qi = q0 + 16 * qh + 4 * g4 + r;
-                if (qi < p.Tq) unsafeAtomicAdd(dQa + (int64_t)qi * p.sacc.t + 16 * dc + l16, acc[r] * p.scale);
-            }
+            for (int r = 0; r < 4; ++r)
+                buffer_atomic_add(rdq, acc[r] * p.scale, voff, (uint32_t)((int64_t)r * p.sacc.t * 4));
         }
         __syncthreads();
     }

@@ -85,24 +85,26 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     const int n_tiles = (kv_end + BN - 1) / BN;
     const int wave_kend = p.causal ? min(kv_end, q0w + 32 + p.off) : kv_end;
 
+    // Tile loads through buffer resources over rows [t*BN, lim): chunk
+    // tid + 256 i is chunk tid moved by a uniform offset (256 i / C8 rows for
+    // K, 8 i column chunks for V), and rows at or past `lim` read as zeros.
+    static_assert(256 % C8 == 0 && 256 % (BN / 2) == 0, "chunks must split into thread + load parts");
     bf16x8 kr[KLPT], va[VLPT], vb[VLPT];
-    auto gload = [&](int t) {
+    const uint32_t k_voff = (uint32_t)(((int64_t)(tid / C8) * p.sk.t + 8 * (tid % C8)) * 2);
+    const uint32_t v_voff = (uint32_t)(((int64_t)(2 * (tid % (BN / 2))) * p.sv.t + 8 * (tid / (BN / 2))) * 2);
+    auto gload = [&](int t, int lim) {
+        const int rows = min(lim - t * BN, BN);
+        const auto rk = row_rsrc(K, p.sk.t, t * BN, rows, D);
+        const auto rv = row_rsrc(V, p.sv.t, t * BN, rows, D);
 #pragma unroll
-        for (int i = 0; i < KLPT; ++i) {
-            const int f = tid + 256 * i;
-            const int row = f / C8, c8 = f % C8;
-            const int key = t * BN + row;
-            kr[i] = key < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)key * p.sk.t + 8 * c8) : bf16x8{};
-        }
+        for (int i = 0; i < KLPT; ++i)
+            kr[i] = buffer_ld8bf(rk, k_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sk.t * 2));
 #pragma unroll
         for (int i = 0; i < VLPT; ++i) {
-            const int f = tid + 256 * i;
-            const int kp = f % (BN / 2), c8 = f / (BN / 2);
-            const int key = t * BN + 2 * kp;
-            if (f >= VTASKS) continue;
-            va[i] = key < p.Tk ? *reinterpret_cast<const bf16x8*>(V + (int64_t)key * p.sv.t + 8 * c8) : bf16x8{};
-            vb[i] = key + 1 < p.Tk ? *reinterpret_cast<const bf16x8*>(V + (int64_t)(key + 1) * p.sv.t + 8 * c8)
-                                   : bf16x8{};
+            if (tid + 256 * i >= VTASKS) continue;
+            const uint32_t col = (uint32_t)(8 * (256 * i / (BN / 2)) * 2);
+            va[i] = buffer_ld8bf(rv, v_voff, col);
+            vb[i] = buffer_ld8bf(rv, v_voff, col + (uint32_t)(p.sv.t * 2));
         }
     };
     auto sstore = [&](int buf) {
@@ -135,25 +137,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     float l_run = 0.f;
     const float c = p.c;
 
-    gload(0);
+    gload(0, p.Tk);
     sstore(0);
     __syncthreads();
 
+    // The prefetch of tile t+1 and its store are straight-line (a row limit
+    // of 0 past the last tile: zeros into a buffer that is not read again).
     for (int t = 0; t < n_tiles; ++t) {
         const int buf = t & 1;
         const int k0 = t * BN;
-        if (t + 1 < n_tiles) gload(t + 1);
+        gload(t + 1, t + 1 < n_tiles ? p.Tk : 0);
 
         if (k0 < wave_kend) {
             f32x16 s[NKB];
-#pragma unroll
-            for (int kb = 0; kb < NKB; ++kb) s[kb] = f32x16{};
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb) {
                     const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Ks[buf][kb * 32 + l32][16 * kk + 8 * g]);
-                    s[kb] = mfma32x32x16bf16(a, qf[kk], s[kb]);
+                    s[kb] = mfma32x32x16bf16(a, qf[kk], kk == 0 ? f32x16{} : s[kb]);
                 }
 
             const bool need_mask = (k0 + BN > p.Tk) || (p.causal && (k0 + BN - 1 > q0w + p.off));
@@ -172,7 +174,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kb][r]);
-            mloc = fmaxf(mloc, shfl_xor(mloc, 32));
+            mloc = max_xor32(mloc);
             const float m_new = fmaxf(m_run, mloc);
             const float alpha = fast_exp2((m_run - m_new) * c);
             const float mc = m_new * c;
@@ -207,7 +209,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
                 }
         }
 
-        if (t + 1 < n_tiles) sstore(buf ^ 1);
+        sstore(buf ^ 1);
         __syncthreads();
     }
 

@@ -48,6 +48,15 @@ __device__ __forceinline__ float shfl_xor(float v, int mask) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
 }
 
+// max(v[l], v[l ^ 32]) in every lane l, on the VALU: v_permlane32_swap of
+// two copies of v exchanges the upper half of the first with the lower half of
+// the second, so in every lane the two results are v[l] and v[l ^ 32] (in
+// either order).
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Sum over aligned groups of W lanes (W = 2..32), result in every lane of the
 // group.  Within a 16-lane DPP row it is VALU-only: quad_perm [1,0,3,2] and
 // [2,3,0,1] build quad sums, row_half_mirror (lane i <- 7-i) pairs the quads of
@@ -123,6 +132,15 @@ __device__ __forceinline__ float buffer_ld1(__amdgpu_buffer_rsrc_t r, uint32_t v
 // fp32 atomic add at byte offset voff + soff (dropped outside the resource).
 __device__ __forceinline__ void buffer_atomic_add(__amdgpu_buffer_rsrc_t r, float v, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, (int)voff, (int)soff, 0);
+}
+// Resource over rows [row0, row0 + rows) of a row-major bf16 matrix (row
+// stride `st` elements, `cols` used columns); loads return raw bf16 bits.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const __bf16* base, int64_t st, int row0, int rows, int cols) {
+    const uint32_t bytes = rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * st + cols) * 2) : 0u;
+    return buffer_rsrc(base + (int64_t)row0 * st, bytes);
+}
+__device__ __forceinline__ bf16x8 buffer_ld8bf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
 // Resource over rows [row0, row0 + rows) of a row-major fp32 matrix with
 // row stride `st` elements and `cols` used columns (rows <= 0: empty).
