@@ -66,6 +66,8 @@ def fwd(**kw):
     (dict(sq=Strides(512, 512, 64, 2)), 3),   # head-dim stride must be 1
     (dict(sk=Strides(-1, 512, 64, 1)), 3),
     (dict(sv=Strides(512, 512, 66, 1)), 7),   # row stride not 4-element aligned
+    (dict(sk=Strides(0, 0, (1 << 22) + 4, 1)), 3),  # row stride above 2^22 (32-bit tile offsets)
+    (dict(so=Strides(0, 0, 1 << 23, 1)), 3),
     (dict(q=FAKE + 4), 7),                    # 16-byte alignment for fp32
 ])
 def test_fwd_validation(kw, status):
