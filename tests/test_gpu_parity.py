@@ -141,26 +141,32 @@ def test_prefix_invariance_bitwise(ia):
         assert torch.equal(l1[:, :, :t], l2[:, :, :t]), f"prefix {t}"
 
 
-def test_strided_qkv_view(ia):
-    """q/k/v read straight out of a [B, T, 3, H, D] projection buffer (no copies)."""
-    print("[case] strided views", flush=True)
-    B, H, T, D = 2, 3, 150, 64
+@pytest.mark.parametrize("dtype,D,T", [(torch.float32, 64, 150), (torch.float32, 128, 97),
+                                     (torch.bfloat16, 64, 150), (torch.bfloat16, 32, 211)])
+def test_strided_qkv_view(ia, dtype, D, T):
+    """q/k/v read straight out of a [B, T, 3, H, D] projection buffer and dq/dk/dv
+    written straight into a gradient buffer of the same layout (no copies)."""
+    print(f"[case] strided views {dtype} D{D} T{T}", flush=True)
+    B, H = 2, 3
     q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=5)
-    buf = torch.empty((B, T, 3, H, D), device="cuda")
-    buf[:, :, 0] = dev(q).transpose(1, 2)
-    buf[:, :, 1] = dev(k).transpose(1, 2)
-    buf[:, :, 2] = dev(v).transpose(1, 2)
-    Q = buf[:, :, 0].permute(0, 2, 1, 3)
-    K = buf[:, :, 1].permute(0, 2, 1, 3)
-    V = buf[:, :, 2].permute(0, 2, 1, 3)
-    assert not Q.is_contiguous()
+    if dtype == torch.bfloat16:
+        q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
+    buf = torch.empty((B, T, 3, H, D), device="cuda", dtype=dtype)
+    gbuf = torch.full((B, T, 3, H, D), float("nan"), device="cuda", dtype=dtype)
+    for i, x in enumerate((q, k, v)):
+        buf[:, :, i] = dev(x, dtype).transpose(1, 2)
+    Q, K, V = (buf[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    dQ, dK, dV = (gbuf[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    assert not Q.is_contiguous() and Q.stride(2) == 3 * H * D
     o, lse = ia.attn_fwd(Q, K, V)
-    dq, dk, dv = ia.attn_bwd(Q, K, V, o, dev(do), lse)
+    ia.attn_bwd(Q, K, V, o, dev(do, dtype), lse, dq=dQ, dk=dK, dv=dV)
     torch.cuda.synchronize()
     o_r, _ = oracle.attn_fwd(q, k, v)
     dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do)
-    for x, r in ((o, o_r), (dq, dq_r), (dk, dk_r), (dv, dv_r)):
-        assert oracle.rel_err(host(x), r) <= TOL_F32
+    tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+    for name, x, r in (("O", o, o_r), ("dQ", dQ, dq_r), ("dK", dK, dk_r), ("dV", dV, dv_r)):
+        e = oracle.rel_err(host(x), r)
+        assert e <= tol, f"{name} rel err {e:.3e}"
 
 
 def test_config2_full_size_heads(ia):
