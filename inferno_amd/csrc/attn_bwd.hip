@@ -29,6 +29,14 @@
 // bf16 dq.
 #include <type_traits>
 
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "bwd_split.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -57,6 +65,8 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdParams p) {
 #pragma unroll
     for (int m = TPR / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
     if (row < rows && c4 == 0) p.delta[row] = s;
+    if (blockIdx.x == 0)
+        for (int i = tid; i < p.n_split * p.B * p.H; i += 256) p.counters[i] = 0u;
 }
 
 template <int D>
@@ -95,10 +105,10 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
     const int l16 = lane & 15;
     const int g4 = lane >> 4;
 
-    const int BH = p.B * p.H;
-    const int w = blockIdx.x;
-    const int kblk = w / BH;
-    const int bh = w % BH;
+    const BwdWork wk = bwd_work(p);
+    if (wk.bh >= p.B * p.H) return;  // padding workgroup of a split plan's grid
+    const int kblk = wk.kblk;
+    const int bh = wk.bh;
     const int b = bh / p.H;
     const int h = bh % p.H;
 
@@ -152,9 +162,8 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
         dk_acc[i] = f32x16{};
     }
 
-    int q_begin = 0;
-    if (p.causal) q_begin = max(0, k0 - p.off);
-    q_begin = (q_begin / BQ) * BQ;
+    const int q_begin = wk.q_begin;
+    const int q_end = wk.q_end;
     const float c = p.c;
 
     // Query-tile staging.  With PF (D <= 64, where the registers fit) the next
@@ -204,9 +213,9 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
         __syncthreads();
     }
 
-    for (int q0 = q_begin; q0 < p.Tq; q0 += BQ) {
+    for (int q0 = q_begin; q0 < q_end; q0 += BQ) {
         if constexpr (PF) {
-            gload_q(q0 + BQ, q0 + BQ < p.Tq ? p.Tq : 0);
+            gload_q(q0 + BQ, q0 + BQ < q_end ? p.Tq : 0);
         } else {
             gload_q(q0, p.Tq);
             sstore_q();
@@ -307,6 +316,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
     }
 
     // ---- dK = scale * dK^T^T, dV = dV^T^T ------------------------------------------
+    if (!bwd_fixup(p, wk, dk_acc, dv_acc)) return;
     if (key < p.Tk) {
         E* dKp = (E*)p.dk + b * p.sdk.b + h * p.sdk.h + (int64_t)key * p.sdk.t;
         E* dVp = (E*)p.dv + b * p.sdv.b + h * p.sdv.h + (int64_t)key * p.sdv.t;
@@ -343,6 +353,204 @@ __global__ __launch_bounds__(256) void bwd_cvt_kernel(BwdParams p) {
     st4((uint16_t*)p.dq + b * p.sdq.b + h * p.sdq.h + i * p.sdq.t + 4 * c4, a);
 }
 
+// ---- split plan (host) ------------------------------------------------------------
+//
+// Under a causal mask key block j has ~(Tq - 128 j) / 32 query tiles, so at
+// config-2 sizes the first key blocks carry up to 8x the work of the last.
+// Measured on MI355X: a workgroup alone on a CU runs ~1.85x faster than each
+// of two sharing it (two resident workgroups give ~8% more throughput than
+// one), so the heaviest workgroups, which always share their CU with lighter
+// ones, set the kernel's length.  bwd_plan simulates the dispatch (workgroup w
+// to XCD w % 8, each XCD's workgroups placed in order on its least-loaded CU
+// with a free slot) for splits of the heaviest key blocks' tile ranges into
+// chunks, and keeps the best if it beats the unsplit order by 3%.
+
+static constexpr double kBwdPairGain = 0.08;  // throughput gained per extra resident workgroup
+// Per-workgroup fixed cost (K/V loads, K^T staging) and the partial store /
+// reduction of a split chunk, in query tiles of that dtype's kernel: a bf16
+// tile costs ~1/5 of an fp32 one, the fixed costs about the same time.
+static constexpr double kBwdOverhead[2] = {0.3, 1.5};
+static constexpr double kBwdFixup[2] = {0.4, 2.0};
+
+static double share_rate(size_t k) { return k <= 1 ? 1.0 : (1.0 + kBwdPairGain * (double)(k - 1)) / (double)k; }
+
+// Makespan, in query tiles of a workgroup alone on a CU, of workgroups of the
+// given costs in dispatch order.
+static double cu_makespan(const std::vector<double>& cost, int cus_per_xcd, int slots) {
+    double worst = 0.0;
+    std::vector<std::vector<double>> res((size_t)cus_per_xcd);
+    for (int x = 0; x < 8; ++x) {
+        for (auto& r : res) r.clear();
+        size_t next = (size_t)x;
+        auto fill = [&]() {
+            while (next < cost.size()) {
+                int best = -1;
+                for (int c = 0; c < cus_per_xcd; ++c)
+                    if ((int)res[(size_t)c].size() < slots &&
+                        (best < 0 || res[(size_t)c].size() < res[(size_t)best].size()))
+                        best = c;
+                if (best < 0) break;
+                res[(size_t)best].push_back(cost[next]);
+                next += 8;
+            }
+        };
+        fill();
+        double t = 0.0;
+        for (;;) {
+            double dt = INFINITY;
+            for (const auto& r : res)
+                for (double v : r) dt = std::min(dt, v / share_rate(r.size()));
+            if (!(dt < INFINITY)) break;
+            t += dt;
+            for (auto& r : res) {
+                const double rate = share_rate(r.size());
+                for (double& v : r) v -= dt * rate;
+                r.erase(std::remove_if(r.begin(), r.end(), [](double v) { return v <= 1e-9; }), r.end());
+            }
+            fill();
+        }
+        worst = std::max(worst, t);
+    }
+    return worst;
+}
+
+// Resident backward workgroups per CU, and CUs per XCD, on the current device.
+static void bwd_slots(int D, int bf16, int* per_cu, int* cus_per_xcd) {
+    static std::mutex mu;
+    static std::map<std::array<int, 3>, std::pair<int, int>> cache;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        dev = -1;
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    const std::array<int, 3> key{dev, D, bf16};
+    auto it = cache.find(key);
+    if (it == cache.end()) {
+        int cus = 256, occ = D >= 128 ? 1 : 2;  // MI355X defaults
+        if (dev >= 0) {
+            int n = 0, o = 0;
+            if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
+            hipError_t e = hipErrorInvalidValue;
+            if (!bf16 && D == 32) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<32, float>, 256, 0);
+            if (!bf16 && D == 64) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<64, float>, 256, 0);
+            if (!bf16 && D == 128) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<128, float>, 256, 0);
+            if (bf16) e = (hipError_t)bwd_main_bf16_occupancy(D, &o);
+            if (e == hipSuccess && o > 0) occ = o;
+            (void)hipGetLastError();
+        }
+        it = cache.emplace(key, std::make_pair(occ, std::max(1, cus / 8))).first;
+    }
+    *per_cu = it->second.first;
+    *cus_per_xcd = it->second.second;
+}
+
+static void bwd_plan_compute(int B, int H, int Tq, int Tk, int bf16, int per_cu, int cus_per_xcd, BwdPlan* out) {
+    const int BH = B * H;
+    const int nkb = (Tk + kBwdBK - 1) / kBwdBK;
+    const int off = Tk - Tq;
+    if ((int64_t)nkb * BH > 8LL * 8 * cus_per_xcd * per_cu) return;  // the tail is a small share
+    std::vector<int> t0((size_t)nkb), nt((size_t)nkb);
+    int max_nt = 0;
+    for (int j = 0; j < nkb; ++j) {
+        t0[(size_t)j] = std::max(0, j * kBwdBK - off) / kBwdBQ;
+        nt[(size_t)j] = (Tq + kBwdBQ - 1) / kBwdBQ - t0[(size_t)j];
+        max_nt = std::max(max_nt, nt[(size_t)j]);
+    }
+    struct G { double cost; int kb, a, b, chunk, n; };
+    auto build = [&](int ch, std::vector<G>& g) {
+        g.clear();
+        for (int j = 0; j < nkb; ++j) {
+            const int n = nt[(size_t)j];
+            const int k = n > ch ? (n + ch - 1) / ch : 1;
+            for (int c = 0; c < k; ++c) {
+                const int a = (int)((int64_t)n * c / k), b = (int)((int64_t)n * (c + 1) / k);
+                g.push_back({(double)(b - a) + kBwdOverhead[bf16] + (k > 1 ? kBwdFixup[bf16] : 0.0), j, t0[(size_t)j] + a,
+                             t0[(size_t)j] + b, c, k});
+            }
+        }
+        std::stable_sort(g.begin(), g.end(), [](const G& x, const G& y) { return x.cost > y.cost; });
+    };
+    // dispatch order of a plan's grid: group-major, BHp heads per group (padding
+    // heads cost nothing); the unsplit grid has B*H heads per key block
+    auto makespan = [&](const std::vector<G>& g, int heads) {
+        std::vector<double> cost;
+        cost.reserve(g.size() * (size_t)heads);
+        for (const G& x : g)
+            for (int i = 0; i < heads; ++i) cost.push_back(i < BH ? x.cost : 0.0);
+        return cu_makespan(cost, cus_per_xcd, per_cu);
+    };
+    std::vector<G> g;
+    build(max_nt, g);
+    const double base = makespan(g, BH);
+    double best = base * 0.97;
+    int best_ch = 0;
+    for (int ch = max_nt - 1; ch >= std::max(2, max_nt / 8); --ch) {
+        build(ch, g);
+        int n_split = 0;
+        for (const G& x : g) n_split += x.chunk == 0 && x.n > 1;
+        if ((int)g.size() > kMaxBwdGroups || n_split == 0) continue;
+        const double ms = makespan(g, bwd_padded_heads(BH));
+        if (ms < best) {
+            best = ms;
+            best_ch = ch;
+        }
+    }
+    if (!best_ch) return;
+    build(best_ch, g);
+    std::vector<int> split_of((size_t)nkb, -1), slot0((size_t)nkb, 0);
+    int n_split = 0, n_slots = 0;
+    for (int j = 0; j < nkb; ++j) {
+        const int n = nt[(size_t)j];
+        if (n > best_ch) {
+            split_of[(size_t)j] = n_split++;
+            slot0[(size_t)j] = n_slots;
+            n_slots += (n + best_ch - 1) / best_ch;
+        }
+    }
+    for (const G& x : g) {
+        BwdGroup& o = out->groups[out->n_groups++];
+        o.kb = x.kb;
+        o.t0 = x.a;
+        o.t1 = x.b;
+        o.split = split_of[(size_t)x.kb];
+        o.chunk = x.chunk;
+        o.n_chunks = x.n;
+        o.slot0 = slot0[(size_t)x.kb];
+    }
+    out->n_split = n_split;
+    out->n_slots = n_slots;
+}
+
+void bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan* out) {
+    *out = BwdPlan{};
+    if (!causal) return;
+    int per_cu = 0, cus_per_xcd = 0;
+    bwd_slots(D, bf16, &per_cu, &cus_per_xcd);
+    static std::mutex mu;
+    static std::map<std::array<int, 7>, BwdPlan> cache;
+    const std::array<int, 7> key{B * H, Tq, Tk, D, bf16, per_cu, cus_per_xcd};
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        auto it = cache.find(key);
+        if (it != cache.end()) {
+            *out = it->second;
+            return;
+        }
+    }
+    bwd_plan_compute(B, H, Tq, Tk, bf16 ? 1 : 0, per_cu, cus_per_xcd, out);
+    std::lock_guard<std::mutex> lk(mu);
+    if (cache.size() > 256) cache.clear();
+    cache[key] = *out;
+}
+
+size_t bwd_split_workspace_bytes(const BwdPlan& plan, int B, int H, int D) {
+    if (!plan.n_split) return 0;
+    const size_t bh = (size_t)B * H;
+    const size_t part = (size_t)plan.n_slots * bh * 2 * (size_t)D * kBwdBK * sizeof(float);
+    return part + (size_t)plan.n_split * bh * sizeof(unsigned);
+}
+
 template <int D, typename E>
 static int launch_bwd_t(const BwdParams& p, hipStream_t s) {
     constexpr int RPB = 256 / (D / 4);
@@ -354,7 +562,7 @@ static int launch_bwd_t(const BwdParams& p, hipStream_t s) {
         if (e) return e;
         hipLaunchKernelGGL((bwd_cvt_kernel<D>), pre_grid, dim3(256), 0, s, p);
     } else {
-        const dim3 grid((unsigned)(p.n_kblocks * p.B * p.H));
+        const dim3 grid((unsigned)(p.n_groups ? p.n_groups * bwd_padded_heads(p.B * p.H) : p.n_kblocks * p.B * p.H));
         hipLaunchKernelGGL((bwd_main_kernel<D, E>), grid, dim3(256), 0, s, p);
     }
     return (int)hipGetLastError();

@@ -22,6 +22,7 @@
 // stores stay 32-bit.  Softmax statistics, P and dS are computed in fp32.
 #include <type_traits>
 
+#include "bwd_split.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -72,10 +73,10 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
     const int l16 = lane & 15;
     const int g4 = lane >> 4;
 
-    const int BH = p.B * p.H;
-    const int w = blockIdx.x;
-    const int kblk = w / BH;
-    const int bh = w % BH;
+    const BwdWork wk = bwd_work(p);
+    if (wk.bh >= p.B * p.H) return;  // padding workgroup of a split plan's grid
+    const int kblk = wk.kblk;
+    const int bh = wk.bh;
     const int b = bh / p.H;
     const int h = bh % p.H;
 
@@ -129,9 +130,8 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
         dk_acc[i] = f32x16{};
     }
 
-    int q_begin = 0;
-    if (p.causal) q_begin = max(0, k0 - p.off);
-    q_begin = (q_begin / BQ) * BQ;
+    const int q_begin = wk.q_begin;
+    const int q_end = wk.q_end;
     const float c = p.c;
 
     // Q / dO staging, prefetched one query tile ahead in registers: tile q0's
@@ -202,8 +202,8 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
     // last tile): conditional blocks would make the compiler wait for every
     // outstanding memory operation, the previous tile's dQ atomics included,
     // at the top of each tile.
-    for (int q0 = q_begin; q0 < p.Tq; q0 += BQ) {
-        gload_q(q0 + BQ, q0 + BQ < p.Tq ? p.Tq : 0);
+    for (int q0 = q_begin; q0 < q_end; q0 += BQ) {
+        gload_q(q0 + BQ, q0 + BQ < q_end ? p.Tq : 0);
 
         const bool active = !p.causal || (q0 + BQ - 1 + p.off >= k0w);
         bf16x8 pb[2], dsb[2];
@@ -294,6 +294,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
         __syncthreads();
     }
 
+    if (!bwd_fixup(p, wk, dk_acc, dv_acc)) return;
     if (key < p.Tk) {
         uint16_t* dKp = (uint16_t*)p.dk + b * p.sdk.b + h * p.sdk.h + (int64_t)key * p.sdk.t;
         uint16_t* dVp = (uint16_t*)p.dv + b * p.sdv.b + h * p.sdv.h + (int64_t)key * p.sdv.t;
@@ -313,8 +314,17 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
     }
 }
 
+int bwd_main_bf16_occupancy(int D, int* blocks_per_cu) {
+    switch (D) {
+        case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<32>, 256, 0);
+        case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<64>, 256, 0);
+        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<128>, 256, 0);
+        default: return (int)hipErrorInvalidValue;
+    }
+}
+
 int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s) {
-    const dim3 grid((unsigned)(p.n_kblocks * p.B * p.H));
+    const dim3 grid((unsigned)(p.n_groups ? p.n_groups * bwd_padded_heads(p.B * p.H) : p.n_kblocks * p.B * p.H));
     switch (p.D) {
         case 32: hipLaunchKernelGGL((bwd_main_bf16_kernel<32>), grid, dim3(256), 0, s, p); break;
         case 64: hipLaunchKernelGGL((bwd_main_bf16_kernel<64>), grid, dim3(256), 0, s, p); break;

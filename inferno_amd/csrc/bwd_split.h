@@ -1,0 +1,116 @@
+// bwd_split.h -- work assignment of a backward workgroup and the fix-up that
+// completes a split key block (shared by the fp32 and bf16 main kernels).
+//
+// Without a plan, workgroup w takes key block w / (B*H) and every query tile
+// that can see it.  With a plan, w takes group w / BHp and head w % BHp, with
+// BHp = B*H rounded up to a multiple of 8 (workgroups of the padding heads
+// exit at once): a key block and a range of its query tiles.  When a key
+// block's tiles are split over several groups, each group ends with partial
+// dK^T / dV^T accumulators; every group stores its partial, and the group that
+// finishes last (an arrival counter per (key block, b, h)) sums all partials in
+// chunk order and stores dK and dV.  No workgroup waits for another, so the
+// split cannot stall the grid.
+//
+// The hand-over stays inside one XCD's L2.  The dispatcher deals workgroups
+// to the 8 XCDs round-robin (w mod 8), and w mod 8 = head mod 8 for every
+// group, so all chunks of a (key block, head) run on one XCD and share its L2.
+// The writer waits for its partial stores to complete (they pass the
+// write-through L1 into the L2) before counting; the last arriver invalidates
+// its CU's L1 before reading the partials.  A device-scope fence would instead
+// write back and invalidate the whole L2 of the XCD, evicting every other
+// resident workgroup's tiles (measured: backward 18% slower at config 2 fp32,
+// 2.1x at bf16).
+#pragma once
+
+#include "common.h"
+#include "kernels.h"
+
+namespace inf {
+
+struct BwdWork {
+    int kblk, bh;
+    int q_begin, q_end;  // query rows [q_begin, q_end), q_begin a multiple of kBwdBQ
+    int split, chunk, n_chunks, slot0;
+};
+
+// Heads per group in the launch grid of a split plan.
+__host__ __device__ inline int bwd_padded_heads(int BH) { return (BH + 7) / 8 * 8; }
+
+// Work of this workgroup; bh >= B*H marks a padding workgroup (none to do).
+__device__ __forceinline__ BwdWork bwd_work(const BwdParams& p) {
+    const int BH = p.B * p.H;
+    const int w = blockIdx.x;
+    BwdWork r;
+    r.bh = w % BH;
+    if (p.n_groups) {
+        const int BHp = bwd_padded_heads(BH);
+        r.bh = w % BHp;
+        const BwdGroup g = p.groups[w / BHp];
+        r.kblk = g.kb;
+        r.q_begin = g.t0 * kBwdBQ;
+        r.q_end = min(p.Tq, g.t1 * kBwdBQ);
+        r.split = g.split;
+        r.chunk = g.chunk;
+        r.n_chunks = g.n_chunks;
+        r.slot0 = g.slot0;
+    } else {
+        r.kblk = w / BH;
+        int qb = p.causal ? max(0, r.kblk * kBwdBK - p.off) : 0;
+        r.q_begin = (qb / kBwdBQ) * kBwdBQ;
+        r.q_end = p.Tq;
+        r.split = -1;
+        r.chunk = 0;
+        r.n_chunks = 1;
+        r.slot0 = 0;
+    }
+    return r;
+}
+
+// For a split key block: store this workgroup's dK^T and dV^T accumulators
+// (N f32x16 per lane each) as its partial, count the arrival, and, in the last
+// workgroup to arrive, replace the accumulators by the chunk-ordered sum of
+// all partials.  Returns whether this workgroup goes on to store dK and dV.
+// Must be reached by every thread of the workgroup.
+template <int N>
+__device__ __forceinline__ bool bwd_fixup(const BwdParams& p, const BwdWork& wk, f32x16 (&dk)[N], f32x16 (&dv)[N]) {
+    if (wk.split < 0) return true;
+    constexpr int NACC = 2 * N;
+    auto acc = [&](int a) -> f32x16& { return a < N ? dk[a] : dv[a - N]; };
+    __shared__ int s_last;
+    const int tid = threadIdx.x;
+    const int BH = p.B * p.H;
+    const size_t per_wg = (size_t)256 * NACC * 16;  // floats of one partial
+    auto slot_ptr = [&](int c) { return p.part + ((size_t)(wk.slot0 + c) * BH + wk.bh) * per_wg; };
+    // lane-major: f32x4 j of accumulator a of thread tid at index (4a + j) * 256 + tid
+    float* mine = slot_ptr(wk.chunk);
+#pragma unroll
+    for (int a = 0; a < NACC; ++a)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<f32x4*>(mine + ((size_t)(4 * a + j) * 256 + tid) * 4) =
+                f32x4{acc(a)[4 * j], acc(a)[4 * j + 1], acc(a)[4 * j + 2], acc(a)[4 * j + 3]};
+    __builtin_amdgcn_s_waitcnt(0);  // the partial's stores have reached the L2
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(&p.counters[wk.split * BH + wk.bh], 1u) == (unsigned)(wk.n_chunks - 1);
+    __syncthreads();
+    if (!s_last) return false;
+    asm volatile("buffer_inv sc0" ::: "memory");  // drop this CU's L1 lines: read the partials from L2
+#pragma unroll
+    for (int a = 0; a < NACC; ++a) acc(a) = f32x16{};
+    for (int c = 0; c < wk.n_chunks; ++c) {
+        const float* src = slot_ptr(c);
+#pragma unroll
+        for (int a = 0; a < NACC; ++a)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(src + ((size_t)(4 * a + j) * 256 + tid) * 4);
+                acc(a)[4 * j] += v[0];
+                acc(a)[4 * j + 1] += v[1];
+                acc(a)[4 * j + 2] += v[2];
+                acc(a)[4 * j + 3] += v[3];
+            }
+    }
+    return true;
+}
+
+}  // namespace inf

@@ -106,6 +106,9 @@ int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dt
         case INF_OP_ATTN_BWD: {
             size_t n = round_up(bh * Tq * sizeof(float));                       // delta
             if (dt == INF_BF16) n += round_up(bh * Tq * (size_t)D * sizeof(float));  // dQ accumulator
+            inf::BwdPlan plan;                                                  // causal split plan
+            inf::bwd_plan(B, H, Tq, Tk, D, 1, dt == INF_BF16, &plan);
+            n += round_up(inf::bwd_split_workspace_bytes(plan, B, H, D));
             *out_bytes = n;
             return INF_OK;
         }
@@ -197,6 +200,18 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     p.scale = scale;
     p.c = scale * 1.4426950408889634f;
     p.n_kblocks = (Tk + inf::kBwdBK - 1) / inf::kBwdBK;
+    inf::BwdPlan plan;
+    inf::bwd_plan(B, H, Tq, Tk, D, p.causal, dt == INF_BF16, &plan);
+    if (plan.n_groups) {
+        size_t offset = round_up(bh * Tq * sizeof(float));
+        if (dt == INF_BF16) offset += round_up(bh * Tq * (size_t)D * sizeof(float));
+        const size_t part_bytes = (size_t)plan.n_slots * bh * 2 * (size_t)D * inf::kBwdBK * sizeof(float);
+        p.part = reinterpret_cast<float*>(ws + offset);
+        p.counters = reinterpret_cast<unsigned*>(ws + offset + part_bytes);
+        p.n_groups = plan.n_groups;
+        p.n_split = plan.n_split;
+        std::memcpy(p.groups, plan.groups, sizeof(p.groups));
+    }
     return hip_status(inf::launch_attn_bwd(p, dt == INF_BF16, (hipStream_t)stream));
 }
 

@@ -55,6 +55,26 @@ struct FwdPlan {
 void fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan* out);
 size_t fwd_workspace_bytes(const FwdPlan& plan, int B, int H, int D);
 
+// Backward work split: a group is one key block's query-tile range [t0, t1)
+// (in 32-row tiles) for every (b, h).  Groups of a split key block write fp32
+// partial dK^T / dV^T accumulators to `part` (slot slot0 + chunk); the last of
+// its `n_chunks` groups to finish (per-(split, b, h) counter) adds the others'
+// partials to its own and stores dK and dV.
+constexpr int kMaxBwdGroups = 48;
+struct BwdGroup {
+    int kb, t0, t1;
+    int split;     // -1: unsplit key block, else index of the split key block
+    int chunk, n_chunks, slot0;
+};
+
+struct BwdPlan {
+    int n_groups = 0, n_split = 0, n_slots = 0;
+    BwdGroup groups[kMaxBwdGroups];
+};
+void bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan* out);
+// Bytes of the split plan's workspace: partials then counters (0 without a split).
+size_t bwd_split_workspace_bytes(const BwdPlan& plan, int B, int H, int D);
+
 struct BwdParams {
     const void* q;
     const void* k;
@@ -73,6 +93,11 @@ struct BwdParams {
     int causal, off;
     float scale, c;
     int n_kblocks;
+    // split plan (n_groups == 0: workgroup w takes key block w / (B*H), all its tiles)
+    int n_groups, n_split;
+    float* part;            // n_slots * B*H * 2*D*kBwdBK floats (lane-major accumulators)
+    unsigned* counters;     // n_split * B*H, zeroed by bwd_pre
+    BwdGroup groups[kMaxBwdGroups];
 };
 
 struct DecodeParams {
@@ -224,6 +249,7 @@ int launch_bcast(int op, const void* a, const void* b, void* out, int64_t n, int
 int launch_attn_fwd(const FwdParams& p, int bf16, hipStream_t s);
 int launch_attn_fwd_bf16(const FwdParams& p, hipStream_t s);  // bf16-MFMA forward
 int launch_attn_bwd(const BwdParams& p, int bf16, hipStream_t s);
+int bwd_main_bf16_occupancy(int D, int* blocks_per_cu);  // hipError_t
 int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s);  // bf16-MFMA backward main kernel
 int launch_attn_decode(const DecodeParams& p, int bf16, hipStream_t s);
 // Decode split plan (number of key splits per row, keys per split) for a shape.

@@ -115,6 +115,44 @@ def test_fwd_split_plan_f32(ia, B, H, Tq, Tk, D):
         assert e <= TOL_F32, f"{name} rel err {e:.3e}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,H,Tq,Tk,D", [
+    (1, 4, 1024, 1024, 64),    # key block 0 split 8 ways
+    (1, 3, 777, 777, 64),
+    (1, 2, 1000, 1000, 32),
+    (1, 2, 1500, 1500, 128),
+    (1, 4, 900, 1024, 64),     # end-aligned causal
+    (1, 2, 130, 1100, 64),     # short query block against a long cache
+])
+def test_bwd_split_plan(ia, dtype, B, H, Tq, Tk, D):
+    """Few workgroups per CU: the backward splits the query-tile range of its heaviest key
+    blocks across workgroups; the last chunk of each to finish sums the partial dK / dV.
+    The workspace (partials, arrival counters) starts NaN-filled and is reused for a second
+    call, whose results must be bit-identical (chunk-ordered sum, counters reset per call)."""
+    print(f"[case] bwd split {dtype} B{B} H{H} Tq{Tq} Tk{Tk} D{D}", flush=True)
+    bf = dtype == torch.bfloat16
+    dt = ia.INF_BF16 if bf else ia.INF_F32
+    ru = lambda x: (x + 255) // 256 * 256
+    base = ru(B * H * Tq * 4) + (ru(B * H * Tq * D * 4) if bf else 0)
+    nbytes = ia.workspace_bytes(ia.OP_ATTN_BWD, B, H, Tq, Tk, D, dt)
+    assert nbytes > base, "expected a split plan for this shape"
+    q, k, v, do = oracle.attn_inputs(B, H, Tq, D, seed=17, Tk=Tk)
+    if bf:
+        q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do)
+    Q, K, V, dO = (dev(x, dtype) for x in (q, k, v, do))
+    o, lse = ia.attn_fwd(Q, K, V)
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")
+    first = ia.attn_bwd(Q, K, V, o, dO, lse, workspace=ws)
+    second = ia.attn_bwd(Q, K, V, o, dO, lse, workspace=ws)
+    torch.cuda.synchronize()
+    tol = TOL_BF16 if bf else TOL_F32
+    for name, x, r in zip(("dQ", "dK", "dV"), first, (dq_r, dk_r, dv_r)):
+        e = oracle.rel_err(host(x), r)
+        assert e <= tol, f"{name} rel err {e:.3e}"
+    assert torch.equal(first[1], second[1]) and torch.equal(first[2], second[2])
+
+
 def test_noncausal_f32(ia):
     print("[case] noncausal", flush=True)
     q, k, v, do = oracle.attn_inputs(1, 2, 96, 64, seed=7)
