@@ -102,7 +102,11 @@ int inf_attn_fwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
  * (mmbackward.cpp:36-98, softmaxbackward.cpp:36-128,
  * multiplybackward.cpp:34-57, transposebackward.cpp:35-51).
  * workspace: at least inf_attn_workspace_bytes(INF_OP_ATTN_BWD, ...) bytes,
- * 256-byte aligned; its contents on entry do not matter.
+ * 256-byte aligned; its contents on entry do not matter.  It holds the row
+ * dots dO.O, the fp32 dQ accumulator (bf16), and, for causal shapes whose
+ * grid leaves the device unevenly loaded, the partial dK / dV of split key
+ * blocks and their arrival counters.  Calls that share one workspace must not
+ * overlap.
  */
 int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, const void* v,
                  inf_strides sv, const void* o, inf_strides so, const void* dout,
