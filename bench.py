@@ -36,36 +36,75 @@ def flops_fwd(B, H, T, D):
     return 2.0 * B * H * T * T * D  # 4*B*H*T^2*D / 2 (causal)
 
 
-def cpu_baseline(B, H, T, D, heads: int):
-    """Time the restated reference CPU path (one core) on `heads` heads of the workload."""
+def _host_cpu():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model
+
+
+def cpu_baseline(B, H, T, D, heads: int, c4_heads: int = 0):
+    """Time the restated reference CPU path on one pinned core: `heads` heads of config 2
+    (fwd+bwd), the whole config-5 decode step, and (if c4_heads) config 4 on c4_heads heads,
+    extrapolated to its 16 heads (heads are independent)."""
     import numpy as np
 
     import oracle
 
-    Hs = min(heads, B * H)
-    q, k, v, do = oracle.attn_inputs(1, Hs, T, D, seed=42)
-    t0 = time.perf_counter()
-    oracle.attn_fwd(q, k, v)
-    oracle.attn_bwd(q, k, v, do)
-    dt = time.perf_counter() - t0
-    f = 3.5 * flops_fwd(1, Hs, T, D)
-    cpu = "unknown"
+    prev = os.sched_getaffinity(0)
+    core = min(prev)
+    os.sched_setaffinity(0, {core})
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+        Hs = min(heads, B * H)
+        q, k, v, do = oracle.attn_inputs(1, Hs, T, D, seed=42)
+        t0 = time.perf_counter()
+        oracle.attn_fwd(q, k, v)
+        oracle.attn_bwd(q, k, v, do)
+        dt = time.perf_counter() - t0
+        f = 3.5 * flops_fwd(1, Hs, T, D)
+        # config 5: one decode step, B32 H12 Tk2048 D64 (query sees every cached key)
+        Bd, Hd, Tk = 32, 12, 2048
+        kc, vc = oracle.randn(500, (Bd, Hd, Tk, D)), oracle.randn(501, (Bd, Hd, Tk, D))
+        qd = oracle.randn(502, (Bd, Hd, 1, D))
+        t1 = time.perf_counter()
+        oracle.attn_fwd(qd, kc, vc)
+        dt5 = time.perf_counter() - t1
+        nbytes5 = 2 * Bd * Hd * Tk * D * 4 + 2 * Bd * Hd * D * 4
+        extra = {
+            "c5_decode": {"seconds": round(dt5, 4), "us_per_step": round(dt5 * 1e6, 1),
+                          "GBs": round(nbytes5 / dt5 / 1e9, 3), "sample": "the whole step, B32 H12 Tk2048 D64"},
+        }
+        if c4_heads > 0:
+            T4, D4 = 8192, 128
+            q4, k4, v4, do4 = oracle.attn_inputs(1, c4_heads, T4, D4, seed=42, qk_sigma=3.0)
+            t2 = time.perf_counter()
+            oracle.attn_fwd(q4, k4, v4)
+            oracle.attn_bwd(q4, k4, v4, do4)
+            dt4 = time.perf_counter() - t2
+            extra["c4"] = {"seconds": round(dt4, 3), "heads_timed": c4_heads,
+                           "TFLOPs": 3.5 * flops_fwd(1, c4_heads, T4, D4) / dt4 / 1e12,
+                           "extrapolated_s_for_16_heads": round(dt4 * 16 / c4_heads, 1)}
+        else:
+            extra["c4"] = "not run (one head takes over a minute on one core); bench.py --cpu-c4-heads 1"
+    finally:
+        os.sched_setaffinity(0, prev)
     return {
         "value": f / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": 1,
         "kind": "port",
         "sample": f"{Hs} of {B * H} heads (T={T}, D={D}) fwd+bwd through the restated reference "
-                  f"CPU chain, {dt:.2f} s single-threaded on {cpu}; the backward recomputes the "
-                  f"forward as the reference chain would; FLOPs counted with the causal convention",
+                  f"CPU chain, {dt:.2f} s on one core pinned to CPU {core} of {os.cpu_count()} "
+                  f"({_host_cpu()}); the backward recomputes the forward as the reference chain "
+                  f"would; FLOPs counted with the causal convention",
         "seconds": dt,
+        "host": {"cpu": _host_cpu(), "nproc": os.cpu_count(), "pinned_core": core},
+        "configs": extra,
     }
 
 
@@ -79,6 +118,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--cpu-heads", type=int, default=12, help="heads in the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--cpu-c4-heads", type=int, default=0, help="config-4 heads timed on the CPU (0 = skip)")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16, config-3 and config-4 lines")
     ap.add_argument("--gpt-steps", type=int, default=5, help="timed steps of the config-3 GPT line")
@@ -220,7 +260,7 @@ def main():
         out["configs"]["gpt_generate"] = bench_generate()
 
     if args.cpu_heads > 0:
-        out["cpu_baseline"] = cpu_baseline(B, H, T, D, args.cpu_heads)
+        out["cpu_baseline"] = cpu_baseline(B, H, T, D, args.cpu_heads, args.cpu_c4_heads)
     print(json.dumps(out), flush=True)
 
 
@@ -272,7 +312,17 @@ def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10
     F = flops_fwd(B, H, T, D)
     peak = MFMA_FP32_PEAK_TFLOPS if dtype == "f32" else MFMA_BF16_PEAK_TFLOPS
     tot = 3.5 * F / ((fwd_ms + bwd_ms) * 1e-3) / 1e12
+    # minimal HBM bytes: fwd Q,K,V in and O out (+ fp32 LSE); bwd Q,K,V,O,dO in and dQ,dK,dV out
+    # (+ LSE); the second roof for the bf16 lines, whose forward sits near the bf16 ridge
+    esz = 4 if dtype == "f32" else 2
+    n = B * H * T * D
+    fwd_bytes = 4 * n * esz + B * H * T * 4
+    bwd_bytes = 8 * n * esz + B * H * T * 4
+    roofs = {"fwd_hbm_bytes": fwd_bytes, "fwd_GBs": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9, 1),
+             "bwd_hbm_bytes": bwd_bytes, "bwd_GBs": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1),
+             "hbm_peak_GBs": HBM_PEAK_GBS}
     return {
+        "roofs": roofs,
         "shape": f"B{B} H{H} T{T} D{D}", "dtype": dtype if dtype == "f32" else "bf16-in/f32-acc",
         "qk_sigma": qk_sigma, "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
         "fwd_tflops": round(F / (fwd_ms * 1e-3) / 1e12, 2),

@@ -105,7 +105,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
     const int l16 = lane & 15;
     const int g4 = lane >> 4;
 
-    const BwdWork wk = bwd_work(p);
+    const BwdWork wk = bwd_work<kBwdBK>(p);
     if (wk.bh >= p.B * p.H) return;  // padding workgroup of a split plan's grid
     const int kblk = wk.kblk;
     const int bh = wk.bh;
@@ -316,7 +316,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
     }
 
     // ---- dK = scale * dK^T^T, dV = dV^T^T ------------------------------------------
-    if (!bwd_fixup(p, wk, dk_acc, dv_acc)) return;
+    if (!bwd_fixup<256>(p, wk, dk_acc, dv_acc)) return;
     if (key < p.Tk) {
         E* dKp = (E*)p.dk + b * p.sdk.b + h * p.sdk.h + (int64_t)key * p.sdk.t;
         E* dVp = (E*)p.dv + b * p.sdv.b + h * p.sdv.h + (int64_t)key * p.sdv.t;
@@ -367,10 +367,13 @@ __global__ __launch_bounds__(256) void bwd_cvt_kernel(BwdParams p) {
 
 static constexpr double kBwdPairGain = 0.08;  // throughput gained per extra resident workgroup
 // Per-workgroup fixed cost (K/V loads, K^T staging) and the partial store /
-// reduction of a split chunk, in query tiles of that dtype's kernel: a bf16
-// tile costs ~1/5 of an fp32 one, the fixed costs about the same time.
-static constexpr double kBwdOverhead[2] = {0.3, 1.5};
-static constexpr double kBwdFixup[2] = {0.4, 2.0};
+// reduction of a split chunk, in query tiles of that dtype's kernel.  A bf16
+// tile costs a fraction of an fp32 one while the fixed costs take about the
+// same time; the bf16 figures are set from measurement (splits lost 5-8% at
+// B4 H12 and config 2 with smaller ones), so bf16 splits only grids far below
+// the device's size.
+static constexpr double kBwdOverhead[2] = {0.3, 5.0};
+static constexpr double kBwdFixup[2] = {0.4, 8.0};
 
 static double share_rate(size_t k) { return k <= 1 ? 1.0 : (1.0 + kBwdPairGain * (double)(k - 1)) / (double)k; }
 
@@ -445,15 +448,17 @@ static void bwd_slots(int D, int bf16, int* per_cu, int* cus_per_xcd) {
     *cus_per_xcd = it->second.second;
 }
 
-static void bwd_plan_compute(int B, int H, int Tq, int Tk, int bf16, int per_cu, int cus_per_xcd, BwdPlan* out) {
+static void bwd_plan_compute(int B, int H, int Tq, int Tk, int D, int bf16, int per_cu, int cus_per_xcd,
+                             BwdPlan* out) {
     const int BH = B * H;
-    const int nkb = (Tk + kBwdBK - 1) / kBwdBK;
+    const int bk = bwd_keys_per_wg(bf16, D);
+    const int nkb = (Tk + bk - 1) / bk;
     const int off = Tk - Tq;
     if ((int64_t)nkb * BH > 8LL * 8 * cus_per_xcd * per_cu) return;  // the tail is a small share
     std::vector<int> t0((size_t)nkb), nt((size_t)nkb);
     int max_nt = 0;
     for (int j = 0; j < nkb; ++j) {
-        t0[(size_t)j] = std::max(0, j * kBwdBK - off) / kBwdBQ;
+        t0[(size_t)j] = std::max(0, j * bk - off) / kBwdBQ;
         nt[(size_t)j] = (Tq + kBwdBQ - 1) / kBwdBQ - t0[(size_t)j];
         max_nt = std::max(max_nt, nt[(size_t)j]);
     }
@@ -524,6 +529,7 @@ static void bwd_plan_compute(int B, int H, int Tq, int Tk, int bf16, int per_cu,
 
 void bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan* out) {
     *out = BwdPlan{};
+    out->bk = bwd_keys_per_wg(bf16, D);
     if (!causal) return;
     int per_cu = 0, cus_per_xcd = 0;
     bwd_slots(D, bf16, &per_cu, &cus_per_xcd);
@@ -538,7 +544,7 @@ void bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan
             return;
         }
     }
-    bwd_plan_compute(B, H, Tq, Tk, bf16 ? 1 : 0, per_cu, cus_per_xcd, out);
+    bwd_plan_compute(B, H, Tq, Tk, D, bf16 ? 1 : 0, per_cu, cus_per_xcd, out);
     std::lock_guard<std::mutex> lk(mu);
     if (cache.size() > 256) cache.clear();
     cache[key] = *out;
@@ -547,7 +553,7 @@ void bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan
 size_t bwd_split_workspace_bytes(const BwdPlan& plan, int B, int H, int D) {
     if (!plan.n_split) return 0;
     const size_t bh = (size_t)B * H;
-    const size_t part = (size_t)plan.n_slots * bh * 2 * (size_t)D * kBwdBK * sizeof(float);
+    const size_t part = (size_t)plan.n_slots * bh * 2 * (size_t)D * plan.bk * sizeof(float);
     return part + (size_t)plan.n_split * bh * sizeof(unsigned);
 }
 

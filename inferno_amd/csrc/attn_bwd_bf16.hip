@@ -1,10 +1,13 @@
 // attn_bwd_bf16.hip -- fused causal attention backward, bf16 inputs, fp32
 // accumulation, on gfx950 bf16 MFMAs.
 //
-// Same ownership as the fp32 kernel (attn_bwd.hip): 4 waves x 32 keys per
-// workgroup, K and V operands and the dK^T / dV^T accumulators in VGPRs for
-// the whole kernel (atomic-free dK, dV), query tiles of 32 rows, dQ through
-// LDS and fp32 atomics into the accumulator.  A bf16 MFMA reduces 16 (32x32x16)
+// Same ownership as the fp32 kernel (attn_bwd.hip), with 8 waves x 32 keys
+// = 256 keys per workgroup at D <= 64 (the fp32 kernel and D = 128: 4 x 32): K and V operands and the
+// dK^T / dV^T accumulators in VGPRs for the whole kernel (atomic-free dK, dV),
+// query tiles of 32 rows, dQ through LDS and fp32 atomics into the
+// accumulator.  At bf16 speed the dQ atomics are a device-wide throughput
+// limit (at config 2 the kernel measured 23% faster with them left out);
+// 256-key blocks add each dQ element once per 256 keys instead of per 128.  A bf16 MFMA reduces 16 (32x32x16)
 // or 32 (16x16x32) elements with each lane supplying 8 consecutive ones, so
 // every operand must be contiguous along its reduction index:
 //   S = Q K^T, dP = dO V^T      reduce over d: Q, dO row-major in LDS; K, V rows
@@ -40,9 +43,11 @@ __device__ __forceinline__ bf16x8 cat4(bf16x4 lo, bf16x4 hi) {
 }
 
 template <int D>
-__global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(BwdParams p) {
-    constexpr int BQ = kBwdBQ;           // 32 query rows per step
-    constexpr int BK = kBwdBK;           // 128 keys per workgroup
+__global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || D >= 128) ? 1 : 2) void bwd_main_bf16_kernel(BwdParams p) {
+    constexpr int NW = bwd_bf16_waves(D);  // waves per workgroup, 32 keys each
+    constexpr int NT = 64 * NW;            // threads
+    constexpr int BQ = kBwdBQ;             // 32 query rows per step
+    constexpr int BK = 32 * NW;            // keys per workgroup
     constexpr int NKK = D / 16;          // S / dP MFMAs along d
     constexpr int NDB = D / 32;          // 32-wide d blocks of dK^T / dV^T
     constexpr int C8 = D / 8;            // 8-element chunks per row
@@ -51,10 +56,10 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
     constexpr int SS = BK + 8;           // dS stride (bf16)
     constexpr int KTS = BK + 8;          // K^T stride (bf16)
     constexpr int QTASK = (BQ / 2) * C8;                 // (row pair, chunk) tasks per tensor
-    constexpr int QLPT = (2 * QTASK + 255) / 256;        // Q and dO together, per thread
+    constexpr int QLPT = (2 * QTASK + NT - 1) / NT;      // Q and dO together, per thread
     constexpr int KTASK = (BK / 2) * C8;
-    constexpr int KLPT = (KTASK + 255) / 256;
-    constexpr int DQB = D / 32;          // 16x16 dQ blocks per wave (2 * D/16 over 4 waves)
+    constexpr int KLPT = (KTASK + NT - 1) / NT;
+    constexpr int NDQ = 2 * (D / 16);    // 16x16 dQ blocks of a query tile, dealt to the waves
 
     __shared__ __attribute__((aligned(16))) __bf16 Qs[BQ][QS];
     __shared__ __attribute__((aligned(16))) __bf16 dOs[BQ][QS];
@@ -73,7 +78,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
     const int l16 = lane & 15;
     const int g4 = lane >> 4;
 
-    const BwdWork wk = bwd_work(p);
+    const BwdWork wk = bwd_work<BK>(p);
     if (wk.bh >= p.B * p.H) return;  // padding workgroup of a split plan's grid
     const int kblk = wk.kblk;
     const int bh = wk.bh;
@@ -104,10 +109,10 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
         }
     }
 
-    // K^T of the 128-key block (keys contiguous per d row), for dQ.
+    // K^T of the key block (keys contiguous per d row), for dQ.
 #pragma unroll
     for (int i = 0; i < KLPT; ++i) {
-        const int f = tid + 256 * i;
+        const int f = tid + NT * i;
         if (f >= KTASK) continue;
         const int kp = f % (BK / 2), c8 = f / (BK / 2);
         const int r0 = k0 + 2 * kp;
@@ -145,14 +150,14 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
     // values only, so no arithmetic waits on the loads here.  Whether chunk f
     // is of Q or dO is uniform over each wave for every head dim (QTASK is a
     // multiple of 64), which keeps the selected resource in SGPRs.
-    static_assert(QTASK % 64 == 0 && 256 % QTASK == 0 || QTASK % 256 == 0, "Q / dO split must be wave-uniform");
+    static_assert(QTASK % 64 == 0, "Q / dO split must be wave-uniform");
     auto gload_q = [&](int q0, int lim) {
         const int rows = min(lim - q0, BQ);
         const auto rq = row_rsrc(Q, p.sq.t, q0, rows, D);
         const auto rdo = row_rsrc(dO, p.sdo.t, q0, rows, D);
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
-            const int f = tid + 256 * i;
+            const int f = tid + NT * i;
             ra[i] = rb[i] = bf16x8{};
             if (f >= 2 * QTASK) continue;
             const int which = __builtin_amdgcn_readfirstlane(f / QTASK);  // 0: Q, 1: dO
@@ -171,7 +176,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
     auto sstore_q = [&]() {
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
-            const int f = tid + 256 * i;
+            const int f = tid + NT * i;
             if (f >= 2 * QTASK) continue;
             const int which = f / QTASK;
             const int rem = f % QTASK;
@@ -270,13 +275,13 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
         // (zeros after the last tile, never read)
         sstore_q();
 
-        // ---- dQ tile (32 x D) += dS (32 x 128) K (128 x D), 16x16 blocks ---------
-        // fp32 atomics through a buffer resource over the tile's rows: rows
-        // past Tq fall outside it and the hardware drops those adds.
+        // ---- dQ tile (32 x D) += dS (32 x BK) K (BK x D), 16x16 blocks ---------
+        // The 2 * D/16 blocks are dealt to the waves (D = 32: waves 4-7 have
+        // none).  fp32 atomics through a buffer resource over the tile's rows:
+        // rows past Tq fall outside it and the hardware drops those adds.
         const auto rdq = row_rsrc(dQa, p.sacc.t, q0, min(p.Tq - q0, BQ), D);
 #pragma unroll
-        for (int bi = 0; bi < DQB; ++bi) {
-            const int blk = wave * DQB + bi;
+        for (int blk = wave; blk < NDQ; blk += NW) {
             const int qh = blk & 1;
             const int dc = blk >> 1;
             f32x4 acc;
@@ -294,7 +299,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
         __syncthreads();
     }
 
-    if (!bwd_fixup(p, wk, dk_acc, dv_acc)) return;
+    if (!bwd_fixup<NT>(p, wk, dk_acc, dv_acc)) return;
     if (key < p.Tk) {
         uint16_t* dKp = (uint16_t*)p.dk + b * p.sdk.b + h * p.sdk.h + (int64_t)key * p.sdk.t;
         uint16_t* dVp = (uint16_t*)p.dv + b * p.sdv.b + h * p.sdv.h + (int64_t)key * p.sdv.t;
@@ -316,9 +321,9 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_bf16_kernel(
 
 int bwd_main_bf16_occupancy(int D, int* blocks_per_cu) {
     switch (D) {
-        case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<32>, 256, 0);
-        case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<64>, 256, 0);
-        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<128>, 256, 0);
+        case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<32>, 64 * bwd_bf16_waves(32), 0);
+        case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<64>, 64 * bwd_bf16_waves(64), 0);
+        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<128>, 64 * bwd_bf16_waves(128), 0);
         default: return (int)hipErrorInvalidValue;
     }
 }
@@ -326,9 +331,9 @@ int bwd_main_bf16_occupancy(int D, int* blocks_per_cu) {
 int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s) {
     const dim3 grid((unsigned)(p.n_groups ? p.n_groups * bwd_padded_heads(p.B * p.H) : p.n_kblocks * p.B * p.H));
     switch (p.D) {
-        case 32: hipLaunchKernelGGL((bwd_main_bf16_kernel<32>), grid, dim3(256), 0, s, p); break;
-        case 64: hipLaunchKernelGGL((bwd_main_bf16_kernel<64>), grid, dim3(256), 0, s, p); break;
-        case 128: hipLaunchKernelGGL((bwd_main_bf16_kernel<128>), grid, dim3(256), 0, s, p); break;
+        case 32: hipLaunchKernelGGL((bwd_main_bf16_kernel<32>), grid, dim3(64 * bwd_bf16_waves(32)), 0, s, p); break;
+        case 64: hipLaunchKernelGGL((bwd_main_bf16_kernel<64>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p); break;
+        case 128: hipLaunchKernelGGL((bwd_main_bf16_kernel<128>), grid, dim3(64 * bwd_bf16_waves(128)), 0, s, p); break;
         default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();

@@ -36,7 +36,9 @@ struct BwdWork {
 // Heads per group in the launch grid of a split plan.
 __host__ __device__ inline int bwd_padded_heads(int BH) { return (BH + 7) / 8 * 8; }
 
-// Work of this workgroup; bh >= B*H marks a padding workgroup (none to do).
+// Work of this workgroup (BK keys per key block); bh >= B*H marks a padding
+// workgroup (none to do).
+template <int BK>
 __device__ __forceinline__ BwdWork bwd_work(const BwdParams& p) {
     const int BH = p.B * p.H;
     const int w = blockIdx.x;
@@ -55,7 +57,7 @@ __device__ __forceinline__ BwdWork bwd_work(const BwdParams& p) {
         r.slot0 = g.slot0;
     } else {
         r.kblk = w / BH;
-        int qb = p.causal ? max(0, r.kblk * kBwdBK - p.off) : 0;
+        int qb = p.causal ? max(0, r.kblk * BK - p.off) : 0;
         r.q_begin = (qb / kBwdBQ) * kBwdBQ;
         r.q_end = p.Tq;
         r.split = -1;
@@ -67,11 +69,11 @@ __device__ __forceinline__ BwdWork bwd_work(const BwdParams& p) {
 }
 
 // For a split key block: store this workgroup's dK^T and dV^T accumulators
-// (N f32x16 per lane each) as its partial, count the arrival, and, in the last
-// workgroup to arrive, replace the accumulators by the chunk-ordered sum of
-// all partials.  Returns whether this workgroup goes on to store dK and dV.
-// Must be reached by every thread of the workgroup.
-template <int N>
+// (N f32x16 per lane each, NT threads) as its partial, count the arrival, and,
+// in the last workgroup to arrive, replace the accumulators by the
+// chunk-ordered sum of all partials.  Returns whether this workgroup goes on
+// to store dK and dV.  Must be reached by every thread of the workgroup.
+template <int NT, int N>
 __device__ __forceinline__ bool bwd_fixup(const BwdParams& p, const BwdWork& wk, f32x16 (&dk)[N], f32x16 (&dv)[N]) {
     if (wk.split < 0) return true;
     constexpr int NACC = 2 * N;
@@ -79,15 +81,15 @@ __device__ __forceinline__ bool bwd_fixup(const BwdParams& p, const BwdWork& wk,
     __shared__ int s_last;
     const int tid = threadIdx.x;
     const int BH = p.B * p.H;
-    const size_t per_wg = (size_t)256 * NACC * 16;  // floats of one partial
+    const size_t per_wg = (size_t)NT * NACC * 16;  // floats of one partial
     auto slot_ptr = [&](int c) { return p.part + ((size_t)(wk.slot0 + c) * BH + wk.bh) * per_wg; };
-    // lane-major: f32x4 j of accumulator a of thread tid at index (4a + j) * 256 + tid
+    // lane-major: f32x4 j of accumulator a of thread tid at index (4a + j) * NT + tid
     float* mine = slot_ptr(wk.chunk);
 #pragma unroll
     for (int a = 0; a < NACC; ++a)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<f32x4*>(mine + ((size_t)(4 * a + j) * 256 + tid) * 4) =
+            *reinterpret_cast<f32x4*>(mine + ((size_t)(4 * a + j) * NT + tid) * 4) =
                 f32x4{acc(a)[4 * j], acc(a)[4 * j + 1], acc(a)[4 * j + 2], acc(a)[4 * j + 3]};
     __builtin_amdgcn_s_waitcnt(0);  // the partial's stores have reached the L2
     __syncthreads();
@@ -103,7 +105,7 @@ __device__ __forceinline__ bool bwd_fixup(const BwdParams& p, const BwdWork& wk,
         for (int a = 0; a < NACC; ++a)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(src + ((size_t)(4 * a + j) * 256 + tid) * 4);
+                const f32x4 v = *reinterpret_cast<const f32x4*>(src + ((size_t)(4 * a + j) * NT + tid) * 4);
                 acc(a)[4 * j] += v[0];
                 acc(a)[4 * j + 1] += v[1];
                 acc(a)[4 * j + 2] += v[2];

@@ -199,13 +199,14 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     p.off = Tk - Tq;
     p.scale = scale;
     p.c = scale * 1.4426950408889634f;
-    p.n_kblocks = (Tk + inf::kBwdBK - 1) / inf::kBwdBK;
+    const int bk = inf::bwd_keys_per_wg(dt == INF_BF16, D);
+    p.n_kblocks = (Tk + bk - 1) / bk;
     inf::BwdPlan plan;
     inf::bwd_plan(B, H, Tq, Tk, D, p.causal, dt == INF_BF16, &plan);
     if (plan.n_groups) {
         size_t offset = round_up(bh * Tq * sizeof(float));
         if (dt == INF_BF16) offset += round_up(bh * Tq * (size_t)D * sizeof(float));
-        const size_t part_bytes = (size_t)plan.n_slots * bh * 2 * (size_t)D * inf::kBwdBK * sizeof(float);
+        const size_t part_bytes = (size_t)plan.n_slots * bh * 2 * (size_t)D * plan.bk * sizeof(float);
         p.part = reinterpret_cast<float*>(ws + offset);
         p.counters = reinterpret_cast<unsigned*>(ws + offset + part_bytes);
         p.n_groups = plan.n_groups;

@@ -117,10 +117,17 @@ __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<
 
 // Raw buffer resource over `bytes` bytes from `base` (gfx9 dword 3: raw
 // addressing, no swizzle).  A load whose offset falls at or past `bytes`
-// returns zeros without a memory access.  The base and size are wave-uniform,
-// so the descriptor lives in SGPRs.
+// returns zeros without a memory access.  Callers pass wave-uniform values;
+// reading them through readfirstlane keeps the descriptor in SGPRs even where
+// the compiler cannot prove the uniformity itself (a descriptor in VGPRs
+// turns every use into a loop over lanes).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    const uint32_t n = __builtin_amdgcn_readfirstlane(bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, (int)n,
+                                             0x00020000);
 }
 // 16-byte load at byte offset voff (per lane) + soff (uniform).
 __device__ __forceinline__ f32x4 buffer_ld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {

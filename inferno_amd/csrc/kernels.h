@@ -69,6 +69,7 @@ struct BwdGroup {
 
 struct BwdPlan {
     int n_groups = 0, n_split = 0, n_slots = 0;
+    int bk = 0;  // keys per workgroup of the kernel the plan is for
     BwdGroup groups[kMaxBwdGroups];
 };
 void bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan* out);
@@ -95,7 +96,7 @@ struct BwdParams {
     int n_kblocks;
     // split plan (n_groups == 0: workgroup w takes key block w / (B*H), all its tiles)
     int n_groups, n_split;
-    float* part;            // n_slots * B*H * 2*D*kBwdBK floats (lane-major accumulators)
+    float* part;            // n_slots * B*H * 2*D*(keys per workgroup) floats (lane-major accumulators)
     unsigned* counters;     // n_split * B*H, zeroed by bwd_pre
     BwdGroup groups[kMaxBwdGroups];
 };
@@ -277,7 +278,12 @@ int launch_masked_fill(const void* in, const void* mask, void* out, const Masked
 
 // Tile shapes the host needs for grids and workspace sizing.
 constexpr int kFwdBM = 128;      // query rows per forward workgroup
-constexpr int kBwdBK = 128;      // keys per backward workgroup
+constexpr int kBwdBK = 128;      // keys per backward workgroup (fp32, and bf16 at D = 128: 4 waves x 32 keys)
+// bf16 at D = 64: 8 waves x 32 keys, half the dQ atomics per key.  D = 128
+// needs ~430 registers per wave (one wave per SIMD), and D = 32 keeps three
+// 4-wave workgroups per CU: both stay at 4 waves.
+constexpr int bwd_bf16_waves(int D) { return D == 64 ? 8 : 4; }
+inline int bwd_keys_per_wg(int bf16, int D) { return bf16 ? 32 * bwd_bf16_waves(D) : kBwdBK; }
 constexpr int kBwdBQ = 32;       // query rows per backward inner step
 
 }  // namespace inf
