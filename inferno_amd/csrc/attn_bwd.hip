@@ -71,24 +71,30 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdParams p) {
 
 template <int D>
 struct BwdTile {
+    static constexpr int NW = bwd_waves(0, D);  // waves per workgroup, 32 keys each
+    static constexpr int BK = 32 * NW;       // keys per workgroup
     static constexpr int QS = D + 4;         // Q / dO row stride in LDS (floats)
-    static constexpr int SS = kBwdBK + 4;    // dS row stride
-    static constexpr int KTS = kBwdBK + 4;   // K^T row stride
+    static constexpr int SS = BK + 4;        // dS row stride
+    static constexpr int KTS = BK + 4;       // K^T row stride
 };
 
 template <int D, typename E>
-__global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdParams p) {
+__global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >= 128) ? 1 : 2) void bwd_main_kernel(
+    BwdParams p) {
+    constexpr int NW = BwdTile<D>::NW;
+    constexpr int NT = 64 * NW;
     constexpr int BQ = kBwdBQ;
-    constexpr int BK = kBwdBK;
+    constexpr int BK = BwdTile<D>::BK;
     constexpr int HD = D / 2;
     constexpr int NDB = D / 32;
     constexpr int C4 = D / 4;
     constexpr int QS = BwdTile<D>::QS;
     constexpr int SS = BwdTile<D>::SS;
     constexpr int KTS = BwdTile<D>::KTS;
-    constexpr int QLPT = BQ * C4 / 256;   // 4-element loads per thread for a Q / dO tile
-    constexpr int KLPT = BK * C4 / 256;   // for the K^T staging
-    constexpr int DQB = D / 32;           // 16x16 dQ blocks per wave
+    constexpr int QLPT = BQ * C4 / NT;    // 4-element loads per thread for a Q / dO tile
+    constexpr int KLPT = BK * C4 / NT;    // for the K^T staging
+    constexpr int NDQ = 2 * (D / 16);     // 16x16 dQ blocks of a query tile, NDQ / NW per wave
+    static_assert(BQ * C4 % NT == 0 && BK * C4 % NT == 0 && NDQ % NW == 0, "whole passes");
 
     __shared__ __attribute__((aligned(16))) float Qs[BQ][QS];
     __shared__ __attribute__((aligned(16))) float dOs[BQ][QS];
@@ -105,7 +111,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
     const int l16 = lane & 15;
     const int g4 = lane >> 4;
 
-    const BwdWork wk = bwd_work<kBwdBK>(p);
+    const BwdWork wk = bwd_work<BK>(p);
     if (wk.bh >= p.B * p.H) return;  // padding workgroup of a split plan's grid
     const int kblk = wk.kblk;
     const int bh = wk.bh;
@@ -141,10 +147,10 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
         for (int i = 0; i < HD; ++i) kf[i] = vf[i] = 0.f;
     }
 
-    // K^T of the whole 128-key block in LDS, for the dQ product.
+    // K^T of the whole key block in LDS, for the dQ product.
 #pragma unroll
     for (int i = 0; i < KLPT; ++i) {
-        const int f = tid + 256 * i;
+        const int f = tid + NT * i;
         const int r = f / C4;
         const int c4 = f % C4;
         f32x4 val = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -173,10 +179,10 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
     // prefetch is straight-line (a row limit of 0 past the last tile) and keeps
     // raw values, so no wait for it lands inside the MFMA blocks.
     // The loads go through buffer resources over rows [q0, lim): chunk
-    // tid + 256 i sits 256 i / C4 rows below chunk tid, and rows past the
+    // tid + NT i sits NT i / C4 rows below chunk tid, and rows past the
     // resource read as zeros, so a load needs no address arithmetic or branch.
     constexpr bool PF = D <= 64;
-    static_assert(256 % C4 == 0, "chunk rows must split into thread + load parts");
+    static_assert(NT % C4 == 0, "chunk rows must split into thread + load parts");
     static_assert(sizeof(E) == 4, "fp32 storage (bf16 has its own kernel)");
     f32x4 ra[QLPT], rd[QLPT];
     float r_lse = 0.f, r_dl = 0.f;
@@ -188,8 +194,8 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
         const auto rdo = row_rsrc((const float*)dO, p.sdo.t, q0, rows, D);
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
-            ra[i] = buffer_ld4(rq, q_voff, (uint32_t)((int64_t)(256 * i / C4) * p.sq.t * 4));
-            rd[i] = buffer_ld4(rdo, do_voff, (uint32_t)((int64_t)(256 * i / C4) * p.sdo.t * 4));
+            ra[i] = buffer_ld4(rq, q_voff, (uint32_t)((int64_t)(NT * i / C4) * p.sq.t * 4));
+            rd[i] = buffer_ld4(rdo, do_voff, (uint32_t)((int64_t)(NT * i / C4) * p.sdo.t * 4));
         }
         // lanes past the tile's rows (all but the first BQ threads) read zeros
         r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
@@ -198,7 +204,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
     auto sstore_q = [&]() {
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
-            const int f = tid + 256 * i;
+            const int f = tid + NT * i;
             *reinterpret_cast<f32x4*>(&Qs[f / C4][4 * (f % C4)]) = ra[i];
             *reinterpret_cast<f32x4*>(&dOs[f / C4][4 * (f % C4)]) = rd[i];
         }
@@ -288,20 +294,22 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
         __syncthreads();
         if constexpr (PF) sstore_q();  // the next tile (zeros after the last one, never read)
 
-        // ---- dQ tile (32 x D) += dS (32 x 128) K (128 x D) ---------------------
-        // fp32 atomics through a buffer resource over the tile's rows: rows
-        // past Tq fall outside it and the hardware drops those adds.
+        // ---- dQ tile (32 x D) += dS (32 x BK) K (BK x D) ---------------------
+        // Each wave takes NDQ / NW adjacent 16x16 blocks; lane group g4
+        // reduces keys g4 * BK/4 .. + BK/4 - 1.  fp32 atomics through a buffer
+        // resource over the tile's rows: rows past Tq fall outside it and the
+        // hardware drops those adds.
         const auto rdq = row_rsrc(dQa, p.sacc.t, q0, min(p.Tq - q0, BQ), D);
 #pragma unroll
-        for (int bi = 0; bi < DQB; ++bi) {
-            const int blk = wave * DQB + bi;
+        for (int bi = 0; bi < NDQ / NW; ++bi) {
+            const int blk = wave * (NDQ / NW) + bi;  // adjacent blocks share K^T rows
             const int qh = blk & 1;
             const int dc = blk >> 1;
             f32x4 acc;
 #pragma unroll
-            for (int kk = 0; kk < 32; kk += 4) {
-                const f32x4 a = *reinterpret_cast<const f32x4*>(&dSs[16 * qh + l16][g4 * 32 + kk]);
-                const f32x4 bb = *reinterpret_cast<const f32x4*>(&Kts[16 * dc + l16][g4 * 32 + kk]);
+            for (int kk = 0; kk < BK / 4; kk += 4) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(&dSs[16 * qh + l16][g4 * (BK / 4) + kk]);
+                const f32x4 bb = *reinterpret_cast<const f32x4*>(&Kts[16 * dc + l16][g4 * (BK / 4) + kk]);
                 acc = mfma16x16x4(a[0], bb[0], kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc);
                 acc = mfma16x16x4(a[1], bb[1], acc);
                 acc = mfma16x16x4(a[2], bb[2], acc);
@@ -316,7 +324,7 @@ __global__ __launch_bounds__(256, (D >= 128 ? 1 : 2)) void bwd_main_kernel(BwdPa
     }
 
     // ---- dK = scale * dK^T^T, dV = dV^T^T ------------------------------------------
-    if (!bwd_fixup<256>(p, wk, dk_acc, dv_acc)) return;
+    if (!bwd_fixup<NT>(p, wk, dk_acc, dv_acc)) return;
     if (key < p.Tk) {
         E* dKp = (E*)p.dk + b * p.sdk.b + h * p.sdk.h + (int64_t)key * p.sdk.t;
         E* dVp = (E*)p.dv + b * p.sdv.b + h * p.sdv.h + (int64_t)key * p.sdv.t;
@@ -430,14 +438,17 @@ static void bwd_slots(int D, int bf16, int* per_cu, int* cus_per_xcd) {
     const std::array<int, 3> key{dev, D, bf16};
     auto it = cache.find(key);
     if (it == cache.end()) {
-        int cus = 256, occ = D >= 128 ? 1 : 2;  // MI355X defaults
+        int cus = 256, occ = (D >= 128 || bwd_waves(bf16, D) == 8) ? 1 : 2;  // MI355X defaults
         if (dev >= 0) {
             int n = 0, o = 0;
             if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
             hipError_t e = hipErrorInvalidValue;
-            if (!bf16 && D == 32) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<32, float>, 256, 0);
-            if (!bf16 && D == 64) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<64, float>, 256, 0);
-            if (!bf16 && D == 128) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<128, float>, 256, 0);
+            if (!bf16 && D == 32)
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<32, float>, 64 * bwd_waves(0, 32), 0);
+            if (!bf16 && D == 64)
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<64, float>, 64 * bwd_waves(0, 64), 0);
+            if (!bf16 && D == 128)
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<128, float>, 64 * bwd_waves(0, 128), 0);
             if (bf16) e = (hipError_t)bwd_main_bf16_occupancy(D, &o);
             if (e == hipSuccess && o > 0) occ = o;
             (void)hipGetLastError();
@@ -569,7 +580,7 @@ static int launch_bwd_t(const BwdParams& p, hipStream_t s) {
         hipLaunchKernelGGL((bwd_cvt_kernel<D>), pre_grid, dim3(256), 0, s, p);
     } else {
         const dim3 grid((unsigned)(p.n_groups ? p.n_groups * bwd_padded_heads(p.B * p.H) : p.n_kblocks * p.B * p.H));
-        hipLaunchKernelGGL((bwd_main_kernel<D, E>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((bwd_main_kernel<D, E>), grid, dim3(64 * bwd_waves(0, D)), 0, s, p);
     }
     return (int)hipGetLastError();
 }

@@ -59,7 +59,8 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     constexpr int QLPT = (2 * QTASK + NT - 1) / NT;      // Q and dO together, per thread
     constexpr int KTASK = (BK / 2) * C8;
     constexpr int KLPT = (KTASK + NT - 1) / NT;
-    constexpr int NDQ = 2 * (D / 16);    // 16x16 dQ blocks of a query tile, dealt to the waves
+    constexpr int NDQ = 2 * (D / 16);    // 16x16 dQ blocks of a query tile, NDQ / NW per wave
+    static_assert(NDQ % NW == 0, "whole dQ blocks per wave");
 
     __shared__ __attribute__((aligned(16))) __bf16 Qs[BQ][QS];
     __shared__ __attribute__((aligned(16))) __bf16 dOs[BQ][QS];
@@ -276,12 +277,13 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
         sstore_q();
 
         // ---- dQ tile (32 x D) += dS (32 x BK) K (BK x D), 16x16 blocks ---------
-        // The 2 * D/16 blocks are dealt to the waves (D = 32: waves 4-7 have
-        // none).  fp32 atomics through a buffer resource over the tile's rows:
-        // rows past Tq fall outside it and the hardware drops those adds.
+        // Each wave takes NDQ / NW adjacent blocks.  fp32 atomics through a
+        // buffer resource over the tile's rows: rows past Tq fall outside it
+        // and the hardware drops those adds.
         const auto rdq = row_rsrc(dQa, p.sacc.t, q0, min(p.Tq - q0, BQ), D);
 #pragma unroll
-        for (int blk = wave; blk < NDQ; blk += NW) {
+        for (int bi = 0; bi < NDQ / NW; ++bi) {
+            const int blk = wave * (NDQ / NW) + bi;  // adjacent blocks share K^T rows
             const int qh = blk & 1;
             const int dc = blk >> 1;
             f32x4 acc;

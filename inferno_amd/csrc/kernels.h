@@ -278,12 +278,16 @@ int launch_masked_fill(const void* in, const void* mask, void* out, const Masked
 
 // Tile shapes the host needs for grids and workspace sizing.
 constexpr int kFwdBM = 128;      // query rows per forward workgroup
-constexpr int kBwdBK = 128;      // keys per backward workgroup (fp32, and bf16 at D = 128: 4 waves x 32 keys)
-// bf16 at D = 64: 8 waves x 32 keys, half the dQ atomics per key.  D = 128
-// needs ~430 registers per wave (one wave per SIMD), and D = 32 keeps three
-// 4-wave workgroups per CU: both stay at 4 waves.
-constexpr int bwd_bf16_waves(int D) { return D == 64 ? 8 : 4; }
-inline int bwd_keys_per_wg(int bf16, int D) { return bf16 ? 32 * bwd_bf16_waves(D) : kBwdBK; }
+// Backward workgroups: one wave per 32 keys.  bf16 at D = 64: 8 waves = 256
+// keys, half the dQ atomics per key (two waves per SIMD, as with two 4-wave
+// workgroups); at bf16 speed the atomics are a device-wide limit.  fp32 keeps
+// 4 waves (its atomics cost ~2.5%, and 256-key blocks measured 5-10% slower
+// under a causal mask: fewer, heavier workgroups).  D = 128 needs ~430
+// registers per wave (one wave per SIMD) and D = 32 keeps three 4-wave
+// workgroups per CU: both use 4 waves.
+constexpr int bwd_waves(int bf16, int D) { return bf16 && D == 64 ? 8 : 4; }
+constexpr int bwd_bf16_waves(int D) { return bwd_waves(1, D); }
+inline int bwd_keys_per_wg(int bf16, int D) { return 32 * bwd_waves(bf16, D); }
 constexpr int kBwdBQ = 32;       // query rows per backward inner step
 
 }  // namespace inf
