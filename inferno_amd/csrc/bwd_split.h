@@ -11,15 +11,16 @@
 // chunk order and stores dK and dV.  No workgroup waits for another, so the
 // split cannot stall the grid.
 //
-// The hand-over stays inside one XCD's L2.  The dispatcher deals workgroups
-// to the 8 XCDs round-robin (w mod 8), and w mod 8 = head mod 8 for every
-// group, so all chunks of a (key block, head) run on one XCD and share its L2.
-// The writer waits for its partial stores to complete (they pass the
-// write-through L1 into the L2) before counting; the last arriver invalidates
-// its CU's L1 before reading the partials.  A device-scope fence would instead
+// The partials are handed over through device-coherent accesses: the writer
+// stores them with device-scope (sc1) buffer stores, which write through the
+// XCD's L2, and waits for their completion before counting; the last arriver
+// reads them with device-scope (sc1) loads, which bypass both cache levels.
+// This holds wherever the chunks run.  (A device-scope fence would instead
 // write back and invalidate the whole L2 of the XCD, evicting every other
-// resident workgroup's tiles (measured: backward 18% slower at config 2 fp32,
-// 2.1x at bf16).
+// resident workgroup's tiles: measured 18% slower at config 2 fp32, 2.1x at
+// bf16.)  The grid is still laid out group-major over B*H padded to a multiple
+// of 8, which keeps a head's chunks on one XCD under the round-robin dispatch
+// and so its K / V tiles in one L2.
 #pragma once
 
 #include "common.h"
@@ -77,35 +78,41 @@ template <int NT, int N>
 __device__ __forceinline__ bool bwd_fixup(const BwdParams& p, const BwdWork& wk, f32x16 (&dk)[N], f32x16 (&dv)[N]) {
     if (wk.split < 0) return true;
     constexpr int NACC = 2 * N;
+    constexpr int kDeviceScope = 0x10;  // buffer cache policy: sc1
     auto acc = [&](int a) -> f32x16& { return a < N ? dk[a] : dv[a - N]; };
     __shared__ int s_last;
     const int tid = threadIdx.x;
     const int BH = p.B * p.H;
     const size_t per_wg = (size_t)NT * NACC * 16;  // floats of one partial
-    auto slot_ptr = [&](int c) { return p.part + ((size_t)(wk.slot0 + c) * BH + wk.bh) * per_wg; };
-    // lane-major: f32x4 j of accumulator a of thread tid at index (4a + j) * NT + tid
-    float* mine = slot_ptr(wk.chunk);
+    auto slot_rsrc = [&](int c) {
+        return buffer_rsrc(p.part + ((size_t)(wk.slot0 + c) * BH + wk.bh) * per_wg, (uint32_t)(per_wg * 4));
+    };
+    // lane-major: f32x4 j of accumulator a of thread tid at byte (((4a + j) * NT + tid) * 16
+    const uint32_t voff = (uint32_t)tid * 16;
+    const auto mine = slot_rsrc(wk.chunk);
 #pragma unroll
     for (int a = 0; a < NACC; ++a)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<f32x4*>(mine + ((size_t)(4 * a + j) * NT + tid) * 4) =
-                f32x4{acc(a)[4 * j], acc(a)[4 * j + 1], acc(a)[4 * j + 2], acc(a)[4 * j + 3]};
-    __builtin_amdgcn_s_waitcnt(0);  // the partial's stores have reached the L2
+        for (int j = 0; j < 4; ++j) {
+            const f32x4 v = f32x4{acc(a)[4 * j], acc(a)[4 * j + 1], acc(a)[4 * j + 2], acc(a)[4 * j + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), mine, (int)voff,
+                                                   (4 * a + j) * NT * 16, kDeviceScope);
+        }
+    __builtin_amdgcn_s_waitcnt(0);  // the partial's stores are complete
     __syncthreads();
     if (tid == 0) s_last = atomicAdd(&p.counters[wk.split * BH + wk.bh], 1u) == (unsigned)(wk.n_chunks - 1);
     __syncthreads();
     if (!s_last) return false;
-    asm volatile("buffer_inv sc0" ::: "memory");  // drop this CU's L1 lines: read the partials from L2
 #pragma unroll
     for (int a = 0; a < NACC; ++a) acc(a) = f32x16{};
     for (int c = 0; c < wk.n_chunks; ++c) {
-        const float* src = slot_ptr(c);
+        const auto src = slot_rsrc(c);
 #pragma unroll
         for (int a = 0; a < NACC; ++a)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(src + ((size_t)(4 * a + j) * NT + tid) * 4);
+                const f32x4 v = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(src, (int)voff, (4 * a + j) * NT * 16, kDeviceScope));
                 acc(a)[4 * j] += v[0];
                 acc(a)[4 * j + 1] += v[1];
                 acc(a)[4 * j + 2] += v[2];
