@@ -75,6 +75,9 @@ struct FwdTile {
     }
 };
 
+// Headroom of the forward's lazy rescaling, in exp2 units: P <= 2^8.
+constexpr float kLazyLog2 = 8.f;
+
 template <int D, typename E>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
     constexpr int BM = kFwdBM;
@@ -239,12 +242,24 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kb][r]);
         mloc = fmaxf(mloc, shfl_xor(mloc, 32));
-        const float m_new = fmaxf(m_run, mloc);
-        // A row can see no key of a chunk that does not start at key 0:
-        // keep m = -inf, l = 0, O = 0 for it instead of exp2(NaN).
-        const bool row_dead = m_new == -INFINITY;
-        const float alpha = row_dead ? 1.f : fast_exp2((m_run - m_new) * c);  // m_run = -inf -> 0
-        const float mc = row_dead ? 0.f : m_new * c;
+        // Lazy rescaling: a row's reference max m_run moves only when the row
+        // sees a score more than kLazyLog2 / c above it, so P stays
+        // <= 2^kLazyLog2; the O / l rescale and its exp2 run only on tiles where
+        // some row of the wave moved (VALU issue adds to fp32 MFMA time one for
+        // one), and for the other rows it multiplies by exactly 1, so every row
+        // depends on its own scores only.  O / l and the LSE do not depend on
+        // the reference.  m_run = -inf with a visible key always moves it.
+        const bool grow = mloc > m_run + kLazyLog2 / c;
+        if (__any(grow)) {
+            // A row can see no key of a chunk that does not start at key 0:
+            // keep m = -inf, l = 0, O = 0 for it instead of exp2(NaN).
+            const float alpha = grow ? fast_exp2((m_run - mloc) * c) : 1.f;  // m_run = -inf -> 0
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+            m_run = grow ? mloc : m_run;
+        }
+        const float mc = m_run == -INFINITY ? 0.f : m_run * c;
         // row sum as four independent partial chains
         float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -255,10 +270,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdParams p) {
                 s[kb][r] = e;
                 ls[r & 3] += e;
             }
-        l_run = fmaf(l_run, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
-        m_run = m_new;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 
         // reg 4j+cc of s[kb] holds key kb*32 + 8j + 4g + cc
 #pragma unroll
