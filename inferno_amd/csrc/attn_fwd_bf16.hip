@@ -175,9 +175,19 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kb][r]);
             mloc = max_xor32(mloc);
-            const float m_new = fmaxf(m_run, mloc);
-            const float alpha = fast_exp2((m_run - m_new) * c);
-            const float mc = m_new * c;
+            // Lazy rescaling, per row: the reference max moves only when the
+            // row sees a score 2^8 (in exp2 units) above it; the wave skips the
+            // O / l rescale when no row moved (a row that did not move would
+            // multiply by exactly 1).  P <= 2^8 enters the MFMA as bf16.
+            const bool grow = mloc > m_run + 8.f / c;
+            if (__any(grow)) {
+                const float alpha = grow ? fast_exp2((m_run - mloc) * c) : 1.f;  // m_run = -inf -> 0
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+                m_run = grow ? mloc : m_run;
+            }
+            const float mc = m_run * c;
             float lsum = 0.f;
             bf16x8 pb[NKB][2];
 #pragma unroll
@@ -188,10 +198,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
                     lsum += e;
                     pb[kb][r >> 3][r & 7] = (__bf16)e;
                 }
-            l_run = fmaf(l_run, alpha, lsum);
-            m_run = m_new;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+            l_run += lsum;
 
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
