@@ -188,17 +188,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
                 m_run = grow ? mloc : m_run;
             }
             const float mc = m_run * c;
-            float lsum = 0.f;
+            float ls[4] = {0.f, 0.f, 0.f, 0.f};  // row sum as four independent chains
             bf16x8 pb[NKB][2];
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const float e = fast_exp2(fmaf(s[kb][r], c, -mc));
-                    lsum += e;
+                    ls[r & 3] += e;
                     pb[kb][r >> 3][r & 7] = (__bf16)e;
                 }
-            l_run += lsum;
+            l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
 
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
