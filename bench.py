@@ -233,9 +233,9 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(bwd_tf / peak, 4),
             # HBM bytes per bwd_main launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-            # (x2.00 / x1.00 copy-kernel calibration): 200.0 MB read + 201.3 MB written
+            # (x2.00 / x1.00 copy-kernel calibration): 202.2 MB read + 201.3 MB written
             # (with the split plan's partial dK / dV stores and reads).
-            "traffic": 401.3e6,
+            "traffic": 403.5e6,
             "algorithmic_flop_per_launch": F_bwd,
             "avg_launch_ms": round(bwd_ms, 4),
         },
