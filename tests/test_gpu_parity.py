@@ -281,6 +281,37 @@ def test_decode_f32(ia, B, H, Tk, D):
     assert oracle.rel_err(o, o_r) <= TOL_F32
 
 
+@pytest.mark.parametrize("B,H,Tk,D", [(2, 3, 1, 64), (2, 3, 100, 32), (2, 2, 513, 128), (4, 12, 2048, 64)])
+def test_decode_bf16(ia, B, H, Tk, D):
+    """bf16 q and caches (fp32 arithmetic, bf16 output) against the oracle on the rounded values."""
+    print(f"[case] decode bf16 B{B} H{H} Tk{Tk} D{D}", flush=True)
+    q = bf16_round(oracle.randn(110, (B, H, 1, D)))
+    kc = bf16_round(oracle.randn(111, (B, H, Tk, D)))
+    vc = bf16_round(oracle.randn(112, (B, H, Tk, D)))
+    o = ia.attn_decode(dev(q, torch.bfloat16), dev(kc, torch.bfloat16), dev(vc, torch.bfloat16))
+    assert o.dtype == torch.bfloat16
+    assert oracle.rel_err(host(o), oracle.attn_decode(q, kc, vc)) <= TOL_BF16
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_cache_view(ia, dtype):
+    """Decode over the filled prefix of a larger cache ([B, H, capacity, D], a strided view) and a
+    query taken out of a [B, 1, H, D] buffer: the same result as on dense copies."""
+    B, H, cap, Tk, D = 3, 5, 1024, 700, 64
+    print(f"[case] decode cache view {dtype}", flush=True)
+    kc_full = dev(oracle.randn(120, (B, H, cap, D)), dtype)
+    vc_full = dev(oracle.randn(121, (B, H, cap, D)), dtype)
+    qbuf = dev(oracle.randn(122, (B, 1, H, D)), dtype)
+    q = qbuf.transpose(1, 2)  # [B, H, 1, D] view, head stride D
+    kc, vc = kc_full[:, :, :Tk], vc_full[:, :, :Tk]
+    o_view = ia.attn_decode(q, kc, vc)
+    o_dense = ia.attn_decode(q.contiguous(), kc.contiguous(), vc.contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(o_view, o_dense)
+    o_r = oracle.attn_decode(host(q), host(kc), host(vc))
+    assert oracle.rel_err(host(o_view), o_r) <= (TOL_F32 if dtype == torch.float32 else TOL_BF16)
+
+
 def test_decode_workspace_reuse(ia):
     """One workspace serves consecutive calls of different shapes (contents on entry do not matter)."""
     print("[case] decode workspace reuse", flush=True)
