@@ -138,6 +138,9 @@ __device__ __forceinline__ float buffer_ld1(__amdgpu_buffer_rsrc_t r, uint32_t v
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }
 // fp32 atomic add at byte offset voff + soff (dropped outside the resource).
+// Cache policy 0: on gfx950 an agent-scope atomicAdd compiles to the same
+// instruction without policy bits, so adds from workgroups on different XCDs
+// to one address are device-coherent, as HIP's atomicAdd is.
 __device__ __forceinline__ void buffer_atomic_add(__amdgpu_buffer_rsrc_t r, float v, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, (int)voff, (int)soff, 0);
 }
