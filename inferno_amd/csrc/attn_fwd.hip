@@ -425,15 +425,17 @@ __global__ __launch_bounds__(256) void attn_fwd_merge_kernel(FwdParams p) {
 }
 
 template <int D, typename E>
+static void launch_merge_t(const FwdParams& p, hipStream_t s) {
+    const int64_t threads = (int64_t)p.n_split * p.B * p.H * kFwdBM * (D / 4);
+    hipLaunchKernelGGL((attn_fwd_merge_kernel<D, E>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, p);
+}
+
+template <int D, typename E>
 static int launch_fwd_t(const FwdParams& p, hipStream_t s) {
     const int BH = p.B * p.H;
     const dim3 grid((unsigned)((p.n_groups ? p.n_groups : p.n_qtiles) * BH));
     hipLaunchKernelGGL((attn_fwd_kernel<D, E>), grid, dim3(256), 0, s, p);
-    if (p.n_split) {
-        const int64_t threads = (int64_t)p.n_split * BH * kFwdBM * (D / 4);
-        hipLaunchKernelGGL((attn_fwd_merge_kernel<D, E>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                           p);
-    }
+    if (p.n_split) launch_merge_t<D, E>(p, s);
     return (int)hipGetLastError();
 }
 
@@ -460,32 +462,38 @@ static double fwd_makespan(const int* cost, int n_groups, int BH, int slots_per_
     return worst;
 }
 
-// Resident forward workgroups per XCD on the current device (8 XCDs).
-static int fwd_slots_per_xcd(int D) {
+// Resident forward workgroups per XCD on the current device (8 XCDs), and
+// the device's CU count.
+struct FwdSlots {
+    int per_xcd, cus;
+};
+static FwdSlots fwd_slots(int D, int bf16) {
     static std::mutex mu;
-    static std::map<std::pair<int, int>, int> cache;
+    static std::map<std::array<int, 3>, FwdSlots> cache;
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess) {
         (void)hipGetLastError();
         dev = -1;
     }
     std::lock_guard<std::mutex> lk(mu);
-    auto it = cache.find({dev, D});
+    const std::array<int, 3> key{dev, D, bf16};
+    auto it = cache.find(key);
     if (it != cache.end()) return it->second;
-    // MI355X: 256 CUs; LDS holds two D<=64 workgroups per CU, one at D = 128.
-    int cus = 256, per_cu = D >= 128 ? 1 : 2;
+    // MI355X: 256 CUs; fp32: two D <= 64 workgroups per CU, one at D = 128.
+    int cus = 256, per_cu = bf16 ? (D >= 128 ? 2 : 4) : (D >= 128 ? 1 : 2);
     if (dev >= 0) {
         int n = 0, occ = 0;
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
         hipError_t e = hipErrorInvalidValue;
-        if (D == 32) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<32, float>, 256, 0);
-        if (D == 64) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<64, float>, 256, 0);
-        if (D == 128) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<128, float>, 256, 0);
+        if (bf16) e = (hipError_t)fwd_bf16_occupancy(D, &occ);
+        else if (D == 32) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<32, float>, 256, 0);
+        else if (D == 64) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<64, float>, 256, 0);
+        else if (D == 128) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<128, float>, 256, 0);
         if (e == hipSuccess && occ > 0) per_cu = occ;
         (void)hipGetLastError();
     }
-    const int slots = std::max(1, cus * per_cu / 8);
-    cache[{dev, D}] = slots;
+    const FwdSlots slots{std::max(1, cus * per_cu / 8), cus};
+    cache[key] = slots;
     return slots;
 }
 
@@ -500,11 +508,24 @@ static int fwd_slots_per_xcd(int D) {
 // into ceil(n / CH) near-equal chunks; the candidate with the smallest
 // simulated makespan (plus the merge pass) wins if it beats the unsplit order
 // by more than 2%.
-static constexpr double kFwdOverhead = 0.35;  // per-workgroup fixed cost, in key tiles
-static constexpr double kFwdMergeCost = 0.5;  // merge kernel, in key tiles
+//
+// bf16 (constants fitted to measurements at T = 1024..8192, D = 32..128): a
+// bf16 key tile costs about a fifth of an fp32 one, so the workgroup's fixed
+// cost and the merge weigh more in its units; up to four workgroups share a CU,
+// whose resident workgroups together run about 1.1 tiles in the time one runs
+// alone, so the makespan is also bounded below by the total work over the
+// CUs; and tiles under 32 key tiles (2048 keys) never split (B1 H12 T1024 D64
+// measured 19.9 us unsplit, 24.1 us split).
+static constexpr double kFwdOverhead[2] = {0.35, 2.0};   // per-workgroup fixed cost, in key tiles (fp32, bf16)
+static constexpr double kFwdMergeCost[2] = {0.5, 12.0};  // merge kernel, in key tiles
+static constexpr double kFwdCuRate[2] = {0.0, 1.1};      // tiles per CU per tile time (0: no bound)
+static constexpr int kFwdMinSplitTiles[2] = {0, 32};
 
-static void fwd_plan_compute(int B, int H, int Tq, int Tk, int D, int slots_per_xcd, FwdPlan* out) {
-    const int BM = kFwdBM, BN = D >= 128 ? FwdTile<128>::BN : FwdTile<64>::BN;
+static void fwd_plan_compute(int B, int H, int Tq, int Tk, int D, int bf16, FwdSlots slots, FwdPlan* out) {
+    const int BM = kFwdBM, BN = bf16 ? kFwdBf16BN : D >= 128 ? FwdTile<128>::BN : FwdTile<64>::BN;
+    const int ix = bf16 ? 1 : 0;
+    const double overhead = kFwdOverhead[ix], merge_cost = kFwdMergeCost[ix], cap = kFwdCuRate[ix] * slots.cus;
+    const int slots_per_xcd = slots.per_xcd;
     const int nq = (Tq + BM - 1) / BM;
     const int BH = B * H;
     const int off = Tk - Tq;
@@ -516,9 +537,19 @@ static void fwd_plan_compute(int B, int H, int Tq, int Tk, int D, int slots_per_
         nt[(size_t)q] = std::max(0, (kend + BN - 1) / BN);
         max_nt = std::max(max_nt, nt[(size_t)q]);
     }
+    if (max_nt < kFwdMinSplitTiles[ix]) return;
+    auto span = [&](const std::vector<int>& c) {
+        double m = fwd_makespan(c.data(), (int)c.size(), BH, slots_per_xcd, overhead);
+        if (cap > 0) {
+            double work = 0.0;
+            for (int x : c) work += x + overhead;
+            m = std::max(m, work * BH / cap);
+        }
+        return m;
+    };
     std::vector<int> cost;
     for (int q = nq - 1; q >= 0; --q) cost.push_back(nt[(size_t)q]);
-    const double base = fwd_makespan(cost.data(), nq, BH, slots_per_xcd, kFwdOverhead);
+    const double base = span(cost);
     double best = base * 0.98;
     int best_ch = 0;
     struct G { int n, qt, t0, t1; };
@@ -549,7 +580,7 @@ static void fwd_plan_compute(int B, int H, int Tq, int Tk, int D, int slots_per_
         if ((int)g.size() > kMaxFwdGroups || n_split > kMaxFwdGroups / 2) continue;
         cost.resize(g.size());
         for (size_t i = 0; i < g.size(); ++i) cost[i] = g[i].n;
-        const double ms = fwd_makespan(cost.data(), (int)g.size(), BH, slots_per_xcd, kFwdOverhead) + kFwdMergeCost;
+        const double ms = span(cost) + merge_cost;
         if (ms < best) {
             best = ms;
             best_ch = ch;
@@ -585,11 +616,12 @@ static void fwd_plan_compute(int B, int H, int Tq, int Tk, int D, int slots_per_
 
 void fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan* out) {
     *out = FwdPlan{};
-    if (bf16 || !causal || (D != 32 && D != 64 && D != 128)) return;
-    const int slots = fwd_slots_per_xcd(D);
+    bf16 = bf16 ? 1 : 0;
+    if (!causal || (D != 32 && D != 64 && D != 128)) return;
+    const FwdSlots slots = fwd_slots(D, bf16);
     static std::mutex mu;
-    static std::map<std::array<int, 5>, FwdPlan> cache;
-    const std::array<int, 5> key{B * H, Tq, Tk, D, slots};
+    static std::map<std::array<int, 7>, FwdPlan> cache;
+    const std::array<int, 7> key{B * H, Tq, Tk, D, bf16, slots.per_xcd, slots.cus};
     {
         std::lock_guard<std::mutex> lk(mu);
         auto it = cache.find(key);
@@ -598,7 +630,7 @@ void fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan
             return;
         }
     }
-    fwd_plan_compute(B, H, Tq, Tk, D, slots, out);
+    fwd_plan_compute(B, H, Tq, Tk, D, bf16, slots, out);
     std::lock_guard<std::mutex> lk(mu);
     if (cache.size() > 256) cache.clear();
     cache[key] = *out;
@@ -609,7 +641,17 @@ size_t fwd_workspace_bytes(const FwdPlan& plan, int B, int H, int D) {
 }
 
 int launch_attn_fwd(const FwdParams& p, int bf16, hipStream_t s) {
-    if (bf16) return launch_attn_fwd_bf16(p, s);
+    if (bf16) {
+        const int e = launch_attn_fwd_bf16(p, s);
+        if (e || !p.n_split) return e;
+        switch (p.D) {  // the merge reads fp32 partials and writes bf16 O
+            case 32: launch_merge_t<32, uint16_t>(p, s); break;
+            case 64: launch_merge_t<64, uint16_t>(p, s); break;
+            case 128: launch_merge_t<128, uint16_t>(p, s); break;
+            default: return (int)hipErrorInvalidValue;
+        }
+        return (int)hipGetLastError();
+    }
     switch (p.D) {
         case 32: return launch_fwd_t<32, float>(p, s);
         case 64: return launch_fwd_t<64, float>(p, s);

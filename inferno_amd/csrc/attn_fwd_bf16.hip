@@ -3,7 +3,9 @@
 //
 // Same structure as the fp32 kernel (attn_fwd.hip): 4 waves x 32 query rows,
 // K/V tiles of 64 keys double-buffered through LDS, S^T = K Q^T and
-// O^T += V^T P^T with queries on the lane axis, online softmax in fp32.
+// O^T += V^T P^T with queries on the lane axis, online softmax in fp32, and
+// the same split plan (fwd_plan: a chunk of a long query tile's key range
+// leaves fp32 partials that attn_fwd_merge_kernel combines into bf16 O).
 // What bf16 changes is the operand shape: one MFMA reduces 16 elements, each
 // lane supplying 8 consecutive ones.
 //   S^T:  A = K[key][8 d's]  -- a 16-byte row read from the row-major K tile
@@ -26,12 +28,14 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 template <int D>
 struct FwdBf16Tile {
-    static constexpr int BN = 64;       // keys per tile
+    static constexpr int BN = kFwdBf16BN;  // keys per tile
     static constexpr int KS = D + 8;    // K row stride in LDS (bf16 elements)
     static constexpr int VS = BN + 4;   // V^T row stride in LDS (bf16 elements)
 };
 
-template <int D>
+// SPLIT: the launch carries a split plan (groups, partial slots); the
+// instantiation without it keeps none of that code in its loop.
+template <int D, bool SPLIT>
 __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     constexpr int BM = kFwdBM;
     constexpr int BN = FwdBf16Tile<D>::BN;
@@ -55,9 +59,21 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     const int l32 = lane & 31;
     const int g = lane >> 5;
 
+    // Work: query tile and key-tile range [t_begin, t_end) of this workgroup
+    // (the whole visible range, heaviest tiles first, without a split plan; a
+    // group of the plan with one); a split chunk writes a partial to `slot`.
     const int BH = p.B * p.H;
     const int w = blockIdx.x;
-    const int qtile = p.n_qtiles - 1 - w / BH;
+    int qtile, t_begin = 0, t_end = 0x7fffffff, slot = -1;
+    if constexpr (SPLIT) {
+        const FwdGroup grp = p.groups[w / BH];
+        qtile = grp.qt;
+        t_begin = grp.t0;
+        t_end = grp.t1;
+        slot = grp.slot;
+    } else {
+        qtile = p.n_qtiles - 1 - w / BH;
+    }
     const int bh = w % BH;
     const int b = bh / p.H;
     const int h = bh % p.H;
@@ -82,20 +98,27 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
 
     int kv_end = p.Tk;
     if (p.causal) kv_end = min(p.Tk, qtile * BM + BM + p.off);
-    const int n_tiles = (kv_end + BN - 1) / BN;
+    const int n_tiles = min((kv_end + BN - 1) / BN, t_end);
     const int wave_kend = p.causal ? min(kv_end, q0w + 32 + p.off) : kv_end;
 
-    // Tile loads through buffer resources over rows [t*BN, lim): chunk
-    // tid + 256 i is chunk tid moved by a uniform offset (256 i / C8 rows for
-    // K, 8 i column chunks for V), and rows at or past `lim` read as zeros.
+    // Tile u of the range (keys kb0 + u*BN ...) loads `rows` rows from the
+    // tile bases kt / vt through buffer resources: chunk tid + 256 i is chunk
+    // tid moved by a uniform offset (256 i / C8 rows for K, 8 i column chunks
+    // for V), and rows past `rows` read as zeros.  The bases advance by one
+    // tile per step (pointer increments, no per-step 64-bit products).
     static_assert(256 % C8 == 0 && 256 % (BN / 2) == 0, "chunks must split into thread + load parts");
+    const int kb0 = t_begin * BN;
+    const int nt = n_tiles - t_begin;  // tiles in this workgroup's range
+    const int klim = p.Tk - kb0;       // keys of the range that exist
+    const int64_t kstep = (int64_t)BN * p.sk.t, vstep = (int64_t)BN * p.sv.t;
+    const __bf16* kt = K + (int64_t)kb0 * p.sk.t;
+    const __bf16* vt = V + (int64_t)kb0 * p.sv.t;
     bf16x8 kr[KLPT], va[VLPT], vb[VLPT];
     const uint32_t k_voff = (uint32_t)(((int64_t)(tid / C8) * p.sk.t + 8 * (tid % C8)) * 2);
     const uint32_t v_voff = (uint32_t)(((int64_t)(2 * (tid % (BN / 2))) * p.sv.t + 8 * (tid / (BN / 2))) * 2);
-    auto gload = [&](int t, int lim) {
-        const int rows = min(lim - t * BN, BN);
-        const auto rk = row_rsrc(K, p.sk.t, t * BN, rows, D);
-        const auto rv = row_rsrc(V, p.sv.t, t * BN, rows, D);
+    auto gload = [&](int rows) {
+        const auto rk = row_rsrc(kt, p.sk.t, 0, rows, D);
+        const auto rv = row_rsrc(vt, p.sv.t, 0, rows, D);
 #pragma unroll
         for (int i = 0; i < KLPT; ++i)
             kr[i] = buffer_ld8bf(rk, k_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sk.t * 2));
@@ -137,16 +160,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     float l_run = 0.f;
     const float c = p.c;
 
-    gload(0, p.Tk);
+    gload(min(klim, BN));
     sstore(0);
     __syncthreads();
 
-    // The prefetch of tile t+1 and its store are straight-line (a row limit
+    // The prefetch of tile u+1 and its store are straight-line (a row limit
     // of 0 past the last tile: zeros into a buffer that is not read again).
-    for (int t = 0; t < n_tiles; ++t) {
-        const int buf = t & 1;
-        const int k0 = t * BN;
-        gload(t + 1, t + 1 < n_tiles ? p.Tk : 0);
+    for (int u = 0; u < nt; ++u) {
+        const int buf = u & 1;
+        const int k0 = kb0 + u * BN;
+        kt += kstep;
+        vt += vstep;
+        gload(u + 1 < nt ? min(klim - (u + 1) * BN, BN) : 0);
 
         if (k0 < wave_kend) {
             f32x16 s[NKB];
@@ -187,7 +212,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
                 for (int db = 0; db < NDB; ++db) o[db] *= alpha;
                 m_run = grow ? mloc : m_run;
             }
-            const float mc = m_run * c;
+            // A row of a split chunk may have no visible key in the chunk: it
+            // keeps m_run = -inf, p = 0, and the merge skips its partial.
+            const float mc = SPLIT && m_run == -INFINITY ? 0.f : m_run * c;
             float ls[4] = {0.f, 0.f, 0.f, 0.f};  // row sum as four independent chains
             bf16x8 pb[NKB][2];
 #pragma unroll
@@ -221,6 +248,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     }
 
     const float l_tot = l_run + shfl_xor(l_run, 32);
+    if (SPLIT && slot >= 0) {
+        // partial of a split query tile (fp32): unnormalised O, row max, row sum
+        if (qrow < p.Tq) {
+            const int r = wave * 32 + l32;
+            float* po = p.part + ((int64_t)slot * BH + bh) * (BM * D) + (int64_t)r * D;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    st4(po + db * 32 + 8 * j + 4 * g,
+                        f32x4{o[db][4 * j + 0], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]});
+            if (g == 0) {
+                float* pml = p.part + (int64_t)p.n_slots * BH * BM * D + (((int64_t)slot * BH + bh) * BM + r) * 2;
+                pml[0] = m_run;
+                pml[1] = l_tot;
+            }
+        }
+        return;
+    }
     const float inv = 1.f / l_tot;
     if (qrow < p.Tq) {
         uint16_t* dst = O + (int64_t)qrow * p.so.t;
@@ -239,15 +285,32 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     }
 }
 
+template <int D>
+static void launch_t(const FwdParams& p, dim3 grid, hipStream_t s) {
+    if (p.n_groups)
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, true>), grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, false>), grid, dim3(256), 0, s, p);
+}
+
 int launch_attn_fwd_bf16(const FwdParams& p, hipStream_t s) {
-    const dim3 grid((unsigned)(p.n_qtiles * p.B * p.H));
+    const dim3 grid((unsigned)((p.n_groups ? p.n_groups : p.n_qtiles) * p.B * p.H));
     switch (p.D) {
-        case 32: hipLaunchKernelGGL((attn_fwd_bf16_kernel<32>), grid, dim3(256), 0, s, p); break;
-        case 64: hipLaunchKernelGGL((attn_fwd_bf16_kernel<64>), grid, dim3(256), 0, s, p); break;
-        case 128: hipLaunchKernelGGL((attn_fwd_bf16_kernel<128>), grid, dim3(256), 0, s, p); break;
+        case 32: launch_t<32>(p, grid, s); break;
+        case 64: launch_t<64>(p, grid, s); break;
+        case 128: launch_t<128>(p, grid, s); break;
         default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();
+}
+
+int fwd_bf16_occupancy(int D, int* blocks_per_cu) {
+    switch (D) {
+        case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, attn_fwd_bf16_kernel<32, true>, 256, 0);
+        case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, attn_fwd_bf16_kernel<64, true>, 256, 0);
+        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, attn_fwd_bf16_kernel<128, true>, 256, 0);
+        default: return (int)hipErrorInvalidValue;
+    }
 }
 
 }  // namespace inf

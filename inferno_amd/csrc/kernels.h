@@ -44,7 +44,7 @@ struct FwdParams {
     int split_qt[kMaxFwdGroups / 2], split_slot0[kMaxFwdGroups / 2], split_count[kMaxFwdGroups / 2];
 };
 
-// Split plan of the forward for a shape (fp32 kernels; bf16 never splits).
+// Split plan of the forward for a shape (causal; fp32 and bf16 kernels).
 struct FwdPlan {
     int n_groups = 0, n_slots = 0;
     FwdGroup groups[kMaxFwdGroups];
@@ -248,7 +248,8 @@ int launch_bcast(int op, const void* a, const void* b, void* out, int64_t n, int
 
 // Launchers return a hipError_t value (0 = hipSuccess).
 int launch_attn_fwd(const FwdParams& p, int bf16, hipStream_t s);
-int launch_attn_fwd_bf16(const FwdParams& p, hipStream_t s);  // bf16-MFMA forward
+int launch_attn_fwd_bf16(const FwdParams& p, hipStream_t s);  // bf16-MFMA forward (no merge pass)
+int fwd_bf16_occupancy(int D, int* blocks_per_cu);  // hipError_t
 int launch_attn_bwd(const BwdParams& p, int bf16, hipStream_t s);
 int bwd_main_bf16_occupancy(int D, int* blocks_per_cu);  // hipError_t
 int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s);  // bf16-MFMA backward main kernel
@@ -278,6 +279,7 @@ int launch_masked_fill(const void* in, const void* mask, void* out, const Masked
 
 // Tile shapes the host needs for grids and workspace sizing.
 constexpr int kFwdBM = 128;      // query rows per forward workgroup
+constexpr int kFwdBf16BN = 64;   // keys per K/V tile of the bf16 forward (every D)
 // Backward workgroups: one wave per 32 keys.  bf16 at D = 64: 8 waves = 256
 // keys, half the dQ atomics per key (two waves per SIMD, as with two 4-wave
 // workgroups); at bf16 speed the atomics are a device-wide limit.  fp32 keeps

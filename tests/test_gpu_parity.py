@@ -91,28 +91,45 @@ def test_fwd_bwd_bf16(ia, B, H, T, D):
         assert e <= TOL_BF16, f"{name} rel err {e:.3e}"
 
 
-@pytest.mark.parametrize("B,H,Tq,Tk,D", [
-    (1, 1, 1000, 1000, 64),
-    (1, 3, 777, 777, 64),
-    (1, 2, 1000, 1000, 32),
-    (1, 2, 1500, 1500, 128),
-    (1, 4, 900, 1024, 64),     # end-aligned causal: key j visible to query i iff j <= i + 124
-    (1, 2, 130, 1100, 64),     # short query block against a long cache
+F32, BF16 = torch.float32, torch.bfloat16
+
+
+@pytest.mark.parametrize("dtype,B,H,Tq,Tk,D", [
+    (F32, 1, 1, 1000, 1000, 64),
+    (F32, 1, 3, 777, 777, 64),
+    (F32, 1, 2, 1000, 1000, 32),
+    (F32, 1, 2, 1500, 1500, 128),
+    (F32, 1, 4, 900, 1024, 64),     # end-aligned causal: key j visible to query i iff j <= i + 124
+    (F32, 1, 2, 130, 1100, 64),     # short query block against a long cache
+    # bf16 splits only query tiles of at least 2048 keys
+    (BF16, 1, 1, 2048, 2048, 64),
+    (BF16, 1, 3, 2500, 2500, 32),
+    (BF16, 1, 1, 2300, 2300, 128),
+    (BF16, 1, 4, 1900, 2100, 64),   # end-aligned causal
+    (BF16, 1, 2, 200, 2200, 64),    # short query block against a long cache
 ])
-def test_fwd_split_plan_f32(ia, B, H, Tq, Tk, D):
+def test_fwd_split_plan(ia, dtype, B, H, Tq, Tk, D):
     """Few (tile, head) workgroups per CU: the forward splits the key range of its heaviest
-    query tiles across workgroups and merges the partials (the workspace is what they need)."""
-    print(f"[case] fwd split B{B} H{H} Tq{Tq} Tk{Tk} D{D}", flush=True)
-    assert ia.workspace_bytes(ia.OP_ATTN_FWD, B, H, Tq, Tk, D) > 0
+    query tiles across workgroups and merges the partials (the workspace is what they need).
+    bf16: the chunks' partials stay fp32 and the merge writes bf16 O; LSE is fp32 either way."""
+    bf = dtype == torch.bfloat16
+    dt = ia.INF_BF16 if bf else ia.INF_F32
+    print(f"[case] fwd split {dtype} B{B} H{H} Tq{Tq} Tk{Tk} D{D}", flush=True)
+    nbytes = ia.workspace_bytes(ia.OP_ATTN_FWD, B, H, Tq, Tk, D, dt)
+    assert nbytes > 0
     q, k, v, _ = oracle.attn_inputs(B, H, Tq, D, seed=13, Tk=Tk)
+    if bf:
+        q, k, v = bf16_round(q), bf16_round(k), bf16_round(v)
     o_r, lse_r = oracle.attn_fwd(q, k, v)
-    Q, K, V = dev(q), dev(k), dev(v)
-    ws = torch.full((ia.workspace_bytes(ia.OP_ATTN_FWD, B, H, Tq, Tk, D),), 0xFF, dtype=torch.uint8, device="cuda")
+    Q, K, V = dev(q, dtype), dev(k, dtype), dev(v, dtype)
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")
     o, lse = ia.attn_fwd(Q, K, V, workspace=ws)  # NaN-filled workspace: contents on entry must not matter
+    o2, lse2 = ia.attn_fwd(Q, K, V)               # a fresh workspace: the same bits
     torch.cuda.synchronize()
-    for name, x, r in (("O", host(o), o_r), ("LSE", host(lse), lse_r)):
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    for name, x, r, tol in (("O", host(o), o_r, TOL_BF16 if bf else TOL_F32), ("LSE", host(lse), lse_r, TOL_F32)):
         e = oracle.rel_err(x, r)
-        assert e <= TOL_F32, f"{name} rel err {e:.3e}"
+        assert e <= tol, f"{name} rel err {e:.3e}"
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
