@@ -181,14 +181,22 @@ def test_noncausal_f32(ia):
         assert oracle.rel_err(x, r) <= TOL_F32
 
 
-def test_prefix_invariance_bitwise(ia):
-    """Changing K[j], V[j] for j >= t must leave O[:, :, :t] (and LSE) bit-identical."""
-    print("[case] prefix invariance", flush=True)
-    B, H, T, D = 1, 2, 300, 64
+@pytest.mark.parametrize("dtype,T,D,cuts", [
+    (torch.float32, 300, 64, (1, 64, 129, 200)),
+    (torch.bfloat16, 300, 64, (1, 64, 129, 200)),
+    (torch.float32, 1500, 128, (1, 700, 1100, 1499)),    # split plan (chunks of the long tiles)
+    (torch.bfloat16, 2300, 128, (1, 1000, 1800, 2299)),  # split plan
+])
+def test_prefix_invariance_bitwise(ia, dtype, T, D, cuts):
+    """Changing K[j], V[j] for j >= t must leave O[:, :, :t] (and LSE) bit-identical, also when
+    the forward splits long query tiles into chunks (keys past a row are exact zeros in its
+    chunk's partial, and a chunk with no visible key for a row is skipped by the merge)."""
+    print(f"[case] prefix invariance {dtype} T{T} D{D}", flush=True)
+    B, H = 1, 2
     q, k, v, _ = oracle.attn_inputs(B, H, T, D, seed=11)
-    Q, K, V = dev(q), dev(k), dev(v)
+    Q, K, V = dev(q, dtype), dev(k, dtype), dev(v, dtype)
     o1, l1 = ia.attn_fwd(Q, K, V)
-    for t in (1, 64, 129, 200):
+    for t in cuts:
         K2, V2 = K.clone(), V.clone()
         K2[:, :, t:] = torch.randn_like(K2[:, :, t:]) * 5
         V2[:, :, t:] = torch.randn_like(V2[:, :, t:]) * 5
