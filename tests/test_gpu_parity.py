@@ -171,6 +171,44 @@ def test_bwd_split_plan(ia, dtype, B, H, Tq, Tk, D):
     assert torch.equal(first[1], second[1]) and torch.equal(first[2], second[2])
 
 
+def _random_cases(n=24, seed=2024):
+    """Seeded draws over the shape space: B, H, ragged Tq <= Tk (causal, end-aligned) or any
+    Tq, Tk (non-causal), D in {32, 64, 128}; fp32 and bf16 alternate."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        causal = bool(rng.integers(0, 4))  # three in four causal
+        D = int(rng.choice([32, 64, 128]))
+        B, H = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+        Tq = int(rng.integers(1, 500))
+        Tk = Tq + int(rng.integers(0, 300)) if causal else int(rng.integers(1, 600))
+        cases.append(("bf16" if i % 2 else "f32", causal, B, H, Tq, Tk, D))
+    return cases
+
+
+@pytest.mark.parametrize("dt,causal,B,H,Tq,Tk,D", _random_cases())
+def test_random_shapes(ia, dt, causal, B, H, Tq, Tk, D):
+    """Forward and backward at seeded random shapes against the oracle (O, dQ, dK, dV within
+    the dtype's bar of max|ref|, floored at 1e-2; LSE within 1e-4 / 1e-3)."""
+    print(f"[case] random {dt} causal={causal} B{B} H{H} Tq{Tq} Tk{Tk} D{D}", flush=True)
+    bf = dt == "bf16"
+    dtype = torch.bfloat16 if bf else torch.float32
+    q, k, v, do = oracle.attn_inputs(B, H, Tq, D, seed=500 + Tq + 7 * Tk + D, Tk=Tk)
+    if bf:
+        q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
+    o_r, lse_r = oracle.attn_fwd(q, k, v, causal=causal)
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do, causal=causal)
+    Q, K, V, dO = (dev(x, dtype) for x in (q, k, v, do))
+    o, lse = ia.attn_fwd(Q, K, V, causal=causal)
+    dq, dk, dv = ia.attn_bwd(Q, K, V, o, dO, lse, causal=causal)
+    torch.cuda.synchronize()
+    tol = TOL_BF16 if bf else TOL_F32
+    assert oracle.rel_err(host(lse), lse_r) <= (1e-3 if bf else TOL_F32), "LSE"
+    for name, x, r in (("O", o, o_r), ("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
+        e = oracle.rel_err(host(x), r, floor=1e-2)
+        assert e <= tol, f"{name} rel err {e:.3e}"
+
+
 def test_noncausal_f32(ia):
     print("[case] noncausal", flush=True)
     q, k, v, do = oracle.attn_inputs(1, 2, 96, 64, seed=7)
