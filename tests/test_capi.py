@@ -115,6 +115,23 @@ def test_workspace_sizes():
         ia.workspace_bytes(9, 1, 1, 8, 8, 64)
 
 
+@pytest.mark.parametrize("dt,B,H,T,D,splits", [
+    (ia.INF_F32, 8, 12, 1024, 64, False),    # config 2: more workgroups than resident slots
+    (ia.INF_F32, 4, 12, 1024, 64, True),
+    (ia.INF_F32, 1, 2, 8192, 128, True),
+    (ia.INF_F32, 1, 16, 8192, 128, False),   # config 4
+    (ia.INF_BF16, 8, 12, 1024, 64, False),   # config 2 bf16: measured 48% slower split
+    (ia.INF_BF16, 4, 12, 1024, 64, False),   # bf16 query tiles under 2048 keys never split
+    (ia.INF_BF16, 1, 12, 2048, 64, True),
+    (ia.INF_BF16, 1, 2, 8192, 128, True),
+    (ia.INF_BF16, 1, 16, 8192, 128, False),  # config 4 bf16
+])
+def test_forward_split_decisions(dt, B, H, T, D, splits):
+    """The forward split plan (a non-zero forward workspace) where it was measured to pay, and
+    none where it was measured to lose, on an MI355X's occupancy (the CPU build assumes it)."""
+    assert (ia.workspace_bytes(ia.OP_ATTN_FWD, B, H, T, T, D, dt) > 0) == splits
+
+
 def test_adamw_multi_validation():
     L = ia.lib()
     T = ia.AdamWTensor
