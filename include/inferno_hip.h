@@ -35,11 +35,17 @@
 extern "C" {
 #endif
 
-typedef enum { INF_F32 = 0, INF_BF16 = 1 } inf_dtype;
+/* INF_F64 and INF_I32 are accepted by the softmax entry points only (the
+ * other element types of the reference's Softmax dispatch); the attention,
+ * decode and nn entry points return INF_ERR_BAD_DTYPE for them. */
+typedef enum { INF_F32 = 0, INF_BF16 = 1, INF_F64 = 2, INF_I32 = 3 } inf_dtype;
 
 /* Element strides of a [B, H, T, D] view: d must be 1, all >= 0, and
  * t <= 2^22 (tiles are addressed with 32-bit byte offsets); otherwise the
- * attention entry points return INF_ERR_BAD_STRIDE. */
+ * attention entry points return INF_ERR_BAD_STRIDE.  Output views (o, dq,
+ * dk, dv) must not overlap themselves: ordering the dims of extent > 1 by
+ * stride, each stride must be at least the span of the dims inside it (D for
+ * the head dim), else INF_ERR_BAD_STRIDE. */
 typedef struct {
     int64_t b, h, t, d;
 } inf_strides;
@@ -119,7 +125,10 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
  * Row softmax over the last axis: y = softmax(x) per row of `cols` elements
  * (unit stride within a row, row strides in elements).  Replaces cpu_softmax /
  * cuda_softmax behind Softmax(Tensor&, int) (softmax.cpp:22-79,
- * cudasoftmax.cu:110-172) for a contiguous last axis.
+ * cudasoftmax.cu:110-172) for a contiguous last axis.  dt follows the
+ * reference's dispatch (RT = promote_t<AT, float>): INF_F32 and INF_BF16
+ * (fp32 arithmetic), INF_F64 (double arithmetic, exp included) and INF_I32
+ * (x holds int32, y fp32: the ints enter the fp32 arithmetic converted).
  */
 int inf_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int64_t x_row_stride,
                     int64_t y_row_stride, inf_dtype dt, void* stream);
@@ -128,7 +137,8 @@ int inf_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int64_t 
  * Softmax backward: dx = y * (dy - sum(dy * y)) per row.  Replaces
  * cpu_softmax_backward / cuda_softmax_backward behind SoftmaxBackward
  * (softmaxbackward.h:64-131, softmaxbackward.cpp:36-128,
- * cudasoftmax.cu:222-373).
+ * cudasoftmax.cu:222-373).  y, dy and dx share dt: INF_F32, INF_BF16 or
+ * INF_F64 (INF_I32 returns INF_ERR_BAD_DTYPE: dispatchFloatTwo takes floats).
  */
 int inf_softmax_bwd(const void* y, const void* dy, void* dx, int64_t rows, int64_t cols,
                     int64_t y_row_stride, int64_t dy_row_stride, int64_t dx_row_stride,

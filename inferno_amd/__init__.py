@@ -17,6 +17,8 @@ LIB_PATH = PKG / "libinferno_hip.so"
 
 INF_F32 = 0
 INF_BF16 = 1
+INF_F64 = 2  # softmax entry points only
+INF_I32 = 3  # softmax forward input only (fp32 output)
 OP_ATTN_FWD, OP_ATTN_BWD, OP_ATTN_DECODE = 0, 1, 2
 
 STATUS = {

@@ -250,14 +250,24 @@ Tensor MultiHeadAttention::forward_cached(const Tensor& x, KVCache& cache) {
         copy_view(knew, kdst);
         copy_view(vnew, vdst);
     }
-    cache.length += t;
-    const std::vector<size_t> all{B, H, cache.length, D};
-    Tensor kall = make_view(cache.k, all, cache.k.strides(), cache.k.offset(), "k_cache");
-    Tensor vall = make_view(cache.v, all, cache.v.strides(), cache.v.offset(), "v_cache");
-    Tensor y4 = t == 1 ? attention_decode(q, kall, vall) : scaled_dot_product_attention(q, kall, vall, true);
-    // [B, H, t, D] -> [B, t, C]; at t = 1 the dense [B, H, 1, D] already has that layout
-    Tensor y = t == 1 ? y4.reshape({B, 1, C}) : y4.transpose(1, 2).contiguous().reshape({B, t, C});
-    return W_out.forward(static_cast<const Tensor&>(y));
+    // The cache advances only when the whole step succeeds: a throw below
+    // leaves its length as it was (the slots just written lie past it).
+    const size_t len0 = cache.length;
+    try {
+        const size_t len = len0 + t;
+        const std::vector<size_t> all{B, H, len, D};
+        Tensor kall = make_view(cache.k, all, cache.k.strides(), cache.k.offset(), "k_cache");
+        Tensor vall = make_view(cache.v, all, cache.v.strides(), cache.v.offset(), "v_cache");
+        Tensor y4 = t == 1 ? attention_decode(q, kall, vall) : scaled_dot_product_attention(q, kall, vall, true);
+        // [B, H, t, D] -> [B, t, C]; at t = 1 the dense [B, H, 1, D] already has that layout
+        Tensor y = t == 1 ? y4.reshape({B, 1, C}) : y4.transpose(1, 2).contiguous().reshape({B, t, C});
+        Tensor out = W_out.forward(static_cast<const Tensor&>(y));
+        cache.length = len;
+        return out;
+    } catch (...) {
+        cache.length = len0;
+        throw;
+    }
 }
 
 // ------------------------------------------------------------ CrossEntropyLoss

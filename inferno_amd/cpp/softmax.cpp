@@ -7,8 +7,13 @@
 //        divide; backward dot = sum g*y in axis order, dx = y*(g - dot)
 //        (softmaxbackward.h:111-128).
 //   HIP: inf_softmax_fwd / inf_softmax_bwd.
+// Dtypes follow the reference's dispatch (softmax.cpp:25, dtype_dispatch.h:8-52):
+// Float32 -> Float32, Int32 -> Float32, Float64 -> Float64 (double
+// arithmetic), plus BFloat16 (fp32 arithmetic); the backward works in
+// promote_t of its operands (Float64 if either is).
 #include <cfloat>
 #include <cmath>
+#include <limits>
 
 #include "detail.h"
 #include "inferno/functional/softmax.h"
@@ -37,64 +42,98 @@ Tensor restore_axis(const Tensor& rows, int axis, size_t nd) {
     return rows.transpose(axis, (int)nd - 1).contiguous();
 }
 
-template <typename Load, typename Store>
+// The reference's three passes in RT arithmetic (softmax_kernels.h:77-102):
+// max from lowest() with a strict >, e = (RT)exp((double)(x - max)), RT running
+// sum, divide.  Loads return the element converted to RT (an Int32 converts to
+// float, as cpu_softmax<int, float> does in every use).
+template <typename RT, typename Load, typename Store>
 void cpu_softmax_rows(size_t rows, size_t cols, Load ld, Store st) {
-    std::vector<float> e(cols);
+    std::vector<RT> e(cols);
     for (size_t r = 0; r < rows; ++r) {
-        float mx = -FLT_MAX;
+        RT mx = std::numeric_limits<RT>::lowest();
         for (size_t k = 0; k < cols; ++k) {
-            const float x = ld(r * cols + k);
+            const RT x = ld(r * cols + k);
             if (x > mx) mx = x;
         }
-        float sum = 0.f;
+        RT sum = RT(0);
         for (size_t k = 0; k < cols; ++k) {
-            e[k] = (float)std::exp((double)(ld(r * cols + k) - mx));
+            e[k] = (RT)std::exp((double)(ld(r * cols + k) - mx));
             sum += e[k];
         }
         for (size_t k = 0; k < cols; ++k) st(r * cols + k, e[k] / sum);
     }
 }
 
-template <typename LoadY, typename LoadG, typename Store>
+// dot = sum g*y in axis order, dx = y*(g - dot), in RT = promote_t<y, g>
+// (softmaxbackward.h:111-128).
+template <typename RT, typename LoadY, typename LoadG, typename Store>
 void cpu_softmax_bwd_rows(size_t rows, size_t cols, LoadY ly, LoadG lg, Store st) {
     for (size_t r = 0; r < rows; ++r) {
-        float dot = 0.f;
+        RT dot = RT(0);
         for (size_t k = 0; k < cols; ++k) dot += lg(r * cols + k) * ly(r * cols + k);
         for (size_t k = 0; k < cols; ++k) st(r * cols + k, ly(r * cols + k) * (lg(r * cols + k) - dot));
     }
 }
 
-void check_float(const Tensor& t) {
-    if (t.dtype() != DType::Float32 && t.dtype() != DType::BFloat16)
-        throw Error(std::string("Softmax: Float32 or BFloat16 expected, got ") + dtype_name(t.dtype()));
+// Output dtype of Softmax: promote_t<AT, float> over the dtypes dispatchAny
+// takes (softmax.cpp:25, dtype_dispatch.h:8-52), plus BFloat16 (fp32
+// arithmetic, bf16 storage).
+DType softmax_out_dtype(DType in) {
+    switch (in) {
+        case DType::Float32:
+        case DType::Int32: return DType::Float32;
+        case DType::Float64: return DType::Float64;
+        case DType::BFloat16: return DType::BFloat16;
+        default: throw Error(std::string("Softmax: unsupported dtype ") + dtype_name(in));
+    }
+}
+
+// promote_t of the backward's two operands (dispatchFloatTwo,
+// softmaxbackward.cpp:40-45): Float64 if either is, else the saved output's.
+DType softmax_grad_dtype(DType y, DType g) {
+    const auto floating = [](DType d) { return d == DType::Float32 || d == DType::Float64 || d == DType::BFloat16; };
+    if (!floating(y) || !floating(g))
+        throw Error(std::string("SoftmaxBackward: floating operands expected, got ") + dtype_name(y) + " and " +
+                    dtype_name(g));
+    if (y == DType::Float64 || g == DType::Float64) return DType::Float64;
+    return y;
+}
+
+inf_dtype sm_dt(DType dt) {
+    switch (dt) {
+        case DType::Float32: return INF_F32;
+        case DType::BFloat16: return INF_BF16;
+        case DType::Float64: return INF_F64;
+        case DType::Int32: return INF_I32;
+        default: throw Error(std::string("Softmax: unsupported dtype ") + dtype_name(dt));
+    }
 }
 
 }  // namespace
 
 Tensor Softmax(Tensor& A, int axis) {
-    check_float(A);
+    const DType odt = softmax_out_dtype(A.dtype());
     const int ax = norm_axis(axis, A.ndim());
     Tensor x = rows_of(A, ax);
     const size_t cols = x.shape().back();
     const size_t rows = cols ? x.numel() / cols : 0;
-    Tensor y(A.dtype(), x.shape(), "softmax", A.device(), false);
+    Tensor y(odt, x.shape(), "softmax", A.device(), false);
     if (rows && cols) {
         if (A.device().is_cpu()) {
-            if (A.dtype() == DType::Float32) {
-                const float* px = static_cast<const float*>(x.data_ptr());
-                float* py = static_cast<float*>(y.data_ptr());
-                cpu_softmax_rows(rows, cols, [&](size_t i) { return px[i]; }, [&](size_t i, float v) { py[i] = v; });
-            } else {
-                const bfloat16* px = static_cast<const bfloat16*>(x.data_ptr());
-                bfloat16* py = static_cast<bfloat16*>(y.data_ptr());
-                cpu_softmax_rows(rows, cols, [&](size_t i) { return (float)px[i]; },
-                                 [&](size_t i, float v) { py[i] = bfloat16(v); });
-            }
+            const char* px = static_cast<const char*>(x.data_ptr());
+            char* py = static_cast<char*>(y.data_ptr());
+            const size_t ei = dtype_size(x.dtype()), eo = dtype_size(odt);
+            const DType idt = x.dtype();
+            auto st = [&](size_t i, double v) { detail::store_elem(py + i * eo, odt, v); };
+            if (odt == DType::Float64)
+                cpu_softmax_rows<double>(rows, cols, [&](size_t i) { return detail::load_elem(px + i * ei, idt); }, st);
+            else
+                cpu_softmax_rows<float>(rows, cols, [&](size_t i) { return (float)detail::load_elem(px + i * ei, idt); },
+                                        st);
         } else {
             detail::DeviceGuard g(A.device().index);
             detail::status_check(inf_softmax_fwd(x.data_ptr(), y.data_ptr(), (int64_t)rows, (int64_t)cols,
-                                                 (int64_t)cols, (int64_t)cols, detail::inf_dt(A.dtype(), "Softmax"),
-                                                 detail::stream_of(A)),
+                                                 (int64_t)cols, (int64_t)cols, sm_dt(x.dtype()), detail::stream_of(A)),
                                  "inf_softmax_fwd");
         }
     }
@@ -114,32 +153,34 @@ void SoftmaxBackward::backward() {
     Tensor g = Engine::grad_in(this, 0);
     Tensor y = rows_of(m_out, m_axis);
     Tensor gr = rows_of(g, m_axis);
+    const DType rdt = softmax_grad_dtype(y.dtype(), gr.dtype());
     const size_t cols = y.shape().back();
     const size_t rows = cols ? y.numel() / cols : 0;
-    Tensor dx(y.dtype(), y.shape(), "softmax_grad", y.device(), false);
+    Tensor dx(rdt, y.shape(), "softmax_grad", y.device(), false);
     if (rows && cols) {
         if (y.device().is_cpu()) {
-            if (y.dtype() == DType::Float32) {
-                const float* py = static_cast<const float*>(y.data_ptr());
-                const float* pg = static_cast<const float*>(gr.data_ptr());
-                float* pd = static_cast<float*>(dx.data_ptr());
-                cpu_softmax_bwd_rows(rows, cols, [&](size_t i) { return py[i]; }, [&](size_t i) { return pg[i]; },
-                                     [&](size_t i, float v) { pd[i] = v; });
-            } else {
-                const bfloat16* py = static_cast<const bfloat16*>(y.data_ptr());
-                const bfloat16* pg = static_cast<const bfloat16*>(gr.data_ptr());
-                bfloat16* pd = static_cast<bfloat16*>(dx.data_ptr());
-                cpu_softmax_bwd_rows(rows, cols, [&](size_t i) { return (float)py[i]; },
-                                     [&](size_t i) { return (float)pg[i]; },
-                                     [&](size_t i, float v) { pd[i] = bfloat16(v); });
-            }
+            const char* py = static_cast<const char*>(y.data_ptr());
+            const char* pg = static_cast<const char*>(gr.data_ptr());
+            char* pd = static_cast<char*>(dx.data_ptr());
+            const size_t ey = dtype_size(y.dtype()), eg = dtype_size(gr.dtype()), ed = dtype_size(rdt);
+            const DType ydt = y.dtype(), gdt = gr.dtype();
+            auto st = [&](size_t i, double v) { detail::store_elem(pd + i * ed, rdt, v); };
+            if (rdt == DType::Float64)
+                cpu_softmax_bwd_rows<double>(rows, cols, [&](size_t i) { return detail::load_elem(py + i * ey, ydt); },
+                                             [&](size_t i) { return detail::load_elem(pg + i * eg, gdt); }, st);
+            else
+                cpu_softmax_bwd_rows<float>(
+                    rows, cols, [&](size_t i) { return (float)detail::load_elem(py + i * ey, ydt); },
+                    [&](size_t i) { return (float)detail::load_elem(pg + i * eg, gdt); }, st);
         } else {
+            if (y.dtype() != gr.dtype())
+                throw Error(std::string("SoftmaxBackward: on HIP the output and its gradient must share a dtype, got ") +
+                            dtype_name(y.dtype()) + " and " + dtype_name(gr.dtype()));
             detail::DeviceGuard dg(y.device().index);
-            detail::status_check(
-                inf_softmax_bwd(y.data_ptr(), gr.data_ptr(), dx.data_ptr(), (int64_t)rows, (int64_t)cols, (int64_t)cols,
-                                (int64_t)cols, (int64_t)cols, detail::inf_dt(y.dtype(), "SoftmaxBackward"),
-                                detail::stream_of(y)),
-                "inf_softmax_bwd");
+            detail::status_check(inf_softmax_bwd(y.data_ptr(), gr.data_ptr(), dx.data_ptr(), (int64_t)rows,
+                                                 (int64_t)cols, (int64_t)cols, (int64_t)cols, (int64_t)cols,
+                                                 sm_dt(y.dtype()), detail::stream_of(y)),
+                                 "inf_softmax_bwd");
         }
     }
     auto e = GetImpl(m_A)->grad_edge();

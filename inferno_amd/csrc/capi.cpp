@@ -11,6 +11,7 @@
 #include <cstdint>
 #include <cstring>
 #include <string>
+#include <utility>
 
 #include "kernels.h"
 
@@ -20,7 +21,7 @@ constexpr size_t kAlign = 256;
 
 size_t round_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
-int elem_bytes(inf_dtype dt) { return dt == INF_F32 ? 4 : 2; }
+int elem_bytes(inf_dtype dt) { return dt == INF_BF16 ? 2 : (dt == INF_F64 ? 8 : 4); }
 
 bool dtype_ok(int dt) { return dt == INF_F32 || dt == INF_BF16; }
 
@@ -40,6 +41,26 @@ int check_view(const void* p, const inf_strides& s, inf_dtype dt) {
     const uintptr_t need = (uintptr_t)(4 * elem_bytes(dt));
     if (a % need) return INF_ERR_ALIGNMENT;
     if ((s.b % 4) || (s.h % 4) || (s.t % 4)) return INF_ERR_ALIGNMENT;
+    return INF_OK;
+}
+
+// An output [B,H,T,D] view must also give every element its own address:
+// workgroups of different heads or rows would otherwise store to (and, for the
+// fp32 dQ accumulation, add into) the same words.  Sufficient condition: with
+// the dims of extent > 1 in increasing stride order, each stride is at least
+// the span of the dims inside it (the head dim's span is D).
+int check_out_view(const void* p, const inf_strides& s, inf_dtype dt, int B, int H, int T, int D) {
+    const int st = check_view(p, s, dt);
+    if (st != INF_OK) return st;
+    struct Dim { int64_t n, stride; } d[3] = {{B, s.b}, {H, s.h}, {T, s.t}};
+    for (int i = 1; i < 3; ++i)  // insertion sort by stride
+        for (int j = i; j > 0 && d[j].stride < d[j - 1].stride; --j) std::swap(d[j], d[j - 1]);
+    int64_t span = D;
+    for (const Dim& x : d) {
+        if (x.n <= 1) continue;
+        if (x.stride < span) return INF_ERR_BAD_STRIDE;
+        span = x.stride * (x.n - 1) + span;
+    }
     return INF_OK;
 }
 
@@ -130,7 +151,7 @@ int inf_attn_fwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     if (st != INF_OK) return st;
     if (causal && Tq > Tk) return INF_ERR_BAD_SHAPE;
     if ((st = check_view(q, sq, dt)) || (st = check_view(k, sk, dt)) ||
-        (st = check_view(v, sv, dt)) || (st = check_view(o, so, dt)))
+        (st = check_view(v, sv, dt)) || (st = check_out_view(o, so, dt, B, H, Tq, D)))
         return st;
     inf::FwdParams p{};
     p.q = q; p.k = k; p.v = v; p.o = o; p.lse = lse;
@@ -171,8 +192,8 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     if (!lse) return INF_ERR_NULL_POINTER;
     if ((st = check_view(q, sq, dt)) || (st = check_view(k, sk, dt)) ||
         (st = check_view(v, sv, dt)) || (st = check_view(o, so, dt)) ||
-        (st = check_view(dout, sdo, dt)) || (st = check_view(dq, sdq, dt)) ||
-        (st = check_view(dk, sdk, dt)) || (st = check_view(dv, sdv, dt)))
+        (st = check_view(dout, sdo, dt)) || (st = check_out_view(dq, sdq, dt, B, H, Tq, D)) ||
+        (st = check_out_view(dk, sdk, dt, B, H, Tk, D)) || (st = check_out_view(dv, sdv, dt, B, H, Tk, D)))
         return st;
     size_t need = 0;
     inf_attn_workspace_bytes(INF_OP_ATTN_BWD, B, H, Tq, Tk, D, dt, &need);
@@ -216,9 +237,19 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     return hip_status(inf::launch_attn_bwd(p, dt == INF_BF16, (hipStream_t)stream));
 }
 
+// Element types of the softmax entry points: the attention dtypes, plus
+// INF_F64 (both directions) and INF_I32 input (forward only, fp32 output).
+static inf::SmType sm_type(inf_dtype dt) {
+    switch (dt) {
+        case INF_BF16: return inf::SmType::BF16;
+        case INF_F64: return inf::SmType::F64;
+        case INF_I32: return inf::SmType::I32;
+        default: return inf::SmType::F32;
+    }
+}
+
 static int softmax_common(const void* a, const void* b, void* c, int64_t rows, int64_t cols,
                           inf_dtype dt, int* vec_ok, int64_t s1, int64_t s2, int64_t s3) {
-    if (!dtype_ok(dt)) return INF_ERR_BAD_DTYPE;
     if (!a || !b || !c) return INF_ERR_NULL_POINTER;
     if (rows < 1 || cols < 1 || rows > (1LL << 31)) return INF_ERR_BAD_SHAPE;
     if (s1 < cols || s2 < cols || s3 < cols) return INF_ERR_BAD_STRIDE;
@@ -232,23 +263,25 @@ static int softmax_common(const void* a, const void* b, void* c, int64_t rows, i
 
 int inf_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int64_t x_row_stride,
                     int64_t y_row_stride, inf_dtype dt, void* stream) {
+    if (!dtype_ok(dt) && dt != INF_F64 && dt != INF_I32) return INF_ERR_BAD_DTYPE;
     int vec_ok = 0;
     const int st = softmax_common(x, x, y, rows, cols, dt, &vec_ok, x_row_stride, y_row_stride,
                                   y_row_stride);
     if (st != INF_OK) return st;
     inf::SoftmaxParams p{x, nullptr, y, rows, cols, x_row_stride, 0, y_row_stride};
-    return hip_status(inf::launch_softmax_fwd(p, dt == INF_BF16, vec_ok, (hipStream_t)stream));
+    return hip_status(inf::launch_softmax_fwd(p, sm_type(dt), vec_ok, (hipStream_t)stream));
 }
 
 int inf_softmax_bwd(const void* y, const void* dy, void* dx, int64_t rows, int64_t cols,
                     int64_t y_row_stride, int64_t dy_row_stride, int64_t dx_row_stride,
                     inf_dtype dt, void* stream) {
+    if (!dtype_ok(dt) && dt != INF_F64) return INF_ERR_BAD_DTYPE;
     int vec_ok = 0;
     const int st = softmax_common(y, dy, dx, rows, cols, dt, &vec_ok, y_row_stride, dy_row_stride,
                                   dx_row_stride);
     if (st != INF_OK) return st;
     inf::SoftmaxParams p{y, dy, dx, rows, cols, y_row_stride, dy_row_stride, dx_row_stride};
-    return hip_status(inf::launch_softmax_bwd(p, dt == INF_BF16, vec_ok, (hipStream_t)stream));
+    return hip_status(inf::launch_softmax_bwd(p, sm_type(dt), vec_ok, (hipStream_t)stream));
 }
 
 int inf_attn_decode(const void* q, inf_strides sq, const void* kcache, inf_strides sk,
@@ -258,7 +291,7 @@ int inf_attn_decode(const void* q, inf_strides sq, const void* kcache, inf_strid
     int st = common_shape(B, H, 1, Tk, D, scale, dt);
     if (st != INF_OK) return st;
     if ((st = check_view(q, sq, dt)) || (st = check_view(kcache, sk, dt)) ||
-        (st = check_view(vcache, sv, dt)) || (st = check_view(o, so, dt)))
+        (st = check_view(vcache, sv, dt)) || (st = check_out_view(o, so, dt, B, H, 1, D)))
         return st;
     size_t need = 0;
     inf_attn_workspace_bytes(INF_OP_ATTN_DECODE, B, H, 1, Tk, D, dt, &need);

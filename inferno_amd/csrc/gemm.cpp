@@ -52,6 +52,7 @@ struct Plan {
     hipblasLtMatmulAlgo_t algo[kMaxAlgos]{};
     int n_algo = 0;
     int cur = 0;  // the candidate in use: the first one that launched
+    uint32_t reported = 0;  // candidates whose skip has been reported (bit i: candidate i)
 };
 
 std::mutex g_mu;
@@ -134,6 +135,15 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
         set_error_detail("inf_gemm: hipGetDevice failed");
         return 1;
     }
+    // An error left pending by an earlier HIP call on this thread fails the
+    // call with that error named (nothing is launched): hipBLASLt would
+    // otherwise report it as its own failure, or the caller would never see it.
+    const hipError_t pending = hipGetLastError();
+    if (pending != hipSuccess) {
+        set_error_detail(std::string("inf_gemm: HIP error pending from an earlier call: ") + hipGetErrorName(pending) +
+                         " (" + hipGetErrorString(pending) + "); nothing launched");
+        return 1;
+    }
     Key k;
     std::memset(&k, 0, sizeof(k));  // padding bytes take part in hashing / comparison
     k.ta = g.ta;
@@ -182,30 +192,35 @@ int launch_gemm(const GemmArgs& g, hipStream_t s) {
             return 1;
         }
     }
-    // An error left pending by an earlier, unrelated HIP call would otherwise be
-    // reported by the library as its own failure.
-    const hipError_t pending = hipGetLastError();
     const float alpha = g.alpha, beta = g.beta;
     // The heuristic's candidates in order, starting from the one in use: a
     // candidate the installed library cannot launch (some builds return
-    // HIPBLAS_STATUS_INTERNAL_ERROR for a listed solution) is skipped for good.
+    // HIPBLAS_STATUS_INTERNAL_ERROR for a listed solution) is skipped for good,
+    // and each skip is reported once, on stderr and in the call's detail string.
     hipblasStatus_t st = HIPBLAS_STATUS_NOT_SUPPORTED;
+    std::string skipped;
     for (; p.cur < p.n_algo; ++p.cur) {
         st = hipblasLtMatmul(h, p.desc, &alpha, g.B, p.la, g.A, p.lb, &beta, g.C, p.lc, g.C, p.lc, &p.algo[p.cur],
                              g.ws, g.ws_bytes, s);
         if (st == HIPBLAS_STATUS_SUCCESS) break;
-        (void)hipGetLastError();
+        const hipError_t le = hipGetLastError();  // the failed launch's own error, if it left one
+        const uint32_t bit = 1u << p.cur;
+        if (!(p.reported & bit)) {
+            p.reported |= bit;
+            char line[160];
+            std::snprintf(line, sizeof(line), "candidate %d of %d skipped (hipblasLtMatmul status %d, HIP %s); ",
+                          p.cur + 1, p.n_algo, (int)st, hipGetErrorName(le));
+            skipped += line;
+            std::fprintf(stderr, "inferno_hip: inf_gemm: %sfor %s\n", line, shape);
+        }
     }
     if (st != HIPBLAS_STATUS_SUCCESS) {
         p.cur = 0;  // all failed: start over on the next call
         set_error_detail(std::string("inf_gemm: hipblasLtMatmul status ") + std::to_string((int)st) + " for " + shape +
-                         " with every one of " + std::to_string(p.n_algo) +
-                         " heuristic candidates; HIP error pending before the call: " + hipGetErrorString(pending));
+                         " with every one of " + std::to_string(p.n_algo) + " heuristic candidates; " + skipped);
         return 1;
     }
-    if (pending != hipSuccess)
-        set_error_detail(std::string("inf_gemm: cleared a pending HIP error before the call: ") +
-                         hipGetErrorString(pending));
+    if (!skipped.empty()) set_error_detail("inf_gemm: " + skipped + "for " + shape);
     return 0;
 }
 

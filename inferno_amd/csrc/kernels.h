@@ -256,8 +256,11 @@ int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s);  // bf16-MFMA backw
 int launch_attn_decode(const DecodeParams& p, int bf16, hipStream_t s);
 // Decode split plan (number of key splits per row, keys per split) for a shape.
 void decode_plan(int B, int H, int Tk, int D, int* nsplit, int* chunk);
-int launch_softmax_fwd(const SoftmaxParams& p, int bf16, int vec_ok, hipStream_t s);
-int launch_softmax_bwd(const SoftmaxParams& p, int bf16, int vec_ok, hipStream_t s);
+// Element types of the standalone softmax: fp32, bf16 storage (fp32
+// arithmetic), int32 input with fp32 output (forward only), fp64.
+enum class SmType { F32, BF16, I32, F64 };
+int launch_softmax_fwd(const SoftmaxParams& p, SmType t, int vec_ok, hipStream_t s);
+int launch_softmax_bwd(const SoftmaxParams& p, SmType t, int vec_ok, hipStream_t s);
 int launch_fill(void* dst, int64_t n, int elem_bytes, uint32_t bits, hipStream_t s);
 int launch_binary(int op, const void* a, const void* b, void* out, int64_t n, int a_scalar, int b_scalar,
                   int bf16, hipStream_t s);

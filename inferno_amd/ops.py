@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import torch
 
-from . import INF_BF16, INF_F32, OP_ATTN_BWD, OP_ATTN_DECODE, OP_ATTN_FWD, InfernoError, Strides, default_scale, lib, workspace_bytes
+from . import INF_BF16, INF_F32, INF_F64, INF_I32, OP_ATTN_BWD, OP_ATTN_DECODE, OP_ATTN_FWD, InfernoError, Strides, default_scale, lib, workspace_bytes
 
 
 def _dt(t: torch.Tensor) -> int:
@@ -16,6 +16,10 @@ def _dt(t: torch.Tensor) -> int:
         return INF_F32
     if t.dtype == torch.bfloat16:
         return INF_BF16
+    if t.dtype == torch.float64:
+        return INF_F64
+    if t.dtype == torch.int32:
+        return INF_I32
     raise TypeError(f"unsupported dtype {t.dtype}")
 
 
@@ -116,7 +120,8 @@ def _rows(t: torch.Tensor):
 def softmax_fwd(x, out=None, stream=None):
     """Row softmax over the last axis."""
     x2, rows, cols, sx = _rows(x)
-    out = torch.empty_like(x2) if out is None else out.reshape(rows, cols)
+    odt = torch.float32 if x.dtype == torch.int32 else x.dtype  # Int32 input -> Float32 output
+    out = torch.empty((rows, cols), dtype=odt, device=x.device) if out is None else out.reshape(rows, cols)
     st = lib().inf_softmax_fwd(x2.data_ptr(), out.data_ptr(), rows, cols, sx,
                                out.stride(0) if rows > 1 else cols, _dt(x), _stream(stream))
     _check(st, "inf_softmax_fwd")

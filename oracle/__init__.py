@@ -58,6 +58,10 @@ def lib():
         L.orc_masked_fill_f32.argtypes = [_f32p, _i32p, ctypes.c_float, _f32p, _i64, _i64]
         L.orc_softmax_f32.argtypes = [_f32p, _f32p, _i64, _i64]
         L.orc_softmax_bwd_f32.argtypes = [_f32p, _f32p, _f32p, _i64, _i64]
+        _f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+        L.orc_softmax_f64.argtypes = [_f64p, _f64p, _i64, _i64]
+        L.orc_softmax_i32.argtypes = [_i32p, _f32p, _i64, _i64]
+        L.orc_softmax_bwd_f64.argtypes = [_f64p, _f64p, _f64p, _i64, _i64]
         L.orc_attn_fwd_f32.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64,
                                        ctypes.c_float, ctypes.c_int, _f32p, _vp, _vp]
         L.orc_attn_bwd_f32.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64,
@@ -79,6 +83,9 @@ def ref_lib():
         R.ref_triu_ones_i32.argtypes = [_i64, _i64, ctypes.c_int, _i32p]
         R.ref_masked_fill_f32.argtypes = [_f32p, _i64, _i64, _i64, _i64, _i32p, ctypes.c_float, _f32p]
         R.ref_softmax_f32.argtypes = [_f32p, _i64, _i64, _f32p]
+        R.ref_softmax_f64.argtypes = [np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS"), _i64, _i64,
+                                      np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")]
+        R.ref_softmax_i32.argtypes = [_i32p, _i64, _i64, _f32p]
         R.ref_transpose_contig_f32.argtypes = [_f32p, _i64, _i64, _i64, _i64, _f32p]
         R.ref_attn_fwd_f32.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, ctypes.c_float,
                                        ctypes.c_int, _f32p, _vp]
@@ -193,6 +200,33 @@ def softmax(x):
     y = np.empty_like(x)
     lib().orc_softmax_f32(x.reshape(-1), y.reshape(-1), rows, cols)
     return y
+
+
+def softmax_f64(x):
+    """cpu_softmax<double, double> over the last axis (Softmax of a Float64 tensor)."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    rows, cols = int(np.prod(x.shape[:-1])), x.shape[-1]
+    y = np.empty_like(x)
+    lib().orc_softmax_f64(x.reshape(-1), y.reshape(-1), rows, cols)
+    return y
+
+
+def softmax_i32(x):
+    """cpu_softmax<int, float> over the last axis (Softmax of an Int32 tensor -> Float32)."""
+    x = np.ascontiguousarray(x, dtype=np.int32)
+    rows, cols = int(np.prod(x.shape[:-1])), x.shape[-1]
+    y = np.empty(x.shape, np.float32)
+    lib().orc_softmax_i32(x.reshape(-1), y.reshape(-1), rows, cols)
+    return y
+
+
+def softmax_bwd_f64(y, g):
+    """cpu_softmax_backward with RT = double (Float64 operands; Float32 ones widen exactly)."""
+    y, g = np.ascontiguousarray(y, np.float64), np.ascontiguousarray(g, np.float64)
+    rows, cols = int(np.prod(y.shape[:-1])), y.shape[-1]
+    dx = np.empty_like(y)
+    lib().orc_softmax_bwd_f64(y.reshape(-1), g.reshape(-1), dx.reshape(-1), rows, cols)
+    return dx
 
 
 def softmax_bwd(y, g):

@@ -13,9 +13,11 @@
  *     orc_softmax_f32 and the composed forward: bit-exact against the
  *     reference's own header kernels compiled from /root/reference into
  *     oracle/_ref (ref_shim.cpp), on config-1 inputs and ragged shapes.
- *   - orc_softmax_bwd_f32 (its reference header cannot be compiled here):
- *     closed form y*(g - <g,y>) in fp64, sum-to-zero invariant, and fp64
- *     central differences of the forward.
+ *   - orc_softmax_f64 and orc_softmax_i32: bit-exact against the reference's
+ *     cpu_softmax<double, double> and cpu_softmax<int, float> in oracle/_ref.
+ *   - orc_softmax_bwd_f32 / _f64 (their reference header cannot be compiled
+ *     here): closed form y*(g - <g,y>) in fp64 (f32) or long double (f64),
+ *     sum-to-zero invariant, and central differences of the forward.
  *   - orc_attn_bwd_f32: per-stage bit-exact against the reference matmul and
  *     multiply kernels in oracle/_ref, plus fp64 finite differences of
  *     L = sum(O * dO) on small shapes, and Q = 0 => dK = 0.
@@ -169,6 +171,56 @@ void orc_softmax_bwd_f32(const float* y, const float* g, float* dx, int64_t rows
         const float* gr = g + r * cols;
         float* dr = dx + r * cols;
         float dot = 0.0f;
+        for (int64_t k = 0; k < cols; ++k) dot += gr[k] * yr[k];
+        for (int64_t k = 0; k < cols; ++k) dr[k] = yr[k] * (gr[k] - dot);
+    }
+}
+
+/* cpu_softmax<double, double>: as the fp32 version with RT = double (max from
+ * lowest(), exp in double, double running sum, divide). */
+void orc_softmax_f64(const double* x, double* y, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const double* xr = x + r * cols;
+        double* yr = y + r * cols;
+        double mx = -DBL_MAX;
+        for (int64_t k = 0; k < cols; ++k)
+            if (xr[k] > mx) mx = xr[k];
+        double sum = 0.0;
+        for (int64_t k = 0; k < cols; ++k) {
+            double e = exp(xr[k] - mx);
+            yr[k] = e;
+            sum += e;
+        }
+        for (int64_t k = 0; k < cols; ++k) yr[k] /= sum;
+    }
+}
+
+/* cpu_softmax<int, float>: RT = float, so every int enters the arithmetic
+ * converted to float (the compare with the float max, the max itself, and
+ * x - max in float before exp in double). */
+void orc_softmax_i32(const int32_t* x, float* y, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const int32_t* xr = x + r * cols;
+        float* yr = y + r * cols;
+        float mx = -FLT_MAX;
+        for (int64_t k = 0; k < cols; ++k)
+            if ((float)xr[k] > mx) mx = (float)xr[k];
+        float sum = 0.0f;
+        for (int64_t k = 0; k < cols; ++k) {
+            float e = (float)exp((double)((float)xr[k] - mx));
+            yr[k] = e;
+            sum += e;
+        }
+        for (int64_t k = 0; k < cols; ++k) yr[k] /= sum;
+    }
+}
+
+void orc_softmax_bwd_f64(const double* y, const double* g, double* dx, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const double* yr = y + r * cols;
+        const double* gr = g + r * cols;
+        double* dr = dx + r * cols;
+        double dot = 0.0;
         for (int64_t k = 0; k < cols; ++k) dot += gr[k] * yr[k];
         for (int64_t k = 0; k < cols; ++k) dr[k] = yr[k] * (gr[k] - dot);
     }

@@ -57,6 +57,13 @@ void orc_masked_fill_f32(const float* in, const int32_t* mask, float fill,
 void orc_softmax_f32(const float* x, float* y, int64_t rows, int64_t cols);
 /* cpu_softmax_backward over the last axis (src/inferno/gradfn/softmaxbackward.h:64-131) */
 void orc_softmax_bwd_f32(const float* y, const float* g, float* dx, int64_t rows, int64_t cols);
+/* Softmax's other dtypes (softmax.cpp:25 dispatchAny, RT = promote_t<AT, float>,
+ * dtype_dispatch.h:8-52): cpu_softmax<double, double> and cpu_softmax<int, float>. */
+void orc_softmax_f64(const double* x, double* y, int64_t rows, int64_t cols);
+void orc_softmax_i32(const int32_t* x, float* y, int64_t rows, int64_t cols);
+/* cpu_softmax_backward<double, double, double> (RT = promote_t<AT, GT> of
+ * dispatchFloatTwo, softmaxbackward.cpp:40-45; a Float32 operand converts exactly). */
+void orc_softmax_bwd_f64(const double* y, const double* g, double* dx, int64_t rows, int64_t cols);
 
 /* ---- attention, composed as InfernoApp/main.cpp:737-754 ------------------ */
 /* Forward on dense [B,H,Tq,D] q and [B,H,Tk,D] k, v.  Causal masking is

@@ -93,6 +93,20 @@ void ref_softmax_f32(const float* x, int64_t rows, int64_t cols, float* y) {
     Inferno::cpu_softmax<float, float>(x, y, s, st, st, 0, 0, 1);
 }
 
+// The other two instantiations Softmax dispatches (dispatchAny with
+// promote_t<AT, float>, dtype_dispatch.h:8-52): Float64 -> Float64 and
+// Int32 -> Float32.
+void ref_softmax_f64(const double* x, int64_t rows, int64_t cols, double* y) {
+    Shape s{(size_t)rows, (size_t)cols};
+    Shape st = dense_strides(s);
+    Inferno::cpu_softmax<double, double>(x, y, s, st, st, 0, 0, 1);
+}
+void ref_softmax_i32(const int32_t* x, int64_t rows, int64_t cols, float* y) {
+    Shape s{(size_t)rows, (size_t)cols};
+    Shape st = dense_strides(s);
+    Inferno::cpu_softmax<int, float>(x, y, s, st, st, 0, 0, 1);
+}
+
 // transpose(-1,-2).contiguous() of a dense [B,H,R,C] tensor -> [B,H,C,R].
 void ref_transpose_contig_f32(const float* x, int64_t B, int64_t H, int64_t R, int64_t C,
                               float* out) {

@@ -31,6 +31,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <fstream>
 #include <functional>
 #include <iostream>
@@ -328,6 +329,61 @@ static int cmd_softmax(int argc, char** argv) {
     return 0;
 }
 
+// Softmax of a Float64 or Int32 tensor (the reference's other dispatchAny
+// dtypes): x.bin holds doubles or int32s, g.bin the gradient in the output's
+// dtype (Float64).  The backward runs where it can be seeded with g through
+// (y * g).backward(): on the CPU device.
+static int cmd_softmax_typed(int argc, char** argv) {
+    if (argc < 8) throw Error("usage: softmax-typed <dir> rows cols f64|i32 cpu|hip axis");
+    const std::string dir = argv[2];
+    const size_t R = std::stoul(argv[3]), C = std::stoul(argv[4]);
+    const std::string ts = argv[5];
+    const Device dev = parse_dev(argv[6]);
+    const int axis = std::stoi(argv[7]);
+    auto raw = [&](const std::string& name, size_t bytes) {
+        std::vector<char> v(bytes);
+        std::ifstream f(dir + "/" + name, std::ios::binary);
+        if (!f.read(v.data(), (std::streamsize)bytes)) throw Error("cannot read " + dir + "/" + name);
+        return v;
+    };
+    auto save = [&](const std::string& name, const Tensor& t) {
+        Tensor h = t.to(Device::cpu()).contiguous();
+        std::ofstream f(dir + "/" + name, std::ios::binary);
+        f.write(static_cast<const char*>(h.data_ptr()), (std::streamsize)(h.numel() * dtype_size(h.dtype())));
+    };
+    if (ts == "f64") {
+        auto xb = raw("x.bin", R * C * 8);
+        std::vector<double> xv(R * C);
+        std::memcpy(xv.data(), xb.data(), xb.size());
+        const bool grad = dev.is_cpu();
+        Tensor x(DType::Float64, xv, {R, C}, "x", dev, grad);
+        Tensor y = Softmax(x, axis);
+        if (y.dtype() != DType::Float64) throw Error("softmax-typed: Float64 in, Float64 out expected");
+        save("y.bin", y);
+        if (grad) {
+            auto gb = raw("g.bin", R * C * 8);
+            std::vector<double> gv(R * C);
+            std::memcpy(gv.data(), gb.data(), gb.size());
+            Tensor g(DType::Float64, gv, {R, C}, "g", dev);
+            (y * g).backward();
+            if (x.Getgrad().dtype() != DType::Float64) throw Error("softmax-typed: Float64 gradient expected");
+            save("dx.bin", x.Getgrad());
+        }
+    } else if (ts == "i32") {
+        auto xb = raw("x.bin", R * C * 4);
+        std::vector<int32_t> xv(R * C);
+        std::memcpy(xv.data(), xb.data(), xb.size());
+        Tensor x(DType::Int32, xv, {R, C}, "x", dev);
+        Tensor y = Softmax(x, axis);
+        if (y.dtype() != DType::Float32) throw Error("softmax-typed: Int32 in, Float32 out expected");
+        save("y.bin", y);
+    } else {
+        throw Error("softmax-typed: f64 or i32");
+    }
+    std::cout << "softmax-typed ok\n";
+    return 0;
+}
+
 static int cmd_decode(int argc, char** argv) {
     if (argc < 9) throw Error("usage: decode <dir> B H Tk D f32|bf16 cpu|hip");
     const std::string dir = argv[2];
@@ -472,6 +528,7 @@ int main(int argc, char** argv) {
         if (cmd == "selftest") return selftest(parse_dev(argc > 2 ? argv[2] : "cpu"));
         if (cmd == "attn") return cmd_attn(argc, argv);
         if (cmd == "softmax") return cmd_softmax(argc, argv);
+        if (cmd == "softmax-typed") return cmd_softmax_typed(argc, argv);
         if (cmd == "decode") return cmd_decode(argc, argv);
         if (cmd == "ckpt-save" || cmd == "ckpt-load") return cmd_ckpt(argc, argv);
         if (cmd == "mask") return cmd_mask(argc, argv);

@@ -194,6 +194,42 @@ def test_bwd_validation():
     assert L.inf_attn_bwd(*args, FAKE, 1 << 20, 1, 1, 8, 8, 96, 0.125, 1, ia.INF_F32, None) == 5
 
 
+@pytest.mark.parametrize("which", ["dq", "dk", "dv"])
+@pytest.mark.parametrize("st,B,H,T,ok", [
+    (Strides(2 * 8 * 64, 8 * 64, 64, 1), 2, 2, 8, True),     # dense [B, H, T, D]
+    (Strides(8 * 2 * 3 * 64, 64, 2 * 3 * 64, 1), 2, 2, 8, True),  # a [B, T, 3, H, D] gradient buffer
+    (Strides(2 * 8 * 64, 8 * 64, 0, 1), 2, 2, 8, False),     # every row of a head on one address
+    (Strides(2 * 8 * 64, 0, 64, 1), 2, 2, 8, False),         # both heads on one buffer
+    (Strides(0, 8 * 64, 64, 1), 2, 2, 8, False),             # both batches on one buffer
+    (Strides(2 * 8 * 64, 8 * 64, 32, 1), 2, 2, 8, False),    # rows overlap by half a row
+    (Strides(2 * 8 * 64, 4 * 64, 64, 1), 2, 2, 8, False),    # heads overlap
+    (Strides(0, 0, 0, 1), 1, 1, 1, True),                     # one row: strides never used
+    (Strides(64, 0, 0, 1), 2, 1, 1, True),                    # B x 1 x 1 rows 64 apart
+])
+def test_bwd_rejects_overlapping_outputs(which, st, B, H, T, ok):
+    """Output views (dq, dk, dv) that map two elements onto one address are rejected before
+    launch; overlap-free ones pass the view checks (and fail on the missing workspace)."""
+    L = ia.lib()
+    s = dense(B, H, T, 64)
+    views = {"dq": s, "dk": s, "dv": s}
+    views[which] = st
+    args = [FAKE, s] * 5 + [FAKE] + [FAKE, views["dq"], FAKE, views["dk"], FAKE, views["dv"]]
+    r = L.inf_attn_bwd(*args, None, 0, B, H, T, T, 64, 0.125, 1, ia.INF_F32, None)
+    assert r == (6 if ok else 3)
+
+
+def test_fwd_and_decode_reject_overlapping_outputs():
+    assert fwd(so=Strides(8 * 64, 8 * 64, 0, 1)) == 3
+    assert fwd(so=Strides(8 * 64, 0, 64, 1), H=2) == 3
+    L = ia.lib()
+    s, kv = dense(2, 2, 1, 64), dense(2, 2, 100, 64)
+    # [B, H, 1, D] outputs: the head stride must keep heads apart
+    assert L.inf_attn_decode(FAKE, s, FAKE, kv, FAKE, kv, FAKE, Strides(128, 0, 64, 1), 2, 2, 100, 64, 0.125,
+                             ia.INF_F32, None, 0, None) == 3
+    assert L.inf_attn_decode(FAKE, s, FAKE, kv, FAKE, kv, FAKE, Strides(128, 64, 0, 1), 2, 2, 100, 64, 0.125,
+                             ia.INF_F32, None, 0, None) == 6
+
+
 def test_decode_and_softmax_validation():
     L = ia.lib()
     s = dense(2, 2, 1, 64)

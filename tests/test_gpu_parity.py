@@ -310,27 +310,82 @@ def np_attn_fwd_bwd64(q, k, v, do, scale):
     return o, (m + np.log(l))[:, 0], (ds @ k) * scale, (ds.T @ q) * scale, p.T @ do
 
 
-def test_config4_long_context_f32(ia):
-    """Config 4 (T=8192, D=128, Q,K ~ N(0, 3^2): sharp softmax) at full length on the GPU.
+@pytest.mark.parametrize("dtype,H", [
+    (torch.float32, 2),      # 32 workgroups: the forward and backward split plans
+    (torch.float32, 16),     # config 4's own grid: unsplit
+    (torch.bfloat16, 2),     # bf16 split plans
+    (torch.bfloat16, 16),    # config 4 bf16 as benched: unsplit
+])
+def test_config4_long_context(ia, dtype, H):
+    """Config 4 (B1 T8192 D128, Q,K ~ N(0, 3^2): a sharp softmax that stresses the online
+    max / LSE) at full length on the GPU.
 
     Rows < 1024 of O, LSE and dQ depend only on keys < 1024, so they are checked against the
-    oracle on that prefix; the whole head (including dK, dV) is checked against the fp64 formula.
-    """
-    print("[case] config4 long context f32", flush=True)
-    B, H, T, D = 1, 2, 8192, 128
+    oracle on that prefix for two heads; one whole head (dK, dV included) against the fp64
+    formula; over every head, finiteness and sum_j dV_j = sum_i dO_i (rows of P sum to 1).
+    bf16: the oracle and the formula take the same bf16-rounded inputs; bar 2e-2 (LSE 1e-3)."""
+    bf = dtype == torch.bfloat16
+    print(f"[case] config4 long context {dtype} H{H}", flush=True)
+    B, T, D = 1, 8192, 128
     q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=42, qk_sigma=3.0)
-    o, lse, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do)
+    if bf:
+        q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
+    tol = TOL_BF16 if bf else TOL_F32
+    tol_lse = 1e-3 if bf else TOL_F32
+    o, lse, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do, dtype=dtype)
+    assert np.isfinite(o).all() and np.isfinite(lse).all()
+    assert np.isfinite(dq).all() and np.isfinite(dk).all() and np.isfinite(dv).all()
+    sdo = do.astype(np.float64).sum(axis=2)
+    assert oracle.rel_err(dv.astype(np.float64).sum(axis=2), sdo) <= tol, "sum_j dV_j != sum_i dO_i"
     t = 1024
-    sl = (slice(0, 1), slice(1, 2), slice(0, t))
-    o_r, lse_r = oracle.attn_fwd(q[sl], k[sl], v[sl])
-    dq_r, _, _ = oracle.attn_bwd(q[sl], k[sl], v[sl], do[sl])
-    for name, x, r in (("O", o[sl], o_r), ("LSE", lse[sl], lse_r), ("dQ", dq[sl], dq_r)):
-        e = oracle.rel_err(x, r)
-        assert e <= TOL_F32, f"prefix {name} rel err {e:.3e}"
-    ref = np_attn_fwd_bwd64(q[0, 1], k[0, 1], v[0, 1], do[0, 1], ia.default_scale(D))
+    for h in (0, H - 1):
+        sl = (slice(0, 1), slice(h, h + 1), slice(0, t))
+        o_r, lse_r = oracle.attn_fwd(q[sl], k[sl], v[sl])
+        dq_r, _, _ = oracle.attn_bwd(q[sl], k[sl], v[sl], do[sl])
+        for name, x, r, tl in (("O", o[sl], o_r, tol), ("LSE", lse[sl], lse_r, tol_lse), ("dQ", dq[sl], dq_r, tol)):
+            e = oracle.rel_err(x, r)
+            assert e <= tl, f"head {h} prefix {name} rel err {e:.3e}"
+    hf = H // 2
+    ref = np_attn_fwd_bwd64(q[0, hf], k[0, hf], v[0, hf], do[0, hf], ia.default_scale(D))
     for name, x, r in zip(("O", "LSE", "dQ", "dK", "dV"), (o, lse, dq, dk, dv), ref):
-        e = oracle.rel_err(x[0, 1], r)
-        assert e <= TOL_F32, f"full head {name} rel err {e:.3e}"
+        e = oracle.rel_err(x[0, hf], r)
+        assert e <= (tol_lse if name == "LSE" else tol), f"full head {hf} {name} rel err {e:.3e}"
+
+
+def test_config2_bf16_full_size_heads(ia):
+    """Config 2's bf16-in variant at its full B8 H12 grid (the backward plan depends on B*H):
+    three heads against the oracle on the bf16-rounded inputs at 2e-2, and over every head
+    finiteness and sum_j dV_j = sum_i dO_i."""
+    print("[case] config2 bf16 full size", flush=True)
+    B, H, T, D = 8, 12, 1024, 64
+    q, k, v, do = (bf16_round(x) for x in oracle.attn_inputs(B, H, T, D, seed=42))
+    o, lse, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do, dtype=torch.bfloat16)
+    assert np.isfinite(o).all() and np.isfinite(dq).all() and np.isfinite(dk).all() and np.isfinite(dv).all()
+    for (b, h) in ((0, 0), (3, 7), (7, 11)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        o_r, lse_r = oracle.attn_fwd(q[sl], k[sl], v[sl])
+        dq_r, dk_r, dv_r = oracle.attn_bwd(q[sl], k[sl], v[sl], do[sl])
+        assert oracle.rel_err(lse[sl], lse_r) <= 1e-3, f"head {(b, h)} LSE"
+        for name, x, r in (("O", o, o_r), ("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
+            e = oracle.rel_err(x[sl], r)
+            assert e <= TOL_BF16, f"head {(b, h)} {name} rel err {e:.3e}"
+    sdo = do.astype(np.float64).sum(axis=2)
+    assert oracle.rel_err(dv.astype(np.float64).sum(axis=2), sdo) <= TOL_BF16
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_config5_decode_full_size(ia, dtype):
+    """Config 5 (decode B32 H12 Tk2048 D64) as benched: the whole step against the oracle
+    (fp32 1e-4; bf16 caches and query, rounded the same way for the oracle, 2e-2)."""
+    print(f"[case] config5 decode full size {dtype}", flush=True)
+    B, H, Tk, D = 32, 12, 2048, 64
+    q = oracle.randn(502, (B, H, 1, D))
+    kc = oracle.randn(500, (B, H, Tk, D))
+    vc = oracle.randn(501, (B, H, Tk, D))
+    if dtype == torch.bfloat16:
+        q, kc, vc = bf16_round(q), bf16_round(kc), bf16_round(vc)
+    o = host(ia.attn_decode(dev(q, dtype), dev(kc, dtype), dev(vc, dtype)))
+    assert oracle.rel_err(o, oracle.attn_decode(q, kc, vc)) <= (TOL_F32 if dtype == torch.float32 else TOL_BF16)
 
 
 @pytest.mark.parametrize("B,H,Tk,D", [(2, 3, 1, 64), (2, 3, 100, 64), (1, 2, 257, 32), (2, 2, 513, 128), (4, 12, 2048, 64)])
@@ -409,6 +464,47 @@ def test_softmax_fwd_bwd_f32(ia, rows, cols):
     torch.cuda.synchronize()
     assert oracle.rel_err(host(y), y_r) <= TOL_F32
     assert oracle.rel_err(host(dx), dx_r) <= TOL_F32
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 1), (5, 3), (64, 128), (33, 1000), (16, 1024), (4, 4096), (3, 5000),
+                                       (2, 4097), (2, 12288)])
+def test_softmax_fwd_bwd_bf16(ia, rows, cols):
+    """bf16 storage, fp32 arithmetic: the wave kernel (rows up to 4096 columns), the streaming
+    workgroup kernel (longer rows) and the scalar paths (columns not a multiple of 4), against
+    the oracle on the bf16-rounded inputs at 2e-2."""
+    print(f"[case] softmax bf16 {rows}x{cols}", flush=True)
+    x = bf16_round(oracle.randn(210, (rows, cols), 3.0))
+    g = bf16_round(oracle.randn(211, (rows, cols)))
+    y_r = oracle.softmax(x)
+    yb = bf16_round(y_r)
+    dx_r = oracle.softmax_bwd(yb, g)
+    y = ia.softmax_fwd(dev(x, torch.bfloat16))
+    dx = ia.softmax_bwd(dev(yb, torch.bfloat16), dev(g, torch.bfloat16))
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16 and dx.dtype == torch.bfloat16
+    assert oracle.rel_err(host(y), y_r) <= TOL_BF16
+    assert oracle.rel_err(host(dx), dx_r) <= TOL_BF16
+    # each row's probabilities sum to 1 within bf16 rounding of its elements
+    assert np.abs(host(y).astype(np.float64).sum(axis=1) - 1).max() <= 1e-2
+
+
+@pytest.mark.parametrize("rows,cols", [(5, 3), (64, 128), (3, 5000)])
+def test_softmax_f64_i32(ia, rows, cols):
+    """The C-ABI's other softmax dtypes: INF_F64 both ways (double arithmetic; within 1e-12 of
+    the reference-exact oracle), INF_I32 input with fp32 output (1e-4)."""
+    print(f"[case] softmax f64/i32 {rows}x{cols}", flush=True)
+    x = oracle.randn(220, (rows, cols), 3.0).astype(np.float64)
+    g = oracle.randn(221, (rows, cols)).astype(np.float64)
+    y_r = oracle.softmax_f64(x)
+    y = ia.softmax_fwd(dev(x, torch.float64))
+    dx = ia.softmax_bwd(dev(y_r, torch.float64), dev(g, torch.float64))
+    xi = (oracle.randn(222, (rows, cols), 4.0) * 3).astype(np.int32)
+    yi = ia.softmax_fwd(torch.from_numpy(xi).to("cuda"))
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float64 and dx.dtype == torch.float64 and yi.dtype == torch.float32
+    assert oracle.rel_err(y.cpu().numpy(), y_r) <= 1e-12
+    assert oracle.rel_err(dx.cpu().numpy(), oracle.softmax_bwd_f64(y_r, g)) <= 1e-12
+    assert oracle.rel_err(yi.cpu().numpy(), oracle.softmax_i32(xi)) <= TOL_F32
 
 
 def test_softmax_masked_scores_exact_zeros(ia):

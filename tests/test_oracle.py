@@ -18,8 +18,14 @@ import pytest
 import oracle
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-REF = oracle.ref_lib()
-needs_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref not built (reference tree absent)")
+# The reference build is loaded by a fixture, only by the tests that use it, so
+# a run that deselects them (`-m gpu`) never maps it.
+needs_ref = pytest.mark.skipif(not oracle.REF_PATH.exists(), reason="oracle/_ref not built (reference tree absent)")
+
+
+@pytest.fixture(scope="module")
+def REF():
+    return oracle.ref_lib()
 
 
 def bits(a):
@@ -65,7 +71,7 @@ def test_bf16_rounding_known_values():
 # ------------------------------------------------ bit-exact vs the reference
 @needs_ref
 @pytest.mark.parametrize("M,K,N", [(1, 1, 1), (3, 5, 7), (17, 64, 33), (128, 32, 128)])
-def test_matmul_bitwise_vs_reference(M, K, N):
+def test_matmul_bitwise_vs_reference(REF, M, K, N):
     a = oracle.randn(1, (1, 1, M, K))
     b = oracle.randn(2, (1, 1, K, N))
     ref = np.empty((1, 1, M, N), np.float32)
@@ -76,7 +82,7 @@ def test_matmul_bitwise_vs_reference(M, K, N):
 
 
 @needs_ref
-def test_elementwise_kernels_bitwise_vs_reference():
+def test_elementwise_kernels_bitwise_vs_reference(REF):
     L = oracle.lib()
     x = oracle.randn(3, (2, 3, 40, 40), 4.0)
     s = np.float32(0.17677669)
@@ -104,7 +110,7 @@ def test_elementwise_kernels_bitwise_vs_reference():
 
 @needs_ref
 @pytest.mark.parametrize("rows,cols", [(1, 1), (5, 7), (64, 128), (3, 1000)])
-def test_softmax_bitwise_vs_reference(rows, cols):
+def test_softmax_bitwise_vs_reference(REF, rows, cols):
     x = oracle.randn(4, (rows, cols), 5.0)
     ref = np.empty_like(x)
     REF.ref_softmax_f32(x, rows, cols, ref)
@@ -112,8 +118,60 @@ def test_softmax_bitwise_vs_reference(rows, cols):
 
 
 @needs_ref
+@pytest.mark.parametrize("rows,cols", [(1, 1), (5, 7), (64, 128), (3, 1000)])
+def test_softmax_f64_and_i32_bitwise_vs_reference(REF, rows, cols):
+    """Softmax's Float64 and Int32 instantiations (cpu_softmax<double, double>, <int, float>)."""
+    x = oracle.randn(14, (rows, cols), 5.0).astype(np.float64) * (1 + 1e-9)
+    ref = np.empty_like(x)
+    REF.ref_softmax_f64(x, rows, cols, ref)
+    assert np.array_equal(oracle.softmax_f64(x).view(np.uint64), ref.view(np.uint64))
+    # ints spanning both exact and rounded int -> float conversions (|x| > 2^24)
+    xi = (oracle.randn(15, (rows, cols), 4.0) * np.float32(3)).astype(np.int32)
+    xi.reshape(-1)[:: 3] += np.int32(1 << 25) + 1
+    refi = np.empty(xi.shape, np.float32)
+    REF.ref_softmax_i32(xi, rows, cols, refi)
+    assert np.array_equal(bits(oracle.softmax_i32(xi)), bits(refi))
+
+
+def test_softmax_f64_i32_closed_forms():
+    x = oracle.randn(16, (6, 50), 2.0).astype(np.float64)
+    y = oracle.softmax_f64(x)
+    e = np.exp(x - x.max(-1, keepdims=True))
+    np.testing.assert_allclose(y, e / e.sum(-1, keepdims=True), rtol=1e-14, atol=0)
+    xi = np.array([[0, 1, 2, -3], [5, 5, 5, 5]], np.int32)
+    yi = oracle.softmax_i32(xi)
+    ei = np.exp(xi.astype(np.float64) - xi.max(-1, keepdims=True))
+    np.testing.assert_allclose(yi, ei / ei.sum(-1, keepdims=True), rtol=1e-6)
+    assert yi.dtype == np.float32 and (yi[1] == np.float32(0.25)).all()
+
+
+def test_softmax_bwd_f64_closed_form_and_finite_differences():
+    x = oracle.randn(17, (3, 11), 1.5).astype(np.float64)
+    g = oracle.randn(18, (3, 11)).astype(np.float64)
+    y = oracle.softmax_f64(x)
+    dx = oracle.softmax_bwd_f64(y, g)
+    yl, gl = y.astype(np.longdouble), g.astype(np.longdouble)
+    closed = yl * (gl - (gl * yl).sum(-1, keepdims=True))
+    assert np.max(np.abs(dx - closed)) <= 1e-15
+    assert np.max(np.abs(dx.sum(-1))) <= 1e-15
+
+    def L(xx):
+        ee = np.exp(xx - xx.max(-1, keepdims=True))
+        return float((g * ee / ee.sum(-1, keepdims=True)).sum())
+
+    h = 1e-5
+    fd = np.zeros_like(x)
+    for idx in np.ndindex(x.shape):
+        xp, xm = x.copy(), x.copy()
+        xp[idx] += h
+        xm[idx] -= h
+        fd[idx] = (L(xp) - L(xm)) / (2 * h)
+    np.testing.assert_allclose(dx, fd, atol=1e-9)
+
+
+@needs_ref
 @pytest.mark.parametrize("B,H,T,D", [(1, 4, 128, 32), (2, 1, 17, 8), (1, 1, 1, 4), (1, 2, 65, 64)])
-def test_attention_chain_bitwise_vs_reference(B, H, T, D):
+def test_attention_chain_bitwise_vs_reference(REF, B, H, T, D):
     q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=42)
     sc = scale_of(D)
     o, _, p = oracle.attn_fwd(q, k, v, want_p=True)

@@ -13,7 +13,7 @@ import pytest
 import oracle
 from oracle import nn as onn
 
-need_ref = pytest.mark.skipif(oracle.ref_lib() is None, reason="oracle/_ref not built (no reference tree)")
+need_ref = pytest.mark.skipif(not oracle.REF_PATH.exists(), reason="oracle/_ref not built (no reference tree)")
 
 
 def rnd(seed, shape, sigma=1.0):

@@ -96,6 +96,28 @@ def test_softmax_cpu_bitwise(tmp_path):
     assert np.array_equal(bits(read(tmp_path, "dx", (6, 50))), bits(oracle.softmax_bwd(y, g)))
 
 
+def test_softmax_f64_i32_cpu_bitwise(tmp_path):
+    """Softmax of Float64 (-> Float64) and Int32 (-> Float32) tensors on the CPU device: the
+    reference's cpu_softmax<double, double> / <int, float>, and the Float64 backward."""
+    x = oracle.randn(21, (5, 37), 3.0).astype(np.float64) * (1 + 1e-9)
+    g = oracle.randn(22, (5, 37)).astype(np.float64) / 3
+    x.tofile(tmp_path / "x.bin")
+    g.tofile(tmp_path / "g.bin")
+    r = run("softmax-typed", tmp_path, 5, 37, "f64", "cpu", -1)
+    assert r.returncode == 0, r.stderr
+    y = np.fromfile(tmp_path / "y.bin", np.float64).reshape(5, 37)
+    assert np.array_equal(y.view(np.uint64), oracle.softmax_f64(x).view(np.uint64))
+    dx = np.fromfile(tmp_path / "dx.bin", np.float64).reshape(5, 37)
+    assert np.array_equal(dx.view(np.uint64), oracle.softmax_bwd_f64(y, g).view(np.uint64))
+
+    xi = (oracle.randn(23, (4, 29), 4.0) * 3).astype(np.int32)
+    xi.tofile(tmp_path / "x.bin")
+    r = run("softmax-typed", tmp_path, 4, 29, "i32", "cpu", -1)
+    assert r.returncode == 0, r.stderr
+    yi = np.fromfile(tmp_path / "y.bin", np.float32).reshape(4, 29)
+    assert np.array_equal(bits(yi), bits(oracle.softmax_i32(xi)))
+
+
 def test_decode_cpu(tmp_path):
     q = oracle.randn(1, (2, 3, 1, 16))
     kc = oracle.randn(2, (2, 3, 40, 16))
@@ -235,6 +257,30 @@ def test_attention_hip_parity(tmp_path, B, H, T, D, dtype, layout):
 
 
 @gpu
+@gpu
+def test_softmax_f64_i32_hip_parity(tmp_path):
+    """Softmax of Float64 and Int32 tensors on HIP through the C++ drop-in (forward), against the
+    reference-exact oracle: Float64 within 1e-12 of max|ref| (exp on the device differs from
+    the host's in the last bits), Int32 -> Float32 within 1e-4."""
+    if not have_gpu():
+        pytest.skip("no GPU")
+    print("[case] api_driver softmax f64 / i32 hip", flush=True)
+    x = oracle.randn(24, (33, 1000), 3.0).astype(np.float64)
+    x.tofile(tmp_path / "x.bin")
+    for axis in (-1, 0):
+        r = run("softmax-typed", tmp_path, 33, 1000, "f64", "hip", axis)
+        assert r.returncode == 0, r.stderr
+        y = np.fromfile(tmp_path / "y.bin", np.float64).reshape(33, 1000)
+        y_r = oracle.softmax_f64(x) if axis == -1 else oracle.softmax_f64(np.ascontiguousarray(x.T)).T
+        assert oracle.rel_err(y, y_r) <= 1e-12
+    xi = (oracle.randn(25, (16, 4096), 4.0) * 3).astype(np.int32)
+    xi.tofile(tmp_path / "x.bin")
+    r = run("softmax-typed", tmp_path, 16, 4096, "i32", "hip", -1)
+    assert r.returncode == 0, r.stderr
+    yi = np.fromfile(tmp_path / "y.bin", np.float32).reshape(16, 4096)
+    assert oracle.rel_err(yi, oracle.softmax_i32(xi)) <= 1e-4
+
+
 def test_softmax_hip_parity(tmp_path):
     if not have_gpu():
         pytest.skip("no GPU")
