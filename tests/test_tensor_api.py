@@ -257,7 +257,6 @@ def test_attention_hip_parity(tmp_path, B, H, T, D, dtype, layout):
 
 
 @gpu
-@gpu
 def test_softmax_f64_i32_hip_parity(tmp_path):
     """Softmax of Float64 and Int32 tensors on HIP through the C++ drop-in (forward), against the
     reference-exact oracle: Float64 within 1e-12 of max|ref| (exp on the device differs from
@@ -281,6 +280,7 @@ def test_softmax_f64_i32_hip_parity(tmp_path):
     assert oracle.rel_err(yi, oracle.softmax_i32(xi)) <= 1e-4
 
 
+@gpu
 def test_softmax_hip_parity(tmp_path):
     if not have_gpu():
         pytest.skip("no GPU")
