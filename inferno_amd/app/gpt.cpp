@@ -298,6 +298,51 @@ static int run_decode_check(const std::string& dir, const Device& dev, size_t P)
     return 0;
 }
 
+// --------------------------------------------------------- generate-check
+// Greedy generation from given parameters and prompt (tokens.bin, [B, P]
+// int32): prefill through the KV caches, then N tokens, each the argmax of
+// the last position's logits (picked on the device) fed back.  Writes
+// generated.bin ([B, N] int32) and gen_logits.bin ([B, N, V] fp32, the
+// logits each pick was made from).
+static int run_generate_check(const std::string& dir, const Device& dev, size_t P, size_t N) {
+    std::ifstream cf(dir + "/config.txt");
+    size_t L, C, H, T, V, B;
+    if (!(cf >> L >> C >> H >> T >> V >> B)) throw Error("bad config.txt");
+    if (P < 1 || P + N > T) throw Error("generate-check: need 1 <= prompt and prompt + new <= context");
+    GPTModel model(V, T, C, H, L, true, dev, DType::Float32);
+    load_params(model, dir);
+    auto tok = read_file(dir + "/tokens.bin");
+    if (tok.size() < B * P * 4) throw Error("generate-check: tokens.bin holds fewer than B * prompt tokens");
+    std::vector<int32_t> prompt(B * P);
+    std::memcpy(prompt.data(), tok.data(), prompt.size() * 4);
+    auto caches = model.make_caches(B, T, dev);
+    std::vector<int32_t> gen(B * N);
+    std::vector<float> glog(B * N * V);
+    Tensor x(DType::Int32, prompt, std::vector<size_t>{B, P}, "prompt", dev);
+    for (size_t i = 0; i < N; ++i) {
+        Tensor logits = model.forward_cached(x, caches);  // [B, t, V]
+        const size_t t = logits.shape()[1];
+        Tensor last = logits.slice(1, t - 1, t - 1);      // [B, 1, V]
+        const std::vector<double> pick = argmax(last).to_host_double();
+        const std::vector<float> lh = last.to_host_float();
+        std::vector<int32_t> nxt(B);
+        for (size_t b = 0; b < B; ++b) {
+            nxt[b] = (int32_t)pick[b];
+            gen[b * N + i] = nxt[b];
+            std::memcpy(&glog[(b * N + i) * V], &lh[b * V], V * 4);
+        }
+        x = Tensor(DType::Int32, nxt, std::vector<size_t>{B, 1}, "next", dev);
+    }
+    {
+        std::ofstream f(dir + "/generated.bin", std::ios::binary);
+        f.write(reinterpret_cast<const char*>(gen.data()), (std::streamsize)(gen.size() * 4));
+    }
+    write_f32(dir + "/gen_logits.bin", glog);
+    sync(dev);
+    std::cout << "generate-check ok\n";
+    return 0;
+}
+
 // ----------------------------------------------------------------- generate
 // Greedy generation with KV caches on hip:0: a random prompt of P tokens per
 // sequence, then N new tokens, each fed back (argmax on the host).
@@ -355,6 +400,138 @@ static int run_generate(int argc, char** argv) {
         "\"first_tokens\": [%d, %d, %d]}\n",
         L, C, H, V, B, P, N, pm, dm / steps, (double)B * steps / (dm * 1e-3), gen[0], gen.size() > 1 ? gen[1] : 0,
         gen.size() > 2 ? gen[2] : 0);
+    return 0;
+}
+
+// ---------------------------------------------------------------- fullcheck
+// Properties of one full-size training step (config 3 by default) that need
+// no oracle run at that size:
+//   - params0.bin / grads.bin / params1.bin: every parameter before the step,
+//     its gradient and its value after AdamW (fp32, concatenated in the order
+//     of params.txt: "name numel" lines), for an elementwise check of the
+//     update and of finiteness;
+//   - dirderiv.txt: directional derivatives.  For a direction u (N(0, 1) per
+//     element, seeded) over a set of parameters and a step h, the loss at
+//     P + h u and P - h u (forward only) against the gradient's prediction
+//     sum g . (P+ - P-) / 2h over the realised fp32 perturbations.  Sets: all
+//     parameters, then each parameter type across the layers.  Lines:
+//     "set h L0 Lplus Lminus predicted".
+static int run_fullcheck(int argc, char** argv) {
+    const std::string dir = argv[2];
+    const size_t L = arg(argc, argv, "--layers", 12), C = arg(argc, argv, "--dmodel", 768),
+                 H = arg(argc, argv, "--heads", 12), T = arg(argc, argv, "--ctx", 1024),
+                 V = arg(argc, argv, "--vocab", 8192), B = arg(argc, argv, "--batch", 8);
+    const Device dev = Device::hip(0);
+    RandomGenerator::initializeWithSeed(42);
+    GPTModel model(V, T, C, H, L, true, dev, DType::Float32);
+    init_normal(model, 0.02f, dev);
+    std::mt19937_64 rng(42);
+    std::uniform_int_distribution<int> tokd(0, (int)V - 1);
+    std::vector<int32_t> seq(B * (T + 1));
+    for (auto& t : seq) t = tokd(rng);
+    std::vector<int32_t> xs(B * T), ys(B * T);
+    for (size_t b = 0; b < B; ++b)
+        for (size_t t = 0; t < T; ++t) {
+            xs[b * T + t] = seq[b * (T + 1) + t];
+            ys[b * T + t] = seq[b * (T + 1) + t + 1];
+        }
+    Tensor x(DType::Int32, xs, std::vector<size_t>{B, T}, "tokens", dev);
+    Tensor y(DType::Int32, ys, std::vector<size_t>{B, T}, "targets", dev);
+
+    // parameters by state-dict name
+    std::vector<std::pair<std::string, Tensor*>> named;
+    {
+        StateDict sd = model.state_dict();
+        std::vector<Tensor*> params = model.parameters();
+        for (auto& [name, t] : sd)
+            for (Tensor* p : params)
+                if (GetImpl(*p) == GetImpl(t)) named.emplace_back(name, p);
+    }
+    std::vector<std::vector<float>> p0, g;
+    CrossEntropyLoss loss_fn;
+    OptimizerAdamW opt(model.parameters());
+    Tensor logits = model.forward(x);
+    Tensor loss = loss_fn(logits, y);
+    loss.backward();
+    const double L0 = loss.to_host_float()[0];
+    {
+        std::ofstream idx(dir + "/params.txt");
+        std::ofstream fp(dir + "/params0.bin", std::ios::binary), fg(dir + "/grads.bin", std::ios::binary);
+        for (auto& [name, p] : named) {
+            if (!p->grad()) throw Error("fullcheck: no gradient for " + name);
+            p0.push_back(p->to_host_float());
+            g.push_back(p->grad()->to_host_float());
+            idx << name << " " << p0.back().size() << "\n";
+            fp.write(reinterpret_cast<const char*>(p0.back().data()), (std::streamsize)(p0.back().size() * 4));
+            fg.write(reinterpret_cast<const char*>(g.back().data()), (std::streamsize)(g.back().size() * 4));
+        }
+    }
+    opt.step();
+    opt.zero_grad();
+    {
+        std::ofstream fp(dir + "/params1.bin", std::ios::binary);
+        for (auto& [name, p] : named) {
+            const std::vector<float> v = p->to_host_float();
+            fp.write(reinterpret_cast<const char*>(v.data()), (std::streamsize)(v.size() * 4));
+        }
+    }
+    sync(dev);
+    std::cout << "step done: loss " << L0 << "\n" << std::flush;
+
+    // directional derivatives (forward only, parameters restored from p0 after each set)
+    auto type_of = [](const std::string& name) {
+        return name.rfind("block", 0) == 0 ? "block*" + name.substr(name.find('.')) : name;
+    };
+    std::vector<std::string> sets{"all"};
+    for (auto& [name, p] : named) {
+        const std::string t = type_of(name);
+        if (std::find(sets.begin(), sets.end(), t) == sets.end()) sets.push_back(t);
+    }
+    auto loss_now = [&]() {
+        NoGradGuard ng;
+        Tensor lg = model.forward(x);
+        return (double)loss_fn(lg, y).to_host_float()[0];
+    };
+    std::ofstream out(dir + "/dirderiv.txt");
+    out.precision(17);
+    const double hs[] = {3e-4, 1e-3, 3e-3};
+    for (size_t si = 0; si < sets.size(); ++si) {
+        std::vector<size_t> members;
+        for (size_t i = 0; i < named.size(); ++i)
+            if (sets[si] == "all" || type_of(named[i].first) == sets[si]) members.push_back(i);
+        std::vector<std::vector<float>> u(members.size());
+        for (size_t m = 0; m < members.size(); ++m) {
+            std::mt19937_64 ur(1000003ULL * (si + 1) + members[m]);
+            std::normal_distribution<float> nd(0.f, 1.f);
+            u[m].resize(p0[members[m]].size());
+            for (float& e : u[m]) e = nd(ur);
+        }
+        for (const double h : hs) {
+            double pred = 0.0, lp = 0.0, lm = 0.0;
+            std::vector<std::vector<float>> plus(members.size());
+            for (int sign : {1, -1}) {
+                for (size_t m = 0; m < members.size(); ++m) {
+                    const std::vector<float>& base = p0[members[m]];
+                    std::vector<float> v(base.size());
+                    for (size_t e = 0; e < v.size(); ++e) v[e] = base[e] + (float)(sign * h) * u[m][e];
+                    if (sign > 0) {
+                        plus[m] = v;
+                    } else {
+                        const std::vector<float>& gm = g[members[m]];
+                        for (size_t e = 0; e < v.size(); ++e)
+                            pred += (double)gm[e] * ((double)plus[m][e] - (double)v[e]);
+                    }
+                    set_param(*named[members[m]].second, v);
+                }
+                (sign > 0 ? lp : lm) = loss_now();
+            }
+            pred /= 2.0 * h;
+            for (size_t m = 0; m < members.size(); ++m) set_param(*named[members[m]].second, p0[members[m]]);
+            out << sets[si] << " " << h << " " << L0 << " " << lp << " " << lm << " " << pred << "\n" << std::flush;
+        }
+        std::cout << "direction " << sets[si] << " done\n" << std::flush;
+    }
+    std::cout << "fullcheck ok\n";
     return 0;
 }
 
@@ -492,12 +669,18 @@ int main(int argc, char** argv) {
             const Device dev = std::strcmp(argv[3], "hip") == 0 ? Device::hip(0) : Device::cpu();
             return run_decode_check(argv[2], dev, arg(argc, argv, "--prefill", 4));
         }
+        if (argc >= 3 && std::strcmp(argv[1], "fullcheck") == 0) return run_fullcheck(argc, argv);
+        if (argc >= 4 && std::strcmp(argv[1], "generate-check") == 0) {
+            const Device dev = std::strcmp(argv[3], "hip") == 0 ? Device::hip(0) : Device::cpu();
+            return run_generate_check(argv[2], dev, arg(argc, argv, "--prompt", 4), arg(argc, argv, "--new", 8));
+        }
         if (argc >= 4 && std::strcmp(argv[1], "step") == 0) {
             const Device dev = std::strcmp(argv[3], "hip") == 0 ? Device::hip(0) : Device::cpu();
             return run_step(argv[2], dev, !flag(argc, argv, "--untied"));
         }
         std::cerr << "usage: gpt bench [options] | gpt step <dir> <cpu|hip> [--untied] | gpt decode-check <dir> "
-                     "<cpu|hip> [--prefill P] | gpt generate [options]\n";
+                     "<cpu|hip> [--prefill P] | gpt generate-check <dir> <cpu|hip> [--prompt P] [--new N] | "
+                     "gpt generate [options]\n";
         return 2;
     } catch (const std::exception& e) {
         std::cerr << "error: " << e.what() << "\n";

@@ -78,11 +78,9 @@ def gpt_loss(params, tokens, targets, L, C, H):
     return gpt_step(params, tokens, targets, L, C, H, backward=False)
 
 
-def gpt_step(params, tokens, targets, L, C, H, step=1, lr=3e-4, backward=True):
-    """Returns (loss, grads, new_params) for one AdamW step from zero moments."""
-    P = {k: np.asarray(v, np.float32) for k, v in params.items()}
+def _forward(P, tokens, L, C, H):
+    """The model's forward: returns (logits [B*T, V], what the backward needs)."""
     B, T = tokens.shape
-    V = P["tok_embedding.weight"].shape[0]
     D = C // H
     N = B * T
     E = P["tok_embedding.weight"]
@@ -107,6 +105,27 @@ def gpt_step(params, tokens, targets, L, C, H, step=1, lr=3e-4, backward=True):
         x = (h + f2).astype(np.float32)
     xf, mf, sf = onn.layernorm(x, P["ln1.gamma"], P["ln1.beta"])
     logits = _mm(xf, E.T)
+    return logits, (x, xf, mf, sf, cache)
+
+
+def gpt_logits(params, tokens, L, C, H):
+    """Logits [B, T, V] of the causal forward over tokens [B, T] (every position attends to
+    itself and the positions before it: what incremental decoding must reproduce)."""
+    P = {k: np.asarray(v, np.float32) for k, v in params.items()}
+    B, T = tokens.shape
+    logits, _ = _forward(P, np.ascontiguousarray(tokens, np.int32), L, C, H)
+    return logits.reshape(B, T, -1)
+
+
+def gpt_step(params, tokens, targets, L, C, H, step=1, lr=3e-4, backward=True):
+    """Returns (loss, grads, new_params) for one AdamW step from zero moments."""
+    P = {k: np.asarray(v, np.float32) for k, v in params.items()}
+    B, T = tokens.shape
+    V = P["tok_embedding.weight"].shape[0]
+    D = C // H
+    N = B * T
+    E = P["tok_embedding.weight"]
+    logits, (x, xf, mf, sf, cache) = _forward(P, tokens, L, C, H)
     loss = onn.cross_entropy(logits, targets.reshape(-1))
     if not backward:
         return loss
