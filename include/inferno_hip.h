@@ -158,6 +158,22 @@ int inf_attn_decode(const void* q, inf_strides sq, const void* kcache, inf_strid
                     int Tk, int D, float scale, inf_dtype dt, void* workspace, size_t ws_bytes,
                     void* stream);
 
+/*
+ * inf_attn_decode without a workspace: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): the split partials
+ * live in a static 4 MiB device array of the library (one per device, held
+ * until the process ends), so the call allocates nothing.  Same arguments,
+ * kernels and results as inf_attn_decode.  A shape whose partials need more
+ * than 4 MiB (inf_attn_workspace_bytes(INF_OP_ATTN_DECODE, ...) > 4 MiB; only
+ * some head-dim-128 shapes) returns INF_ERR_WORKSPACE before any HIP call.
+ * Every call on a device shares that device's array: calls that overlap on
+ * one device (other streams, other threads) race.
+ */
+int inf_attn_decode_static(const void* q, inf_strides sq, const void* kcache, inf_strides sk,
+                           const void* vcache, inf_strides sv, void* o, inf_strides so, int B, int H,
+                           int Tk, int D, float scale, inf_dtype dt, void* stream);
+
 /* ---- element-wise support for the Tensor layer around the path ------------- */
 
 /* dst[i] = value for i < n; elem_bytes 1, 2 or 4; `bits` holds the value's bit

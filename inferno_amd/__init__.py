@@ -64,6 +64,7 @@ EXPORTS = (
     "inf_col_sum",
     "inf_binary_bcast",
     "inf_argmax_rows",
+    "inf_attn_decode_static",
     "inf_last_error_detail",
 )
 
@@ -150,6 +151,7 @@ def lib() -> ctypes.CDLL:
         L.inf_col_sum.argtypes = [vp, i64, i64, i64, vp, i32, i32, vp, sz, vp]
         L.inf_binary_bcast.argtypes = [i32, vp, vp, vp, i64, i64, i32, vp]
         L.inf_argmax_rows.argtypes = [vp, i64, i64, i64, vp, i32, vp]
+        L.inf_attn_decode_static.argtypes = [vp, S, vp, S, vp, S, vp, S, i32, i32, i32, i32, f32, i32, vp]
         for name in EXPORTS[11:-1]:
             getattr(L, name).restype = i32
         L.inf_last_error_detail.argtypes = []

@@ -307,6 +307,39 @@ int inf_attn_decode(const void* q, inf_strides sq, const void* kcache, inf_strid
     return hip_status(inf::launch_attn_decode(p, dt == INF_BF16, (hipStream_t)stream));
 }
 
+int inf_attn_decode_static(const void* q, inf_strides sq, const void* kcache, inf_strides sk,
+                           const void* vcache, inf_strides sv, void* o, inf_strides so, int B, int H,
+                           int Tk, int D, float scale, inf_dtype dt, void* stream) {
+    int st = common_shape(B, H, 1, Tk, D, scale, dt);
+    if (st != INF_OK) return st;
+    if ((st = check_view(q, sq, dt)) || (st = check_view(kcache, sk, dt)) ||
+        (st = check_view(vcache, sv, dt)) || (st = check_out_view(o, so, dt, B, H, 1, D)))
+        return st;
+    size_t need = 0;
+    inf_attn_workspace_bytes(INF_OP_ATTN_DECODE, B, H, 1, Tk, D, dt, &need);
+    if (need > inf::kDecodeScratchBytes) {
+        inf::set_error_detail("inf_attn_decode_static: this shape's split partials need " + std::to_string(need) +
+                              " bytes; the static scratch holds " + std::to_string(inf::kDecodeScratchBytes) +
+                              " (use inf_attn_decode with a workspace)");
+        return INF_ERR_WORKSPACE;
+    }
+    float* scratch = nullptr;
+    const int e = inf::decode_scratch(&scratch);
+    if (e != 0) {
+        inf::set_error_detail(std::string("inf_attn_decode_static: hipGetSymbolAddress of the scratch failed: ") +
+                              hipGetErrorString((hipError_t)e));
+        return INF_ERR_HIP;
+    }
+    inf::DecodeParams p{};
+    p.q = q; p.k = kcache; p.v = vcache; p.o = o;
+    p.part = scratch;
+    inf::decode_plan(B, H, Tk, D, &p.nsplit, &p.chunk);
+    p.sq = view(sq); p.sk = view(sk); p.sv = view(sv); p.so = view(so);
+    p.B = B; p.H = H; p.Tk = Tk; p.D = D;
+    p.c = scale * 1.4426950408889634f;
+    return hip_status(inf::launch_attn_decode(p, dt == INF_BF16, (hipStream_t)stream));
+}
+
 int inf_fill(void* dst, int64_t n, int elem_bytes, uint32_t bits, void* stream) {
     if (n < 0) return INF_ERR_BAD_SHAPE;
     if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4) return INF_ERR_BAD_DTYPE;

@@ -16,12 +16,45 @@
 // Scores are in the log2 domain (q is pre-scaled by scale * log2 e).  No key
 // is masked: the query sits at the end of the cache, so the causal rule
 // j <= i + (Tk - 1) admits all of them (InfernoApp/main.cpp:747-748, Tq = 1).
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 
 namespace inf {
 
 constexpr int kDecodeU = 4;  // keys per group per step
+
+// Scratch of inf_attn_decode_static: the split partials (B*H*nsplit*(D+2)
+// floats) in a file-scope device array instead of a caller's workspace.  Every
+// device the library runs on holds its own copy at its own address until the
+// process ends.  In host code the array's name is only a stand-in: the
+// kernels get the device address hipGetSymbolAddress returns with that device
+// current, looked up once per device and kept.  Calls that overlap on one
+// device share the array and race.
+static __device__ __align__(256) float scratch[kDecodeScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices] = {};
+}  // namespace
+
+int decode_scratch(float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        g_scratch[dev] = static_cast<float*>(ptr);
+    }
+    *out = g_scratch[dev];
+    return 0;
+}
 
 template <typename E>
 __device__ __forceinline__ void store_out(E* dst, float v) {

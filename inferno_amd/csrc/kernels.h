@@ -256,6 +256,12 @@ int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s);  // bf16-MFMA backw
 int launch_attn_decode(const DecodeParams& p, int bf16, hipStream_t s);
 // Decode split plan (number of key splits per row, keys per split) for a shape.
 void decode_plan(int B, int H, int Tk, int D, int* nsplit, int* chunk);
+// The static scratch of inf_attn_decode_static (4 MiB: every shape whose
+// B*H*nsplit*(D+2) floats fit; the plan keeps B*H*nsplit below 8192, so only
+// some D = 128 shapes with 4033 <= B*H*nsplit <= 8191 need more), and its
+// device address on the current device (looked up once per device).
+constexpr size_t kDecodeScratchBytes = (size_t)4 << 20;
+int decode_scratch(float** out);
 // Element types of the standalone softmax: fp32, bf16 storage (fp32
 // arithmetic), int32 input with fp32 output (forward only), fp64.
 enum class SmType { F32, BF16, I32, F64 };

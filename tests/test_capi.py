@@ -230,6 +230,26 @@ def test_fwd_and_decode_reject_overlapping_outputs():
                              ia.INF_F32, None, 0, None) == 6
 
 
+def test_static_decode_validation():
+    """inf_attn_decode_static validates like inf_attn_decode and rejects, before any HIP call,
+    a shape whose split partials exceed its 4 MiB static scratch."""
+    L = ia.lib()
+    s, kv = dense(2, 2, 1, 64), dense(2, 2, 100, 64)
+    assert L.inf_attn_decode_static(None, s, FAKE, kv, FAKE, kv, FAKE, s, 2, 2, 100, 64, 0.125, ia.INF_F32, None) == 1
+    assert L.inf_attn_decode_static(FAKE, s, FAKE, kv, FAKE, kv, FAKE, s, 2, 2, 100, 48, 0.125, ia.INF_F32, None) == 5
+    assert L.inf_attn_decode_static(FAKE, s, FAKE, kv, FAKE, kv, FAKE, Strides(128, 0, 64, 1), 2, 2, 100, 64, 0.125,
+                                    ia.INF_F32, None) == 3
+    # B*H = 4095 rows of D = 128 take 2 splits: 4095 * 2 * 130 * 4 bytes > 4 MiB
+    B, H, Tk, D = 1, 4095, 64, 128
+    assert ia.workspace_bytes(ia.OP_ATTN_DECODE, B, H, 1, Tk, D) > 4 << 20
+    sq, skv = dense(B, H, 1, D), dense(B, H, Tk, D)
+    assert L.inf_attn_decode_static(FAKE, sq, FAKE, skv, FAKE, skv, FAKE, sq, B, H, Tk, D, 0.125, ia.INF_F32,
+                                    None) == 6
+    assert b"static scratch" in L.inf_last_error_detail()
+    # 4032 rows: 4032 * 2 * 130 * 4 bytes fit
+    assert ia.workspace_bytes(ia.OP_ATTN_DECODE, 1, 4032, 1, Tk, D) <= 4 << 20
+
+
 def test_decode_and_softmax_validation():
     L = ia.lib()
     s = dense(2, 2, 1, 64)
