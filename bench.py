@@ -48,10 +48,21 @@ def _host_cpu():
     return model
 
 
-def cpu_baseline(B, H, T, D, heads: int, c4_heads: int = 0):
+def cpu_baseline(B, H, T, D, heads: int, c4_rows: int = 512, c4_heads: int = 0):
     """Time the restated reference CPU path on one pinned core: `heads` heads of config 2
-    (fwd+bwd), the whole config-5 decode step, and (if c4_heads) config 4 on c4_heads heads,
-    extrapolated to its 16 heads (heads are independent)."""
+    (fwd+bwd), the whole config-5 decode step, a row sample of config 4, and an estimate of the
+    config-3 step.
+
+    Config 4 (B1 H16 T8192 D128): the reference chain computes every entry of the T x T score
+    square whatever the mask (cpu_matmul, then masked_fill), so its work per query row is the
+    same for every row; the last `c4_rows` rows of one head against all 8192 keys (end-aligned
+    causal, which the oracle takes as Tq < Tk) are timed and scaled by 8192 / c4_rows rows and
+    16 heads.  With c4_heads > 0, whole heads are timed instead (over a minute each).
+
+    Config 3 (the GPT step) would take hours on one core: it is estimated from the oracle's
+    GEMM rate, timed on one of the step's products, times the step's GEMM FLOPs, plus its 12
+    layers x 96 heads of attention at the per-head time of the config-2 sample.
+    """
     import numpy as np
 
     import oracle
@@ -79,18 +90,51 @@ def cpu_baseline(B, H, T, D, heads: int, c4_heads: int = 0):
             "c5_decode": {"seconds": round(dt5, 4), "us_per_step": round(dt5 * 1e6, 1),
                           "GBs": round(nbytes5 / dt5 / 1e9, 3), "sample": "the whole step, B32 H12 Tk2048 D64"},
         }
+        T4, D4, H4 = 8192, 128, 16
+        F4 = 3.5 * flops_fwd(1, H4, T4, D4)
         if c4_heads > 0:
-            T4, D4 = 8192, 128
             q4, k4, v4, do4 = oracle.attn_inputs(1, c4_heads, T4, D4, seed=42, qk_sigma=3.0)
             t2 = time.perf_counter()
             oracle.attn_fwd(q4, k4, v4)
             oracle.attn_bwd(q4, k4, v4, do4)
             dt4 = time.perf_counter() - t2
-            extra["c4"] = {"seconds": round(dt4, 3), "heads_timed": c4_heads,
-                           "TFLOPs": 3.5 * flops_fwd(1, c4_heads, T4, D4) / dt4 / 1e12,
-                           "extrapolated_s_for_16_heads": round(dt4 * 16 / c4_heads, 1)}
+            est = dt4 * H4 / c4_heads
+            sample4 = f"{c4_heads} whole head(s) of 16, x{H4 / c4_heads:g} (extrapolated)"
         else:
-            extra["c4"] = "not run (one head takes over a minute on one core); bench.py --cpu-c4-heads 1"
+            r = min(c4_rows, T4)
+            q4 = oracle.randn(42, (1, 1, r, D4), 3.0)
+            k4 = oracle.randn(43, (1, 1, T4, D4), 3.0)
+            v4 = oracle.randn(44, (1, 1, T4, D4), 1.0)
+            do4 = oracle.randn(45, (1, 1, r, D4), 1.0)
+            t2 = time.perf_counter()
+            oracle.attn_fwd(q4, k4, v4)
+            oracle.attn_bwd(q4, k4, v4, do4)
+            dt4 = time.perf_counter() - t2
+            est = dt4 * (T4 / r) * H4
+            sample4 = (f"the last {r} of 8192 query rows of one head against all 8192 keys, "
+                       f"x{T4 / r:g} rows x16 heads (extrapolated: the reference computes the full score "
+                       f"square, so every row costs the same)")
+        extra["c4"] = {"seconds_timed": round(dt4, 3), "sample": sample4,
+                       "extrapolated_s_for_config4": round(est, 1),
+                       "TFLOPs": F4 / est / 1e12}
+        # config 3: GEMM rate of the oracle's cpu_matmul on a Wqkv-shaped product, 256 rows
+        a = oracle.randn(600, (256, 768))
+        w = oracle.randn(601, (768, 2304))
+        t3 = time.perf_counter()
+        oracle.matmul(a, w)
+        dt3 = time.perf_counter() - t3
+        gemm_rate = 2.0 * 256 * 768 * 2304 / dt3
+        L3, C3, V3, N3 = 12, 768, 8192, 8 * 1024
+        # per layer: Wqkv (C x 3C), W_out (C x C), ff1 (C x 4C), ff2 (4C x C), forward + 2 backward
+        # products each; plus the tied logits (C x V) forward and its 2 backward products
+        gemm_flops = 3 * 2.0 * N3 * (L3 * (3 * C3 * C3 + C3 * C3 + 8 * C3 * C3) + C3 * V3)
+        attn_s = L3 * 96 * (dt / Hs)
+        step_s = gemm_flops / gemm_rate + attn_s
+        extra["c3_gpt"] = {"estimated_s_per_step": round(step_s, 1), "tokens_per_s": round(N3 / step_s, 3),
+                           "sample": f"estimated, not run: {gemm_flops / 1e12:.2f} TFLOP of GEMMs at the oracle's "
+                                     f"{gemm_rate / 1e9:.2f} GFLOP/s (one 256x768x2304 product timed) plus "
+                                     f"12 layers x 96 heads of attention at {dt / Hs:.2f} s per head "
+                                     f"(the config-2 sample); element-wise work not counted"}
     finally:
         os.sched_setaffinity(0, prev)
     return {
@@ -118,7 +162,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--cpu-heads", type=int, default=12, help="heads in the CPU-baseline sample (0 = skip)")
-    ap.add_argument("--cpu-c4-heads", type=int, default=0, help="config-4 heads timed on the CPU (0 = skip)")
+    ap.add_argument("--cpu-c4-rows", type=int, default=512, help="config-4 query rows timed on the CPU")
+    ap.add_argument("--cpu-c4-heads", type=int, default=0,
+                    help="time whole config-4 heads on the CPU instead of a row sample (over a minute each)")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16, config-3 and config-4 lines")
     ap.add_argument("--gpt-steps", type=int, default=5, help="timed steps of the config-3 GPT line")
@@ -261,7 +307,7 @@ def main():
         out["configs"]["gpt_generate"] = bench_generate()
 
     if args.cpu_heads > 0:
-        out["cpu_baseline"] = cpu_baseline(B, H, T, D, args.cpu_heads, args.cpu_c4_heads)
+        out["cpu_baseline"] = cpu_baseline(B, H, T, D, args.cpu_heads, args.cpu_c4_rows, args.cpu_c4_heads)
     print(json.dumps(out), flush=True)
 
 
