@@ -215,13 +215,37 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
         bf16x8 pb[2], dsb[2];
         if (active && k0w < p.Tk) {
             f32x16 s, dp;
+            bf16x8 qa[NKK], da[NKK];
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk) {
-                const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&Qs[l32][16 * kk + 8 * g]);
-                const bf16x8 da = *reinterpret_cast<const bf16x8*>(&dOs[l32][16 * kk + 8 * g]);
-                s = mfma32x32x16bf16(qa, kf[kk], kk == 0 ? f32x16{} : s);  // zero accumulator as an operand
-                dp = mfma32x32x16bf16(da, vf[kk], kk == 0 ? f32x16{} : dp);
+                qa[kk] = *reinterpret_cast<const bf16x8*>(&Qs[l32][16 * kk + 8 * g]);
+                da[kk] = *reinterpret_cast<const bf16x8*>(&dOs[l32][16 * kk + 8 * g]);
             }
+            // all eight operand reads are issued before the first MFMA (the
+            // scheduler would otherwise pair each read with its MFMA and wait
+            // out one LDS latency per product)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk) {
+                s = mfma32x32x16bf16(qa[kk], kf[kk], kk == 0 ? f32x16{} : s);  // zero accumulator as an operand
+                dp = mfma32x32x16bf16(da[kk], vf[kk], kk == 0 ? f32x16{} : dp);
+            }
+            // transposed Q / dO operands of the dV / dK products, read while P and dS are formed
+            bf16x8 ado[2][NDB], aq[2][NDB];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const int qc = 16 * m + 4 * g;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    const __bf16* dorow = &dOTs[db * 32 + l32][0];
+                    const __bf16* qrow = &QTs[db * 32 + l32][0];
+                    ado[m][db] = cat4(*reinterpret_cast<const bf16x4*>(dorow + qc),
+                                      *reinterpret_cast<const bf16x4*>(dorow + qc + 8));
+                    aq[m][db] = cat4(*reinterpret_cast<const bf16x4*>(qrow + qc),
+                                     *reinterpret_cast<const bf16x4*>(qrow + qc + 8));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
             // P and dS; register r holds query row 8*(r/4) + 4*g + r%4 of the
             // tile.  Only tiles that cross the causal diagonal or the end of
             // the queries / keys evaluate the visibility test.
@@ -251,20 +275,12 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
                 p_ds(std::false_type{});
             // dV^T += dO^T P ; dK^T += Q^T dS  (reduce over the 32 queries, 16 per MFMA)
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
-                const int qc = 16 * m + 4 * g;
+            for (int m = 0; m < 2; ++m)
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) {
-                    const __bf16* dorow = &dOTs[db * 32 + l32][0];
-                    const __bf16* qrow = &QTs[db * 32 + l32][0];
-                    const bf16x8 ado = cat4(*reinterpret_cast<const bf16x4*>(dorow + qc),
-                                            *reinterpret_cast<const bf16x4*>(dorow + qc + 8));
-                    const bf16x8 aq = cat4(*reinterpret_cast<const bf16x4*>(qrow + qc),
-                                           *reinterpret_cast<const bf16x4*>(qrow + qc + 8));
-                    dv_acc[db] = mfma32x32x16bf16(ado, pb[m], dv_acc[db]);
-                    dk_acc[db] = mfma32x32x16bf16(aq, dsb[m], dk_acc[db]);
+                    dv_acc[db] = mfma32x32x16bf16(ado[m][db], pb[m], dv_acc[db]);
+                    dk_acc[db] = mfma32x32x16bf16(aq[m][db], dsb[m], dk_acc[db]);
                 }
-            }
         } else {
             pb[0] = pb[1] = dsb[0] = dsb[1] = bf16x8{};
         }
@@ -287,12 +303,16 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
             const int qh = blk & 1;
             const int dc = blk >> 1;
             f32x4 acc;
+            bf16x8 a[BK / 32], bb[BK / 32];
 #pragma unroll
             for (int kk = 0; kk < BK / 32; ++kk) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8*>(&dSs[16 * qh + l16][32 * kk + 8 * g4]);
-                const bf16x8 bb = *reinterpret_cast<const bf16x8*>(&KTs[16 * dc + l16][32 * kk + 8 * g4]);
-                acc = mfma16x16x32bf16(a, bb, kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc);
+                a[kk] = *reinterpret_cast<const bf16x8*>(&dSs[16 * qh + l16][32 * kk + 8 * g4]);
+                bb[kk] = *reinterpret_cast<const bf16x8*>(&KTs[16 * dc + l16][32 * kk + 8 * g4]);
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kk = 0; kk < BK / 32; ++kk)
+                acc = mfma16x16x32bf16(a[kk], bb[kk], kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc);
             const uint32_t voff = (uint32_t)(((int64_t)(16 * qh + 4 * g4) * p.sacc.t + 16 * dc + l16) * 4);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
