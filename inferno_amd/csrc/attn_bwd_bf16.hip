@@ -20,7 +20,10 @@
 //                               16m + 4g + {0..3} and 16m + 8 + 4g + {0..3}
 //   dQ += dS K                  reduce over keys: dS (bf16) through LDS with
 //                               keys contiguous, K staged transposed once per
-//                               workgroup; v_mfma_f32_16x16x32_bf16 tiles
+//                               workgroup; v_mfma_f32_16x16x32_bf16 tiles.  At
+//                               D = 64 each wave's 16x16 dQ block reads the same
+//                               K^T rows for every tile: half of them are held
+//                               in VGPRs (all of them would spill)
 // Transposed staging writes dwords that pack two rows' elements, so the LDS
 // stores stay 32-bit.  Softmax statistics, P and dS are computed in fp32.
 #include <type_traits>
@@ -62,14 +65,15 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     constexpr int NDQ = 2 * (D / 16);    // 16x16 dQ blocks of a query tile, NDQ / NW per wave
     static_assert(NDQ % NW == 0, "whole dQ blocks per wave");
 
-    __shared__ __attribute__((aligned(16))) __bf16 Qs[BQ][QS];
-    __shared__ __attribute__((aligned(16))) __bf16 dOs[BQ][QS];
-    __shared__ __attribute__((aligned(16))) __bf16 QTs[D][TS];
-    __shared__ __attribute__((aligned(16))) __bf16 dOTs[D][TS];
-    __shared__ __attribute__((aligned(16))) __bf16 dSs[BQ][SS];
+    // staged query tile and dS double-buffered: one barrier per tile
+    __shared__ __attribute__((aligned(16))) __bf16 Qs2[2][BQ][QS];
+    __shared__ __attribute__((aligned(16))) __bf16 dOs2[2][BQ][QS];
+    __shared__ __attribute__((aligned(16))) __bf16 QTs2[2][D][TS];
+    __shared__ __attribute__((aligned(16))) __bf16 dOTs2[2][D][TS];
+    __shared__ __attribute__((aligned(16))) __bf16 dSs2[2][BQ][SS];
     __shared__ __attribute__((aligned(16))) __bf16 KTs[D][KTS];
-    __shared__ __attribute__((aligned(16))) float lse_s[BQ];
-    __shared__ __attribute__((aligned(16))) float dl_s[BQ];
+    __shared__ __attribute__((aligned(16))) float lse_s2[2][BQ];
+    __shared__ __attribute__((aligned(16))) float dl_s2[2][BQ];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -141,9 +145,12 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     const float c = p.c;
 
     // Q / dO staging, prefetched one query tile ahead in registers: tile q0's
-    // rows are loaded while tile q0 - BQ computes, and stored to LDS once the
-    // previous tile's S / dP / dV / dK phase is done with the staged copies
-    // (after the dS barrier), so each tile needs two barriers.
+    // rows are loaded while tile q0 - BQ computes.  The staged tile and dS are
+    // double-buffered, so each tile needs one barrier: a tile stages the next
+    // one into the buffer the previous tile read (every wave passed the
+    // previous barrier after its reads), writes its dS, and meets the others
+    // at the barrier before the dQ product reads dS.  (With single buffers and
+    // two barriers per tile the kernel measured 6% slower at config 2.)
     bf16x8 ra[QLPT], rb[QLPT];
     float r_lse = 0.f, r_dl = 0.f;
     // Loads through buffer resources over rows [q0, lim) (<= Tq): rows past
@@ -174,7 +181,13 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
         r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
         r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
     };
-    auto sstore_q = [&]() {
+    auto sstore_q = [&](int sb) {
+        __bf16(*Qs)[QS] = Qs2[sb];
+        __bf16(*dOs)[QS] = dOs2[sb];
+        __bf16(*QTs)[TS] = QTs2[sb];
+        __bf16(*dOTs)[TS] = dOTs2[sb];
+        float* lse_s = lse_s2[sb];
+        float* dl_s = dl_s2[sb];
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
             const int f = tid + NT * i;
@@ -201,15 +214,35 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     };
 
     gload_q(q_begin, p.Tq);
-    sstore_q();
+    sstore_q(0);
     __syncthreads();
+
+    // The first KR K^T operands of this wave's dQ block, the same for every
+    // query tile, held in VGPRs (KR = 4 of 8 at D = 64 fits the 256-VGPR
+    // budget of 2 waves per SIMD; 3.5% faster at config 2; K^T is staged and
+    // visible after the barrier above).
+    constexpr int KR = (NDQ / NW) == 1 && D == 64 ? 4 : 0;
+    bf16x8 ktr[KR > 0 ? KR : 1];
+#pragma unroll
+    for (int kk = 0; kk < KR; ++kk) {
+        const int dc = (wave * (NDQ / NW)) >> 1;
+        ktr[kk] = *reinterpret_cast<const bf16x8*>(&KTs[16 * dc + l16][32 * kk + 8 * g4]);
+    }
 
     // The prefetch and its store are straight-line (a row limit of 0 past the
     // last tile): conditional blocks would make the compiler wait for every
     // outstanding memory operation, the previous tile's dQ atomics included,
     // at the top of each tile.
-    for (int q0 = q_begin; q0 < q_end; q0 += BQ) {
+    int cb = 0;
+    for (int q0 = q_begin; q0 < q_end; q0 += BQ, cb ^= 1) {
         gload_q(q0 + BQ, q0 + BQ < q_end ? p.Tq : 0);
+        __bf16(*Qs)[QS] = Qs2[cb];
+        __bf16(*dOs)[QS] = dOs2[cb];
+        __bf16(*QTs)[TS] = QTs2[cb];
+        __bf16(*dOTs)[TS] = dOTs2[cb];
+        __bf16(*dSs)[SS] = dSs2[cb];
+        const float* lse_s = lse_s2[cb];
+        const float* dl_s = dl_s2[cb];
 
         const bool active = !p.causal || (q0 + BQ - 1 + p.off >= k0w);
         bf16x8 pb[2], dsb[2];
@@ -287,10 +320,10 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
         // dS block of this wave -> LDS (rows = queries, columns = the 128 keys)
 #pragma unroll
         for (int r = 0; r < 16; ++r) dSs[8 * (r >> 2) + 4 * g + (r & 3)][wave * 32 + l32] = dsb[r >> 3][r & 7];
+        // the other buffer was last read by the previous tile, before the
+        // previous barrier: stage the next tile there (zeros after the last)
+        sstore_q(cb ^ 1);
         __syncthreads();
-        // every wave is past its reads of the staged tile: stage the next one
-        // (zeros after the last tile, never read)
-        sstore_q();
 
         // ---- dQ tile (32 x D) += dS (32 x BK) K (BK x D), 16x16 blocks ---------
         // Each wave takes NDQ / NW adjacent blocks.  fp32 atomics through a
@@ -307,7 +340,7 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
 #pragma unroll
             for (int kk = 0; kk < BK / 32; ++kk) {
                 a[kk] = *reinterpret_cast<const bf16x8*>(&dSs[16 * qh + l16][32 * kk + 8 * g4]);
-                bb[kk] = *reinterpret_cast<const bf16x8*>(&KTs[16 * dc + l16][32 * kk + 8 * g4]);
+                bb[kk] = kk < KR ? ktr[kk < KR ? kk : 0] : *reinterpret_cast<const bf16x8*>(&KTs[16 * dc + l16][32 * kk + 8 * g4]);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -318,7 +351,6 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
             for (int r = 0; r < 4; ++r)
                 buffer_atomic_add(rdq, acc[r] * p.scale, voff, (uint32_t)((int64_t)r * p.sacc.t * 4));
         }
-        __syncthreads();
     }
 
     if (!bwd_fixup<NT>(p, wk, dk_acc, dv_acc)) return;
