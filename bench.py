@@ -31,6 +31,16 @@ MFMA_FP32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix
 HBM_PEAK_GBS = 8000.0
 
+# HBM bytes per launch (read + written) of the backward call's kernels at config 2, from
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script, scaled by what the same
+# counters read for a plain device copy (FETCH_SIZE x2.00, WRITE_SIZE x1.00).  fp32 bwd_main
+# runs the split plan (partial dK / dV written and read back); the bf16 call adds the dQ
+# conversion pass.
+BWD_TRAFFIC = {
+    "f32": {"bwd_pre": 50.40e6 + 25.56e6, "bwd_main": 202.27e6 + 201.35e6},
+    "bf16": {"bwd_pre": 25.23e6 + 25.56e6, "bwd_main": 56.20e6 + 88.08e6, "bwd_cvt": 25.22e6 + 12.58e6},
+}
+
 METRIC = "causal attn fwd+bwd TFLOP/s (B8 H12 T1024 D64 fp32) + % of MFMA peak"
 
 
@@ -281,15 +291,15 @@ def main():
         "timings": {"fwd": pct(fwd_all), "bwd": pct(bwd_all), "fwd+bwd": pct(step_all)},
         "roofline": {
             "bound": "mfma",
-            "kernel": "bwd (bwd_pre + bwd_main; bwd_main dominates)",
+            "kernel": "bwd: " + " + ".join(BWD_TRAFFIC[args.dtype]) + " (one inf_attn_bwd call; bwd_main dominates)",
             "achieved": round(bwd_tf, 3),
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(bwd_tf / peak, 4),
-            # HBM bytes per bwd_main launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-            # (x2.00 / x1.00 copy-kernel calibration): 202.2 MB read + 201.3 MB written
-            # (with the split plan's partial dK / dV stores and reads).
-            "traffic": 403.5e6,
+            # HBM bytes of the timed backward call's kernels, measured at this config by
+            # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (x2.00 / x1.00 copy-kernel calibration)
+            "traffic": round(sum(BWD_TRAFFIC[args.dtype].values()), -5),
+            "traffic_by_kernel": BWD_TRAFFIC[args.dtype],
             "algorithmic_flop_per_launch": F_bwd,
             "avg_launch_ms": round(bwd_ms, 4),
         },
