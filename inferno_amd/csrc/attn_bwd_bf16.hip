@@ -1,9 +1,11 @@
 // attn_bwd_bf16.hip -- fused causal attention backward, bf16 inputs, fp32
 // accumulation, on gfx950 bf16 MFMAs.
 //
-// Same ownership as the fp32 kernel (attn_bwd.hip), with 8 waves x 32 keys
-// = 256 keys per workgroup at D <= 64 (the fp32 kernel and D = 128: 4 x 32): K and V operands and the
-// dK^T / dV^T accumulators in VGPRs for the whole kernel (atomic-free dK, dV),
+// Same ownership as the fp32 kernel (attn_bwd.hip): each wave owns a run of
+// keys, with 8 waves x 32 keys = 256 keys per workgroup at D = 64 (4 x 32 at
+// D = 32; D = 128 has its own kernel below, 8 waves x 16 keys): K and V
+// operands and the dK^T / dV^T accumulators in VGPRs for the whole kernel
+// (atomic-free dK, dV),
 // query tiles of 32 rows, dQ through LDS and fp32 atomics into the
 // accumulator.  At bf16 speed the dQ atomics are a device-wide throughput
 // limit (at config 2 the kernel measured 23% faster with them left out);
@@ -34,15 +36,10 @@
 
 namespace inf {
 
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x4 mfma16x16x32bf16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ bf16x8 cat4(bf16x4 lo, bf16x4 hi) {
-    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 template <int D>
@@ -55,13 +52,11 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     constexpr int NDB = D / 32;          // 32-wide d blocks of dK^T / dV^T
     constexpr int C8 = D / 8;            // 8-element chunks per row
     constexpr int QS = D + 8;            // row-major Q / dO stride (bf16)
-    // Transposed Q / dO: at D <= 64 each row stores the queries in the order
-    // the dV / dK MFMAs take them (a lane's 8 queries 16m + 4g + {0..3} and
-    // 16m + 8 + 4g + {0..3} contiguous at 16m + 8g), so an operand is one
-    // 16-byte read instead of two 8-byte ones (1.5-2% at D = 32 and 64; 1%
-    // slower at D = 128, which keeps the plain order).
-    constexpr bool QPERM = D <= 64;
-    constexpr int TS = QPERM ? BQ + 8 : BQ + 4;  // row stride (bf16): 20 dwords keep the 16-byte reads conflict-free
+    // Transposed Q / dO: each row stores the queries in the order the dV / dK
+    // MFMAs take them (a lane's 8 queries 16m + 4g + {0..3} and 16m + 8 + 4g +
+    // {0..3} contiguous at 16m + 8g), so an operand is one 16-byte read
+    // instead of two 8-byte ones (1.5-2% faster at D = 32 and 64).
+    constexpr int TS = BQ + 8;           // row stride (bf16): 20 dwords keep the 16-byte reads conflict-free
     constexpr int SS = BK + 8;           // dS stride (bf16)
     constexpr int KTS = BK + 8;          // K^T stride (bf16)
     constexpr int QTASK = (BQ / 2) * C8;                 // (row pair, chunk) tasks per tensor
@@ -70,6 +65,7 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     constexpr int KLPT = (KTASK + NT - 1) / NT;
     constexpr int NDQ = 2 * (D / 16);    // 16x16 dQ blocks of a query tile, NDQ / NW per wave
     static_assert(NDQ % NW == 0, "whole dQ blocks per wave");
+    static_assert(D <= 64, "D = 128 runs bwd_main_bf16_w16_kernel");
 
     // staged query tile and dS double-buffered: one barrier per tile
     __shared__ __attribute__((aligned(16))) __bf16 Qs2[2][BQ][QS];
@@ -210,9 +206,9 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
                 bf16x2 pr;
                 pr[0] = ra[i][e];
                 pr[1] = rb[i][e];
-                // query q = 16m + 8h + 4g + c at 16m + 8g + 4h + c when permuted
+                // query q = 16m + 8h + 4g + c at 16m + 8g + 4h + c
                 const int q = 2 * qp;
-                const int pos = QPERM ? (q & 16) | ((q & 4) << 1) | ((q & 8) >> 1) | (q & 3) : q;
+                const int pos = (q & 16) | ((q & 4) << 1) | ((q & 8) >> 1) | (q & 3);
                 *reinterpret_cast<bf16x2*>(&cols[8 * c8 + e][pos]) = pr;
             }
         }
@@ -276,20 +272,10 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
             bf16x8 ado[2][NDB], aq[2][NDB];
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
-                const int qc = 16 * m + 4 * g;
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) {
-                    const __bf16* dorow = &dOTs[db * 32 + l32][0];
-                    const __bf16* qrow = &QTs[db * 32 + l32][0];
-                    if constexpr (QPERM) {
-                        ado[m][db] = *reinterpret_cast<const bf16x8*>(dorow + 16 * m + 8 * g);
-                        aq[m][db] = *reinterpret_cast<const bf16x8*>(qrow + 16 * m + 8 * g);
-                    } else {
-                        ado[m][db] = cat4(*reinterpret_cast<const bf16x4*>(dorow + qc),
-                                          *reinterpret_cast<const bf16x4*>(dorow + qc + 8));
-                        aq[m][db] = cat4(*reinterpret_cast<const bf16x4*>(qrow + qc),
-                                         *reinterpret_cast<const bf16x4*>(qrow + qc + 8));
-                    }
+                    ado[m][db] = *reinterpret_cast<const bf16x8*>(&dOTs[db * 32 + l32][16 * m + 8 * g]);
+                    aq[m][db] = *reinterpret_cast<const bf16x8*>(&QTs[db * 32 + l32][16 * m + 8 * g]);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -387,11 +373,307 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     }
 }
 
+// D = 128: 8 waves x 16 keys (128 keys per workgroup) on v_mfma_f32_16x16x32_bf16,
+// two waves per SIMD (216 VGPRs).  (32 keys per wave on 32x32 MFMAs needs
+// ~470 registers per wave at D = 128: one wave per SIMD; against that layout
+// this one measured 11-28% faster at T <= 2048 and 2% at config 4, whose
+// 64 key blocks per head make the dQ atomics the limit: 39% faster there
+// with the atomics left out.)  Per wave: K / V operands of its 16
+// keys and the dK^T / dV^T accumulators (8 blocks of 16 d x 16 keys each) in
+// VGPRs.  A 16x16x32 MFMA reduces 32 elements, each lane (row or column l16,
+// group g4) supplying 8 consecutive ones:
+//   S = Q K^T, dP = dO V^T   (per 16-query half): A = Q rows from LDS, B = K
+//                            rows of the wave's keys (registers); output lane
+//                            = key l16, registers r = queries 4 g4 + r
+//   dV^T += dO^T P, dK^T += Q^T dS: B = P / dS straight from the S / dP
+//                            outputs (a lane's 8 queries 4 g4 + {0..3} and
+//                            16 + 4 g4 + {0..3}); A = dO^T / Q^T rows staged
+//                            with the queries in that order (16-byte reads)
+//   dQ += dS K               dS through LDS (keys contiguous), K^T staged once;
+//                            each wave one 16-query half x two 16-wide d blocks
+template <int D>
+__global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) {
+    static_assert(D == 128, "16-key waves are the D = 128 kernel");
+    constexpr int NW = 8;
+    constexpr int NT = 64 * NW;
+    constexpr int BQ = kBwdBQ;           // 32
+    constexpr int KW = 16;               // keys per wave
+    constexpr int BK = KW * NW;          // 128 keys per workgroup
+    constexpr int NKC = D / 32;          // 32-wide d chunks: reduction steps of S / dP
+    constexpr int NDB = D / 16;          // 16-row d blocks of dK^T / dV^T
+    constexpr int C8 = D / 8;
+    constexpr int QS = D + 8;            // row-major Q / dO stride (bf16)
+    constexpr int TS = BQ + 8;           // transposed Q / dO stride (bf16)
+    constexpr int SS = BK + 8;           // dS stride
+    constexpr int KTS = BK + 8;          // K^T stride
+    constexpr int QTASK = (BQ / 2) * C8; // 256: Q tasks on threads 0..255, dO on 256..511
+    constexpr int KTASK = (BK / 2) * C8;
+    constexpr int KLPT = (KTASK + NT - 1) / NT;
+    static_assert(2 * QTASK == NT, "one Q / dO staging task per thread");
+
+    __shared__ __attribute__((aligned(16))) __bf16 Qs2[2][BQ][QS];
+    __shared__ __attribute__((aligned(16))) __bf16 dOs2[2][BQ][QS];
+    __shared__ __attribute__((aligned(16))) __bf16 QTs2[2][D][TS];
+    __shared__ __attribute__((aligned(16))) __bf16 dOTs2[2][D][TS];
+    __shared__ __attribute__((aligned(16))) __bf16 dSs2[2][BQ][SS];
+    __shared__ __attribute__((aligned(16))) __bf16 KTs[D][KTS];
+    __shared__ __attribute__((aligned(16))) float lse_s2[2][BQ];
+    __shared__ __attribute__((aligned(16))) float dl_s2[2][BQ];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l16 = lane & 15;
+    const int g4 = lane >> 4;
+
+    const BwdWork wk = bwd_work<BK>(p);
+    if (wk.bh >= p.B * p.H) return;  // padding workgroup of a split plan's grid
+    const int kblk = wk.kblk;
+    const int bh = wk.bh;
+    const int b = bh / p.H;
+    const int h = bh % p.H;
+
+    const __bf16* Q = (const __bf16*)p.q + b * p.sq.b + h * p.sq.h;
+    const __bf16* K = (const __bf16*)p.k + b * p.sk.b + h * p.sk.h;
+    const __bf16* V = (const __bf16*)p.v + b * p.sv.b + h * p.sv.h;
+    const __bf16* dO = (const __bf16*)p.dout + b * p.sdo.b + h * p.sdo.h;
+    float* dQa = p.dq_acc + b * p.sacc.b + h * p.sacc.h;
+    const float* LSE = p.lse + (int64_t)bh * p.Tq;
+    const float* DL = p.delta + (int64_t)bh * p.Tq;
+
+    const int k0 = kblk * BK;
+    const int k0w = k0 + wave * KW;
+    const int key = k0w + l16;
+
+    // K / V operands: chunk kk takes row `key`, columns 32 kk + 8 g4 .. +7.
+    bf16x8 kf[NKC], vf[NKC];
+#pragma unroll
+    for (int kk = 0; kk < NKC; ++kk) {
+        if (key < p.Tk) {
+            kf[kk] = *reinterpret_cast<const bf16x8*>(K + (int64_t)key * p.sk.t + 32 * kk + 8 * g4);
+            vf[kk] = *reinterpret_cast<const bf16x8*>(V + (int64_t)key * p.sv.t + 32 * kk + 8 * g4);
+        } else {
+            kf[kk] = vf[kk] = bf16x8{};
+        }
+    }
+
+    // K^T of the key block (keys contiguous per d row), for dQ.
+#pragma unroll
+    for (int i = 0; i < KLPT; ++i) {
+        const int f = tid + NT * i;
+        if (f >= KTASK) continue;
+        const int kp = f % (BK / 2), c8 = f / (BK / 2);
+        const int r0 = k0 + 2 * kp;
+        const bf16x8 a = r0 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)r0 * p.sk.t + 8 * c8) : bf16x8{};
+        const bf16x8 c = r0 + 1 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)(r0 + 1) * p.sk.t + 8 * c8)
+                                       : bf16x8{};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            bf16x2 pr;
+            pr[0] = a[e];
+            pr[1] = c[e];
+            *reinterpret_cast<bf16x2*>(&KTs[8 * c8 + e][2 * kp]) = pr;
+        }
+    }
+
+    f32x4 dv_acc[NDB], dk_acc[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) {
+        dv_acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dk_acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const int q_begin = wk.q_begin;
+    const int q_end = wk.q_end;
+    const float c = p.c;
+
+    // Q / dO staging as in bwd_main_bf16_kernel (prefetched one tile ahead,
+    // double-buffered with dS, one barrier per tile); the transposed copies
+    // put query q = 16 h + 4 g + c at 8 g + 4 h + c.
+    bf16x8 ra, rb;
+    float r_lse = 0.f, r_dl = 0.f;
+    const int which = tid / QTASK;          // 0: Q, 1: dO (wave-uniform)
+    const int rem = tid % QTASK;
+    const int qp = rem % (BQ / 2), c8q = rem / (BQ / 2);
+    auto gload_q = [&](int q0, int lim) {
+        const int rows = min(lim - q0, BQ);
+        const int64_t st = which ? p.sdo.t : p.sq.t;
+        const auto rs = row_rsrc(which ? dO : Q, st, q0, rows, D);
+        const uint32_t voff = (uint32_t)(((int64_t)(2 * qp) * st + 8 * c8q) * 2);
+        ra = buffer_ld8bf(rs, voff, 0);
+        rb = buffer_ld8bf(rs, voff, (uint32_t)(st * 2));
+        r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
+        r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
+    };
+    auto sstore_q = [&](int sb) {
+        __bf16(*rows)[QS] = which ? dOs2[sb] : Qs2[sb];
+        __bf16(*cols)[TS] = which ? dOTs2[sb] : QTs2[sb];
+        *reinterpret_cast<bf16x8*>(&rows[2 * qp][8 * c8q]) = ra;
+        *reinterpret_cast<bf16x8*>(&rows[2 * qp + 1][8 * c8q]) = rb;
+        const int q = 2 * qp;
+        const int pos = 8 * ((q >> 2) & 3) + 4 * (q >> 4) + (q & 3);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            bf16x2 pr;
+            pr[0] = ra[e];
+            pr[1] = rb[e];
+            *reinterpret_cast<bf16x2*>(&cols[8 * c8q + e][pos]) = pr;
+        }
+        if (tid < BQ) {
+            lse_s2[sb][tid] = r_lse * kLog2e;  // LSE in base 2
+            dl_s2[sb][tid] = r_dl;
+        }
+    };
+
+    gload_q(q_begin, p.Tq);
+    sstore_q(0);
+    __syncthreads();
+
+    // dQ blocks of this wave: query half qhw, d blocks 2 dcw and 2 dcw + 1
+    const int qhw = wave & 1;
+    const int dcw = wave >> 1;
+
+    int cb = 0;
+    for (int q0 = q_begin; q0 < q_end; q0 += BQ, cb ^= 1) {
+        gload_q(q0 + BQ, q0 + BQ < q_end ? p.Tq : 0);
+        __bf16(*Qs)[QS] = Qs2[cb];
+        __bf16(*dOs)[QS] = dOs2[cb];
+        __bf16(*QTs)[TS] = QTs2[cb];
+        __bf16(*dOTs)[TS] = dOTs2[cb];
+        __bf16(*dSs)[SS] = dSs2[cb];
+        const float* lse_s = lse_s2[cb];
+        const float* dl_s = dl_s2[cb];
+
+        const bool active = !p.causal || (q0 + BQ - 1 + p.off >= k0w);
+        bf16x8 pb, dsb;
+        if (active && k0w < p.Tk) {
+            f32x4 s[2], dp[2];
+            bf16x8 qa[2][NKC], da[2][NKC];
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                for (int kk = 0; kk < NKC; ++kk) {
+                    qa[qh][kk] = *reinterpret_cast<const bf16x8*>(&Qs[16 * qh + l16][32 * kk + 8 * g4]);
+                    da[qh][kk] = *reinterpret_cast<const bf16x8*>(&dOs[16 * qh + l16][32 * kk + 8 * g4]);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kk = 0; kk < NKC; ++kk)
+#pragma unroll
+                for (int qh = 0; qh < 2; ++qh) {
+                    s[qh] = mfma16x16x32bf16(qa[qh][kk], kf[kk], kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[qh]);
+                    dp[qh] = mfma16x16x32bf16(da[qh][kk], vf[kk], kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dp[qh]);
+                }
+            // P and dS: register r of half qh is query 16 qh + 4 g4 + r
+            const f32x4 L0 = *reinterpret_cast<const f32x4*>(&lse_s[4 * g4]);
+            const f32x4 L1 = *reinterpret_cast<const f32x4*>(&lse_s[16 + 4 * g4]);
+            const f32x4 D0 = *reinterpret_cast<const f32x4*>(&dl_s[4 * g4]);
+            const f32x4 D1 = *reinterpret_cast<const f32x4*>(&dl_s[16 + 4 * g4]);
+            auto p_ds = [&](auto masked) {
+#pragma unroll
+                for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float Lq = qh ? L1[r] : L0[r];
+                        const float Dq = qh ? D1[r] : D0[r];
+                        float pr = fast_exp2(fmaf(s[qh][r], c, -Lq));
+                        if constexpr (decltype(masked)::value) {
+                            const int qi = q0 + 16 * qh + 4 * g4 + r;
+                            const bool vis = (qi < p.Tq) && (key < p.Tk) && (!p.causal || key <= qi + p.off);
+                            pr = vis ? pr : 0.f;
+                        }
+                        pb[4 * qh + r] = (__bf16)pr;
+                        dsb[4 * qh + r] = (__bf16)(pr * (dp[qh][r] - Dq));
+                    }
+            };
+            const bool need_mask = q0 + BQ > p.Tq || k0w + KW > p.Tk || (p.causal && k0w + KW - 1 > q0 + p.off);
+            if (need_mask)
+                p_ds(std::true_type{});
+            else
+                p_ds(std::false_type{});
+            // dV^T += dO^T P ; dK^T += Q^T dS over the 32 queries (one MFMA per d block)
+            bf16x8 ado[NDB], aq[NDB];
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                ado[db] = *reinterpret_cast<const bf16x8*>(&dOTs[16 * db + l16][8 * g4]);
+                aq[db] = *reinterpret_cast<const bf16x8*>(&QTs[16 * db + l16][8 * g4]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                dv_acc[db] = mfma16x16x32bf16(ado[db], pb, dv_acc[db]);
+                dk_acc[db] = mfma16x16x32bf16(aq[db], dsb, dk_acc[db]);
+            }
+        } else {
+            pb = dsb = bf16x8{};
+        }
+        // dS of this wave -> LDS (rows = queries, columns = the block's keys)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) dSs[16 * (r >> 2) + 4 * g4 + (r & 3)][wave * KW + l16] = dsb[r];
+        sstore_q(cb ^ 1);
+        __syncthreads();
+
+        // ---- dQ (32 x D) += dS (32 x BK) K (BK x D): this wave's two 16x16 blocks
+        const auto rdq = row_rsrc(dQa, p.sacc.t, q0, min(p.Tq - q0, BQ), D);
+        f32x4 acc0, acc1;
+        bf16x8 a[BK / 32], b0[BK / 32], b1[BK / 32];
+#pragma unroll
+        for (int kk = 0; kk < BK / 32; ++kk) {
+            a[kk] = *reinterpret_cast<const bf16x8*>(&dSs[16 * qhw + l16][32 * kk + 8 * g4]);
+            b0[kk] = *reinterpret_cast<const bf16x8*>(&KTs[32 * dcw + l16][32 * kk + 8 * g4]);
+            b1[kk] = *reinterpret_cast<const bf16x8*>(&KTs[32 * dcw + 16 + l16][32 * kk + 8 * g4]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kk = 0; kk < BK / 32; ++kk) {
+            acc0 = mfma16x16x32bf16(a[kk], b0[kk], kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc0);
+            acc1 = mfma16x16x32bf16(a[kk], b1[kk], kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc1);
+        }
+        const uint32_t voff = (uint32_t)(((int64_t)(16 * qhw + 4 * g4) * p.sacc.t + 32 * dcw + l16) * 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            buffer_atomic_add(rdq, acc0[r] * p.scale, voff, (uint32_t)((int64_t)r * p.sacc.t * 4));
+            buffer_atomic_add(rdq, acc1[r] * p.scale, voff + 64, (uint32_t)((int64_t)r * p.sacc.t * 4));
+        }
+    }
+
+    // split plans: the fix-up takes the accumulators as two f32x16 each
+    f32x16 dk16[NDB / 4], dv16[NDB / 4];
+#pragma unroll
+    for (int i = 0; i < NDB / 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                dk16[i][4 * j + r] = dk_acc[4 * i + j][r];
+                dv16[i][4 * j + r] = dv_acc[4 * i + j][r];
+            }
+    if (!bwd_fixup<NT>(p, wk, dk16, dv16)) return;
+    if (key < p.Tk) {
+        uint16_t* dKp = (uint16_t*)p.dk + b * p.sdk.b + h * p.sdk.h + (int64_t)key * p.sdk.t;
+        uint16_t* dVp = (uint16_t*)p.dv + b * p.sdv.b + h * p.sdv.h + (int64_t)key * p.sdv.t;
+#pragma unroll
+        for (int i = 0; i < NDB / 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int db = 4 * i + j;
+                f32x4 a, v;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    a[r] = dk16[i][4 * j + r] * p.scale;
+                    v[r] = dv16[i][4 * j + r];
+                }
+                st4(dKp + 16 * db + 4 * g4, a);
+                st4(dVp + 16 * db + 4 * g4, v);
+            }
+    }
+}
+
 int bwd_main_bf16_occupancy(int D, int* blocks_per_cu) {
     switch (D) {
         case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<32>, 64 * bwd_bf16_waves(32), 0);
         case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<64>, 64 * bwd_bf16_waves(64), 0);
-        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<128>, 64 * bwd_bf16_waves(128), 0);
+        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_w16_kernel<128>, 512, 0);
         default: return (int)hipErrorInvalidValue;
     }
 }
@@ -401,7 +683,7 @@ int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s) {
     switch (p.D) {
         case 32: hipLaunchKernelGGL((bwd_main_bf16_kernel<32>), grid, dim3(64 * bwd_bf16_waves(32)), 0, s, p); break;
         case 64: hipLaunchKernelGGL((bwd_main_bf16_kernel<64>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p); break;
-        case 128: hipLaunchKernelGGL((bwd_main_bf16_kernel<128>), grid, dim3(64 * bwd_bf16_waves(128)), 0, s, p); break;
+        case 128: hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128>), grid, dim3(512), 0, s, p); break;
         default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();

@@ -293,12 +293,13 @@ constexpr int kFwdBf16BN = 64;   // keys per K/V tile of the bf16 forward (every
 // keys, half the dQ atomics per key (two waves per SIMD, as with two 4-wave
 // workgroups); at bf16 speed the atomics are a device-wide limit.  fp32 keeps
 // 4 waves (its atomics cost ~2.5%, and 256-key blocks measured 5-10% slower
-// under a causal mask: fewer, heavier workgroups).  D = 128 needs ~430
-// registers per wave (one wave per SIMD) and D = 32 keeps three 4-wave
-// workgroups per CU: both use 4 waves.
+// under a causal mask: fewer, heavier workgroups).  fp32 at D = 128 needs
+// ~430 registers per wave (one wave per SIMD) and D = 32 keeps three 4-wave
+// workgroups per CU: both use 4 waves.  bf16 at D = 128 runs its own kernel,
+// 8 waves x 16 keys: 128 keys per workgroup, as with 4 x 32.
 constexpr int bwd_waves(int bf16, int D) { return bf16 && D == 64 ? 8 : 4; }
 constexpr int bwd_bf16_waves(int D) { return bwd_waves(1, D); }
-inline int bwd_keys_per_wg(int bf16, int D) { return 32 * bwd_waves(bf16, D); }
+inline int bwd_keys_per_wg(int bf16, int D) { return bf16 && D == 128 ? 128 : 32 * bwd_waves(bf16, D); }
 constexpr int kBwdBQ = 32;       // query rows per backward inner step
 
 }  // namespace inf
