@@ -59,8 +59,9 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdParams p) {
         const f32x4 o4 = ld4((const E*)p.o + b * p.so.b + h * p.so.h + i * p.so.t + 4 * c4);
         const f32x4 d4 = ld4((const E*)p.dout + b * p.sdo.b + h * p.sdo.h + i * p.sdo.t + 4 * c4);
         s = o4[0] * d4[0] + o4[1] * d4[1] + o4[2] * d4[2] + o4[3] * d4[3];
-        *reinterpret_cast<f32x4*>(p.dq_acc + b * p.sacc.b + h * p.sacc.h + i * p.sacc.t + 4 * c4) =
-            f32x4{0.f, 0.f, 0.f, 0.f};
+        if (!p.dq_direct)
+            *reinterpret_cast<f32x4*>(p.dq_acc + b * p.sacc.b + h * p.sacc.h + i * p.sacc.t + 4 * c4) =
+                f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int m = TPR / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
@@ -577,7 +578,12 @@ static int launch_bwd_t(const BwdParams& p, hipStream_t s) {
     if constexpr (sizeof(E) == 2) {
         const int e = launch_bwd_main_bf16(p, s);
         if (e) return e;
-        hipLaunchKernelGGL((bwd_cvt_kernel<D>), pre_grid, dim3(256), 0, s, p);
+        if (p.dq_direct) {
+            const int e2 = launch_bwd_dq_bf16(p, s);
+            if (e2) return e2;
+        } else {
+            hipLaunchKernelGGL((bwd_cvt_kernel<D>), pre_grid, dim3(256), 0, s, p);
+        }
     } else {
         const dim3 grid((unsigned)(p.n_groups ? p.n_groups * bwd_padded_heads(p.B * p.H) : p.n_kblocks * p.B * p.H));
         hipLaunchKernelGGL((bwd_main_kernel<D, E>), grid, dim3(64 * bwd_waves(0, D)), 0, s, p);

@@ -318,8 +318,10 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
             pb[0] = pb[1] = dsb[0] = dsb[1] = bf16x8{};
         }
         // dS block of this wave -> LDS (rows = queries, columns = the 128 keys)
+        if (!p.dq_direct) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dSs[8 * (r >> 2) + 4 * g + (r & 3)][wave * 32 + l32] = dsb[r >> 3][r & 7];
+            for (int r = 0; r < 16; ++r) dSs[8 * (r >> 2) + 4 * g + (r & 3)][wave * 32 + l32] = dsb[r >> 3][r & 7];
+        }
         // the other buffer was last read by the previous tile, before the
         // previous barrier: stage the next tile there (zeros after the last)
         sstore_q(cb ^ 1);
@@ -329,6 +331,7 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
         // Each wave takes NDQ / NW adjacent blocks.  fp32 atomics through a
         // buffer resource over the tile's rows: rows past Tq fall outside it
         // and the hardware drops those adds.
+        if (p.dq_direct) continue;
         const auto rdq = row_rsrc(dQa, p.sacc.t, q0, min(p.Tq - q0, BQ), D);
 #pragma unroll
         for (int bi = 0; bi < NDQ / NW; ++bi) {
@@ -608,12 +611,15 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
             pb = dsb = bf16x8{};
         }
         // dS of this wave -> LDS (rows = queries, columns = the block's keys)
+        if (!p.dq_direct) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) dSs[16 * (r >> 2) + 4 * g4 + (r & 3)][wave * KW + l16] = dsb[r];
+            for (int r = 0; r < 8; ++r) dSs[16 * (r >> 2) + 4 * g4 + (r & 3)][wave * KW + l16] = dsb[r];
+        }
         sstore_q(cb ^ 1);
         __syncthreads();
 
         // ---- dQ (32 x D) += dS (32 x BK) K (BK x D): this wave's two 16x16 blocks
+        if (p.dq_direct) continue;
         const auto rdq = row_rsrc(dQa, p.sacc.t, q0, min(p.Tq - q0, BQ), D);
         f32x4 acc0, acc1;
         bf16x8 a[BK / 32], b0[BK / 32], b1[BK / 32];
@@ -667,6 +673,213 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
                 st4(dVp + 16 * db + 4 * g4, v);
             }
     }
+}
+
+
+// ---- query-major dQ pass (bf16, long key ranges) ---------------------------
+//
+// 4 waves x 32 query rows per workgroup (heaviest query tiles first), key
+// tiles of BN keys streamed through LDS as K rows, V rows and K^T (keys of each
+// 32-key block in the MFMA operand order 16m + 8g + 4h + c for key
+// 16m + 8h + 4g + c); Q and dO rows of the wave's queries in VGPRs, LSE and
+// delta one value per lane.  Per tile, with queries on the lane axis:
+//   S^T = K Q^T, dP^T = V dO^T, P^T = exp2(S^T c - L), dS^T = P^T (dP^T - delta)
+//   dQ^T += K^T dS^T (dS^T straight from registers, as the forward's P^T)
+// dQ accumulates in fp32 VGPRs and is written once (bf16, times the scale):
+// no accumulator, no atomics, no conversion pass, and the same sum order on
+// every run.  It recomputes S and dP (two more products per score than the
+// atomic path's dQ), so it pays only where the atomics bound the fused
+// kernel (bwd_dq_direct): at D = 128 with many key blocks.  (At D = 64 it
+// measured 28% slower than the atomics at B1 H16 T8192.)
+template <int D>
+__global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
+    constexpr int BM = kBwdDqBM;
+    constexpr int BN = D >= 128 ? 32 : 64;
+    constexpr int KS = D + 8;            // K / V row stride (bf16)
+    constexpr int TS = BN + 8;           // K^T row stride (bf16)
+    constexpr int NKK = D / 16;
+    constexpr int NKB = BN / 32;
+    constexpr int NDB = D / 32;
+    constexpr int C8 = D / 8;
+    constexpr int KTASK = (BN / 2) * C8;  // (key pair, chunk) tasks
+    constexpr int KLPT = (KTASK + 255) / 256;
+    constexpr int VLPT = BN * C8 / 256;
+    static_assert(BN * C8 % 256 == 0 && KTASK % 256 == 0, "whole staging passes");
+
+    __shared__ __attribute__((aligned(16))) __bf16 Ks[2][BN][KS];
+    __shared__ __attribute__((aligned(16))) __bf16 Vs[2][BN][KS];
+    __shared__ __attribute__((aligned(16))) __bf16 KTs[2][D][TS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+
+    const int BH = p.B * p.H;
+    const int w = blockIdx.x;
+    const int qtile = p.n_qtiles - 1 - w / BH;
+    const int bh = w % BH;
+    const int b = bh / p.H;
+    const int h = bh % p.H;
+
+    const __bf16* Q = (const __bf16*)p.q + b * p.sq.b + h * p.sq.h;
+    const __bf16* K = (const __bf16*)p.k + b * p.sk.b + h * p.sk.h;
+    const __bf16* V = (const __bf16*)p.v + b * p.sv.b + h * p.sv.h;
+    const __bf16* dO = (const __bf16*)p.dout + b * p.sdo.b + h * p.sdo.h;
+
+    const int q0w = qtile * BM + wave * 32;
+    const int qrow = q0w + l32;
+    bf16x8 qf[NKK], df[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+        if (qrow < p.Tq) {
+            qf[kk] = *reinterpret_cast<const bf16x8*>(Q + (int64_t)qrow * p.sq.t + 16 * kk + 8 * g);
+            df[kk] = *reinterpret_cast<const bf16x8*>(dO + (int64_t)qrow * p.sdo.t + 16 * kk + 8 * g);
+        } else {
+            qf[kk] = df[kk] = bf16x8{};
+        }
+    }
+    const float Lq = qrow < p.Tq ? p.lse[(int64_t)bh * p.Tq + qrow] * kLog2e : 0.f;
+    const float Dq = qrow < p.Tq ? p.delta[(int64_t)bh * p.Tq + qrow] : 0.f;
+
+    int kv_end = p.Tk;
+    if (p.causal) kv_end = min(p.Tk, qtile * BM + BM + p.off);
+    const int nt = (kv_end + BN - 1) / BN;
+    const int wave_kend = p.causal ? min(kv_end, q0w + 32 + p.off) : kv_end;
+
+    const int64_t kstep = (int64_t)BN * p.sk.t, vstep = (int64_t)BN * p.sv.t;
+    const __bf16* kt = K;
+    const __bf16* vt = V;
+    bf16x8 ka[KLPT], kb2[KLPT], vr[VLPT];
+    const int kp = tid % (BN / 2), kc8 = tid / (BN / 2);
+    const uint32_t k_voff = (uint32_t)(((int64_t)(2 * kp) * p.sk.t + 8 * kc8) * 2);
+    const uint32_t v_voff = (uint32_t)(((int64_t)(tid / C8) * p.sv.t + 8 * (tid % C8)) * 2);
+    auto gload = [&](int rows) {
+        const auto rk = row_rsrc(kt, p.sk.t, 0, rows, D);
+        const auto rv = row_rsrc(vt, p.sv.t, 0, rows, D);
+#pragma unroll
+        for (int i = 0; i < KLPT; ++i) {
+            const uint32_t col = (uint32_t)(8 * (256 * i / (BN / 2)) * 2);
+            ka[i] = buffer_ld8bf(rk, k_voff, col);
+            kb2[i] = buffer_ld8bf(rk, k_voff, col + (uint32_t)(p.sk.t * 2));
+        }
+#pragma unroll
+        for (int i = 0; i < VLPT; ++i)
+            vr[i] = buffer_ld8bf(rv, v_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sv.t * 2));
+    };
+    auto sstore = [&](int buf) {
+        const int k = 2 * kp;
+        const int pos = (k & ~15) | ((k & 4) << 1) | ((k & 8) >> 1) | (k & 3);
+#pragma unroll
+        for (int i = 0; i < KLPT; ++i) {
+            const int c8 = kc8 + 256 * i / (BN / 2);
+            *reinterpret_cast<bf16x8*>(&Ks[buf][k][8 * c8]) = ka[i];
+            *reinterpret_cast<bf16x8*>(&Ks[buf][k + 1][8 * c8]) = kb2[i];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                bf16x2 pr;
+                pr[0] = ka[i][e];
+                pr[1] = kb2[i][e];
+                *reinterpret_cast<bf16x2*>(&KTs[buf][8 * c8 + e][pos]) = pr;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VLPT; ++i) {
+            const int f = tid + 256 * i;
+            *reinterpret_cast<bf16x8*>(&Vs[buf][f / C8][8 * (f % C8)]) = vr[i];
+        }
+    };
+    auto rows_of = [&](int u) { return u < nt ? min(p.Tk - u * BN, BN) : 0; };
+
+    f32x16 dq[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) dq[i] = f32x16{};
+    const float c = p.c;
+
+    gload(rows_of(0));
+    sstore(0);
+    __syncthreads();
+    for (int u = 0; u < nt; ++u) {
+        const int buf = u & 1;
+        const int k0 = u * BN;
+        kt += kstep;
+        vt += vstep;
+        gload(rows_of(u + 1));
+        if (k0 < wave_kend) {
+            f32x16 s[NKB], dp[NKB];
+            bf16x8 ak[NKK][NKB], av[NKK][NKB];
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) {
+                    ak[kk][kb] = *reinterpret_cast<const bf16x8*>(&Ks[buf][kb * 32 + l32][16 * kk + 8 * g]);
+                    av[kk][kb] = *reinterpret_cast<const bf16x8*>(&Vs[buf][kb * 32 + l32][16 * kk + 8 * g]);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) {
+                    s[kb] = mfma32x32x16bf16(ak[kk][kb], qf[kk], kk == 0 ? f32x16{} : s[kb]);
+                    dp[kb] = mfma32x32x16bf16(av[kk][kb], df[kk], kk == 0 ? f32x16{} : dp[kb]);
+                }
+            // register r of block kb: key k0 + kb*32 + 8 (r / 4) + 4 g + r % 4, query qrow
+            const bool need_mask = (k0 + BN > p.Tk) || (qtile * BM + BM > p.Tq) || (p.causal && (k0 + BN - 1 > q0w + p.off));
+            const int lim = p.causal ? min(p.Tk - 1, qrow + p.off) : p.Tk - 1;
+            bf16x8 dsb[NKB][2];
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float pr = fast_exp2(fmaf(s[kb][r], c, -Lq));
+                    if (need_mask) {
+                        const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                        pr = (key <= lim && qrow < p.Tq) ? pr : 0.f;
+                    }
+                    dsb[kb][r >> 3][r & 7] = (__bf16)(pr * (dp[kb][r] - Dq));
+                }
+            // dQ^T[d][q] += K^T[d][keys] dS^T[keys][q]
+            bf16x8 akt[NDB][NKB][2];
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                    for (int m = 0; m < 2; ++m)
+                        akt[db][kb][m] = *reinterpret_cast<const bf16x8*>(&KTs[buf][db * 32 + l32][kb * 32 + 16 * m + 8 * g]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+                for (int m = 0; m < 2; ++m)
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) dq[db] = mfma32x32x16bf16(akt[db][kb][m], dsb[kb][m], dq[db]);
+        }
+        sstore(buf ^ 1);
+        __syncthreads();
+    }
+    if (qrow < p.Tq) {
+        uint16_t* dst = (uint16_t*)p.dq + b * p.sdq.b + h * p.sdq.h + (int64_t)qrow * p.sdq.t;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f32x4 val;
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) val[cc] = dq[db][4 * j + cc] * p.scale;
+                st4(dst + db * 32 + 8 * j + 4 * g, val);
+            }
+    }
+}
+
+int launch_bwd_dq_bf16(const BwdParams& p, hipStream_t s) {
+    const dim3 grid((unsigned)(p.n_qtiles * p.B * p.H));
+    switch (p.D) {
+        case 128: hipLaunchKernelGGL((bwd_dq_bf16_kernel<128>), grid, dim3(256), 0, s, p); break;
+        default: return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
 }
 
 int bwd_main_bf16_occupancy(int D, int* blocks_per_cu) {

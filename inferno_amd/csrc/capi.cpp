@@ -126,7 +126,8 @@ int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dt
         }
         case INF_OP_ATTN_BWD: {
             size_t n = round_up(bh * Tq * sizeof(float));                       // delta
-            if (dt == INF_BF16) n += round_up(bh * Tq * (size_t)D * sizeof(float));  // dQ accumulator
+            if (dt == INF_BF16 && !inf::bwd_dq_direct(B * H, Tq, Tk, D, inf::bwd_keys_per_wg(1, D)))
+                n += round_up(bh * Tq * (size_t)D * sizeof(float));  // dQ accumulator
             inf::BwdPlan plan;                                                  // causal split plan
             inf::bwd_plan(B, H, Tq, Tk, D, 1, dt == INF_BF16, &plan);
             n += round_up(inf::bwd_split_workspace_bytes(plan, B, H, D));
@@ -222,11 +223,14 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     p.c = scale * 1.4426950408889634f;
     const int bk = inf::bwd_keys_per_wg(dt == INF_BF16, D);
     p.n_kblocks = (Tk + bk - 1) / bk;
+    p.dq_direct = dt == INF_BF16 && inf::bwd_dq_direct(B * H, Tq, Tk, D, bk);
+    p.n_qtiles = (Tq + inf::kBwdDqBM - 1) / inf::kBwdDqBM;
+    if (p.dq_direct) p.dq_acc = nullptr;  // dq is written by the dQ pass
     inf::BwdPlan plan;
     inf::bwd_plan(B, H, Tq, Tk, D, p.causal, dt == INF_BF16, &plan);
     if (plan.n_groups) {
         size_t offset = round_up(bh * Tq * sizeof(float));
-        if (dt == INF_BF16) offset += round_up(bh * Tq * (size_t)D * sizeof(float));
+        if (dt == INF_BF16 && !p.dq_direct) offset += round_up(bh * Tq * (size_t)D * sizeof(float));
         const size_t part_bytes = (size_t)plan.n_slots * bh * 2 * (size_t)D * plan.bk * sizeof(float);
         p.part = reinterpret_cast<float*>(ws + offset);
         p.counters = reinterpret_cast<unsigned*>(ws + offset + part_bytes);

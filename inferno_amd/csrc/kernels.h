@@ -94,6 +94,8 @@ struct BwdParams {
     int causal, off;
     float scale, c;
     int n_kblocks;
+    int dq_direct;          // bf16: dQ from the query-major pass (no accumulator, no atomics)
+    int n_qtiles;           // query tiles of kBwdDqBM rows (dQ pass)
     // split plan (n_groups == 0: workgroup w takes key block w / (B*H), all its tiles)
     int n_groups, n_split;
     float* part;            // n_slots * B*H * 2*D*(keys per workgroup) floats (lane-major accumulators)
@@ -301,5 +303,16 @@ constexpr int bwd_waves(int bf16, int D) { return bf16 && D == 64 ? 8 : 4; }
 constexpr int bwd_bf16_waves(int D) { return bwd_waves(1, D); }
 inline int bwd_keys_per_wg(int bf16, int D) { return bf16 && D == 128 ? 128 : 32 * bwd_waves(bf16, D); }
 constexpr int kBwdBQ = 32;       // query rows per backward inner step
+constexpr int kBwdDqBM = 128;    // query rows per workgroup of the query-major dQ pass
+int launch_bwd_dq_bf16(const BwdParams& p, hipStream_t s);
+// bf16 at D = 128: dQ from a query-major pass instead of fp32 atomics when a
+// query row collects adds from many key blocks (the atomic stream bounds the
+// fused kernel there: config 4 -24%, B2 H8 T4096 -14%) and the pass fills
+// the device (two workgroups per CU); short ranges, small grids and D = 64
+// (whose 256-key blocks halve the adds) keep the atomics.
+inline bool bwd_dq_direct(int BH, int Tq, int Tk, int D, int keys_per_wg) {
+    return D == 128 && (Tk + keys_per_wg - 1) / keys_per_wg >= 32 &&
+           (int64_t)((Tq + kBwdDqBM - 1) / kBwdDqBM) * BH >= 512;
+}
 
 }  // namespace inf

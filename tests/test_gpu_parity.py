@@ -352,6 +352,35 @@ def test_config4_long_context(ia, dtype, H):
         assert e <= (tol_lse if name == "LSE" else tol), f"full head {hf} {name} rel err {e:.3e}"
 
 
+def test_bf16_query_major_dq(ia):
+    """bf16 at D = 128 with many key blocks and a full grid takes dQ from the query-major pass
+    (no atomics): B2 H8 T4096 D128.  Rows < 512 of O, LSE, dQ on two heads against the oracle
+    (they depend on keys < 512 only), dK / dV over all heads through sum_j dV_j = sum_i dO_i and
+    finiteness, and dQ bit-identical on a second call (a fixed summation order)."""
+    print("[case] bf16 query-major dQ B2 H8 T4096 D128", flush=True)
+    B, H, T, D = 2, 8, 4096, 128
+    q, k, v, do = (bf16_round(x) for x in oracle.attn_inputs(B, H, T, D, seed=11))
+    Q, K, V, dO = (dev(x, torch.bfloat16) for x in (q, k, v, do))
+    o_t, lse_t = ia.attn_fwd(Q, K, V, causal=True)
+    dq1, dk1, dv1 = ia.attn_bwd(Q, K, V, o_t, dO, lse_t, causal=True)
+    dq2, _, _ = ia.attn_bwd(Q, K, V, o_t, dO, lse_t, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(dq1, dq2), "dQ of the query-major pass differs between two calls"
+    o, lse, dq, dk, dv = host(o_t), host(lse_t), host(dq1), host(dk1), host(dv1)
+    assert np.isfinite(dq).all() and np.isfinite(dk).all() and np.isfinite(dv).all()
+    t = 512
+    for (b, h) in ((0, 0), (1, H - 1)):
+        sl = (slice(b, b + 1), slice(h, h + 1), slice(0, t))
+        o_r, lse_r = oracle.attn_fwd(q[sl], k[sl], v[sl])
+        dq_r, _, _ = oracle.attn_bwd(q[sl], k[sl], v[sl], do[sl])
+        assert oracle.rel_err(lse[sl], lse_r) <= 1e-3, f"head {(b, h)} LSE"
+        for name, x, r in (("O", o[sl], o_r), ("dQ", dq[sl], dq_r)):
+            e = oracle.rel_err(x, r)
+            assert e <= TOL_BF16, f"head {(b, h)} prefix {name} rel err {e:.3e}"
+    sdo = do.astype(np.float64).sum(axis=2)
+    assert oracle.rel_err(dv.astype(np.float64).sum(axis=2), sdo) <= TOL_BF16
+
+
 def test_config2_bf16_full_size_heads(ia):
     """Config 2's bf16-in variant at its full B8 H12 grid (the backward plan depends on B*H):
     three heads against the oracle on the bf16-rounded inputs at 2e-2, and over every head
