@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0
 # conversion pass.
 BWD_TRAFFIC = {
     "f32": {"bwd_pre": 50.40e6 + 25.56e6, "bwd_main": 202.27e6 + 201.35e6},
-    "bf16": {"bwd_pre": 25.23e6 + 25.56e6, "bwd_main": 56.20e6 + 88.08e6, "bwd_cvt": 25.22e6 + 12.58e6},
+    "bf16": {"bwd_pre": 25.23e6 + 25.56e6, "bwd_main": 66.10e6 + 102.57e6, "bwd_cvt": 25.22e6 + 12.58e6},
 }
 
 METRIC = "causal attn fwd+bwd TFLOP/s (B8 H12 T1024 D64 fp32) + % of MFMA peak"
