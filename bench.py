@@ -343,7 +343,9 @@ def warm_up(fn, torch, seconds=0.2):
 
 
 def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10):
-    """fwd and bwd timings of one attention config (HIP events on the launch stream)."""
+    """One attention config: fwd+bwd throughput over `steps` back-to-back steps between two
+    synchronizations (as `value`), and the fwd / bwd breakdown from HIP events recorded on the
+    launch stream around each call in a second pass (the events add the launch gaps)."""
     tdt = torch.float32 if dtype == "f32" else torch.bfloat16
     q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=42, qk_sigma=qk_sigma)
     Q, K, V, dO = (torch.from_numpy(x).to(dev, tdt) for x in (q, k, v, do))
@@ -362,6 +364,12 @@ def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10
         ia.attn_bwd(Q, K, V, O, dO, LSE, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
 
     warm_up(step, torch)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    step_ms = (time.perf_counter() - t0) * 1e3 / steps
     evs = []
     for i in range(steps):
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
@@ -376,7 +384,7 @@ def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10
     bwd_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
     F = flops_fwd(B, H, T, D)
     peak = MFMA_FP32_PEAK_TFLOPS if dtype == "f32" else MFMA_BF16_PEAK_TFLOPS
-    tot = 3.5 * F / ((fwd_ms + bwd_ms) * 1e-3) / 1e12
+    tot = 3.5 * F / (step_ms * 1e-3) / 1e12
     # minimal HBM bytes: fwd Q,K,V in and O out (+ fp32 LSE); bwd Q,K,V,O,dO in and dQ,dK,dV out
     # (+ LSE); the second roof for the bf16 lines, whose forward sits near the bf16 ridge
     esz = 4 if dtype == "f32" else 2
@@ -389,7 +397,7 @@ def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10
     return {
         "roofs": roofs,
         "shape": f"B{B} H{H} T{T} D{D}", "dtype": dtype if dtype == "f32" else "bf16-in/f32-acc",
-        "qk_sigma": qk_sigma, "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+        "qk_sigma": qk_sigma, "ms_per_step": round(step_ms, 4), "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
         "fwd_tflops": round(F / (fwd_ms * 1e-3) / 1e12, 2),
         "bwd_tflops": round(2.5 * F / (bwd_ms * 1e-3) / 1e12, 2),
         "fwd_bwd_tflops": round(tot, 2), "peak_tflops": peak, "frac": round(tot / peak, 4),
