@@ -301,7 +301,9 @@ static int run_decode_check(const std::string& dir, const Device& dev, size_t P)
 // --------------------------------------------------------- generate-check
 // Greedy generation from given parameters and prompt (tokens.bin, [B, P]
 // int32): prefill through the KV caches, then N tokens, each the argmax of
-// the last position's logits (picked on the device) fed back.  Writes
+// the last position's logits, picked on the device and fed back from there
+// (the same loop as `gpt generate`; the picks and logits are also copied out
+// for the check).  Writes
 // generated.bin ([B, N] int32) and gen_logits.bin ([B, N, V] fp32, the
 // logits each pick was made from).
 static int run_generate_check(const std::string& dir, const Device& dev, size_t P, size_t N) {
@@ -323,15 +325,14 @@ static int run_generate_check(const std::string& dir, const Device& dev, size_t 
         Tensor logits = model.forward_cached(x, caches);  // [B, t, V]
         const size_t t = logits.shape()[1];
         Tensor last = logits.slice(1, t - 1, t - 1);      // [B, 1, V]
-        const std::vector<double> pick = argmax(last).to_host_double();
+        Tensor next = argmax(last);                       // [B, 1] Int32 on the device
+        const std::vector<double> pick = next.to_host_double();
         const std::vector<float> lh = last.to_host_float();
-        std::vector<int32_t> nxt(B);
         for (size_t b = 0; b < B; ++b) {
-            nxt[b] = (int32_t)pick[b];
-            gen[b * N + i] = nxt[b];
+            gen[b * N + i] = (int32_t)pick[b];
             std::memcpy(&glog[(b * N + i) * V], &lh[b * V], V * 4);
         }
-        x = Tensor(DType::Int32, nxt, std::vector<size_t>{B, 1}, "next", dev);
+        x = next;
     }
     {
         std::ofstream f(dir + "/generated.bin", std::ios::binary);
@@ -345,7 +346,9 @@ static int run_generate_check(const std::string& dir, const Device& dev, size_t 
 
 // ----------------------------------------------------------------- generate
 // Greedy generation with KV caches on hip:0: a random prompt of P tokens per
-// sequence, then N new tokens, each fed back (argmax on the host).
+// sequence, then N new tokens.  Each pick stays on the device as the next
+// step's input ([B, 1] Int32 from argmax), so the host enqueues step after
+// step without waiting for the GPU; the tokens are read back after the loop.
 static size_t arg(int argc, char** argv, const char* name, size_t def);
 static void init_normal(Module& m, float stddev, const Device& dev);
 
@@ -363,27 +366,25 @@ static int run_generate(int argc, char** argv) {
     std::uniform_int_distribution<int> tokd(0, (int)V - 1);
     std::vector<int32_t> prompt(B * P);
     for (auto& t : prompt) t = tokd(rng);
-    auto argmax_last = [&](const Tensor& logits) {
-        // the greedy pick of the last position on the device; B indices leave it
+    auto pick_last = [&](const Tensor& logits) {
+        // the greedy pick of the last position: [B, 1] Int32 on the device
         const size_t t = logits.shape()[1];
-        const std::vector<double> h = argmax(logits.slice(1, t - 1, t - 1)).to_host_double();
-        std::vector<int32_t> nxt(B);
-        for (size_t b = 0; b < B; ++b) nxt[b] = (int32_t)h[b];
-        return nxt;
+        return argmax(logits.slice(1, t - 1, t - 1));
     };
     auto run_once = [&](double* prefill_ms, double* decode_ms, std::vector<int32_t>* out) {
         auto caches = model.make_caches(B, T, dev);
         Tensor xp(DType::Int32, prompt, std::vector<size_t>{B, P}, "prompt", dev);
         sync(dev);
         const auto t0 = std::chrono::steady_clock::now();
-        std::vector<int32_t> nxt = argmax_last(model.forward_cached(xp, caches));
+        std::vector<Tensor> picks;
+        picks.push_back(pick_last(model.forward_cached(xp, caches)));
+        sync(dev);
         const auto t1 = std::chrono::steady_clock::now();
-        out->clear();
+        for (size_t i = 1; i < N; ++i) picks.push_back(pick_last(model.forward_cached(picks.back(), caches)));
+        out->assign(B * N, 0);  // step-major: token i of sequence b at i * B + b
         for (size_t i = 0; i < N; ++i) {
-            out->insert(out->end(), nxt.begin(), nxt.end());
-            if (i + 1 == N) break;
-            Tensor x1(DType::Int32, nxt, std::vector<size_t>{B, 1}, "next", dev);
-            nxt = argmax_last(model.forward_cached(x1, caches));
+            const std::vector<double> h = picks[i].to_host_double();
+            for (size_t b = 0; b < B; ++b) (*out)[i * B + b] = (int32_t)h[b];
         }
         const auto t2 = std::chrono::steady_clock::now();
         *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
