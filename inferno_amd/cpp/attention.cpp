@@ -10,13 +10,25 @@
 // SoftmaxBackward / MultiplyBackward / TransposeBackward (mmbackward.cpp:77-80,
 // softmaxbackward.h:111-128, multiplybackward.cpp:41) -- so CPU results equal
 // what Inferno's CPU path computes.  A HIP tensor never takes the CPU branch.
+//
+// Head dims on HIP: the fused kernels are built for D in {32, 64, 128}.  Any
+// other D up to 128 runs them on copies zero-padded along D to the next of
+// those sizes: the zero columns add exact zeros to q k^T and leave zero
+// columns in O, dQ, dK and dV, so the first D columns (and the LSE) are the
+// unpadded results; the scale stays that of the real D.  D above 128 (Float32)
+// runs the reference's composed chain (main.cpp:732-754: q k^T, * scale, the
+// causal mask, Softmax, P v) on the library's HIP ops, its backward through
+// their nodes; the mask enters as an added -1e9 bias (masked_fill's output
+// carries no graph node, as in the reference, which would cut dQ and dK).
 #include <algorithm>
 #include <cfloat>
 #include <cmath>
 #include <mutex>
 
 #include "detail.h"
+#include "inferno/core/ops.h"
 #include "inferno/functional/attention.h"
+#include "inferno/functional/softmax.h"
 #include "inferno/gradengine/engine.h"
 
 namespace Inferno {
@@ -84,6 +96,42 @@ void* decode_workspace(size_t bytes, const Device& dev) {
 inf_strides strides_of(const Tensor& t) {
     const auto& s = t.strides();
     return inf_strides{(int64_t)s[0], (int64_t)s[1], (int64_t)s[2], (int64_t)s[3]};
+}
+
+// ---- head dims the fused kernels do not take -------------------------------
+bool fused_head_dim(size_t D) { return D == 32 || D == 64 || D == 128; }
+size_t padded_head_dim(size_t D) { return D <= 32 ? 32 : D <= 64 ? 64 : 128; }
+
+// dst = src, two HIP views of one shape.
+void copy_into(const Tensor& src, Tensor& dst) {
+    const auto shape = detail::to_i64(src.shape());
+    const auto ss = detail::to_i64(src.strides());
+    const auto ds = detail::to_i64(dst.strides());
+    detail::DeviceGuard g(src.device().index);
+    detail::status_check(inf_copy_strided(src.data_ptr(), ss.data(), dst.data_ptr(), ds.data(), (int)src.ndim(),
+                                          shape.data(), (int)dtype_size(src.dtype()), detail::stream_of(src)),
+                         "inf_copy_strided");
+}
+
+// [B, H, T, D] -> a dense zero-filled [B, H, T, Dp] holding it in columns [0, D).
+Tensor pad_head_dim(const Tensor& t, size_t Dp) {
+    NoGradGuard ng;
+    std::vector<size_t> shape = t.shape();
+    shape[3] = Dp;
+    Tensor out = Tensor::zeros(shape, t.dtype(), t.device(), "attention_padded");
+    if (t.numel()) {
+        Tensor dst = make_view(out, t.shape(), out.strides(), out.offset(), "attention_pad_dst");
+        copy_into(t, dst);
+    }
+    return out;
+}
+
+// The first D columns of [B, H, T, Dp], dense.
+Tensor unpad_head_dim(const Tensor& t, size_t D) {
+    NoGradGuard ng;
+    std::vector<size_t> shape = t.shape();
+    shape[3] = D;
+    return detail::dense_copy(make_view(t, shape, t.strides(), t.offset(), "attention_unpad_src"));
 }
 
 // ---- CPU branch: the reference chain, one head at a time -------------------
@@ -212,6 +260,88 @@ void cpu_bwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& g,
         }
 }
 
+// The fused forward on HIP views (D in {32, 64, 128}) into out / lse.
+void hip_fwd(const Tensor& q, const Tensor& k, const Tensor& v, Tensor& out, Tensor& lse, const Shape4& s, float sc,
+             bool causal) {
+    Tensor qa = abi_view(q), ka = abi_view(k), va = abi_view(v);
+    detail::DeviceGuard g(q.device().index);
+    const inf_dtype dt = detail::inf_dt(q.dtype(), "scaled_dot_product_attention");
+    size_t ws_bytes = 0;
+    if (causal)
+        detail::status_check(inf_attn_workspace_bytes(INF_OP_ATTN_FWD, (int)s.B, (int)s.H, (int)s.Tq, (int)s.Tk,
+                                                      (int)s.D, dt, &ws_bytes),
+                             "inf_attn_workspace_bytes");
+    Workspace ws(ws_bytes, q.device());
+    detail::status_check(
+        inf_attn_fwd(qa.data_ptr(), strides_of(qa), ka.data_ptr(), strides_of(ka), va.data_ptr(), strides_of(va),
+                     out.data_ptr(), strides_of(out), static_cast<float*>(lse.data_ptr()), ws.ptr, ws_bytes, (int)s.B,
+                     (int)s.H, (int)s.Tq, (int)s.Tk, (int)s.D, sc, causal ? 1 : 0, dt, detail::stream_of(q)),
+        "inf_attn_fwd");
+}
+
+// The fused backward on HIP views into dq / dk / dv.
+void hip_bwd(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& o, const Tensor& g, const Tensor& lse,
+             Tensor& dq, Tensor& dk, Tensor& dv, const Shape4& s, float sc, bool causal) {
+    const inf_dtype dt = detail::inf_dt(q.dtype(), "AttentionBackward");
+    size_t ws_bytes = 0;
+    detail::status_check(inf_attn_workspace_bytes(INF_OP_ATTN_BWD, (int)s.B, (int)s.H, (int)s.Tq, (int)s.Tk,
+                                                  (int)s.D, dt, &ws_bytes),
+                         "inf_attn_workspace_bytes");
+    Workspace ws(ws_bytes, q.device());
+    Tensor qa = abi_view(q), ka = abi_view(k), va = abi_view(v), oa = abi_view(o), ga = abi_view(g);
+    detail::DeviceGuard dg(q.device().index);
+    detail::status_check(
+        inf_attn_bwd(qa.data_ptr(), strides_of(qa), ka.data_ptr(), strides_of(ka), va.data_ptr(), strides_of(va),
+                     oa.data_ptr(), strides_of(oa), ga.data_ptr(), strides_of(ga),
+                     static_cast<const float*>(lse.data_ptr()), dq.data_ptr(), strides_of(dq), dk.data_ptr(),
+                     strides_of(dk), dv.data_ptr(), strides_of(dv), ws.ptr, ws_bytes, (int)s.B, (int)s.H, (int)s.Tq,
+                     (int)s.Tk, (int)s.D, sc, causal ? 1 : 0, dt, detail::stream_of(q)),
+        "inf_attn_bwd");
+}
+
+// Per-row log-sum-exp of dense fp32 scores [B, H, Tq, Tk] on HIP: the
+// cross-entropy kernel's row LSE (its loss against target 0 is discarded).
+Tensor rows_lse(const Tensor& S, const Shape4& s) {
+    NoGradGuard ng;
+    const int64_t rows = (int64_t)(s.B * s.H * s.Tq), cols = (int64_t)s.Tk;
+    Tensor lse(DType::Float32, {s.B, s.H, s.Tq}, "attention_lse", S.device(), false);
+    Tensor targets = Tensor::zeros({(size_t)rows}, DType::Int32, S.device(), "lse_targets");
+    Tensor loss(DType::Float32, {1}, "lse_loss", S.device(), false);
+    size_t ws_bytes = 0;
+    detail::status_check(inf_nn_workspace_bytes(INF_OP_CROSS_ENTROPY, rows, cols, &ws_bytes), "inf_nn_workspace_bytes");
+    Workspace ws(ws_bytes, S.device());
+    detail::DeviceGuard g(S.device().index);
+    detail::status_check(inf_cross_entropy_fwd(S.data_ptr(), cols, static_cast<const int32_t*>(targets.data_ptr()),
+                                               static_cast<float*>(loss.data_ptr()),
+                                               static_cast<float*>(lse.data_ptr()), rows, cols, INF_F32, ws.ptr,
+                                               ws_bytes, detail::stream_of(S)),
+                         "inf_cross_entropy_fwd");
+    return lse;
+}
+
+// D > 128 on HIP: the reference's composed chain, fp32, with autograd through
+// matmul / multiply / add / Softmax.
+Tensor composed_attention(const Tensor& q, const Tensor& k, const Tensor& v, const Shape4& s, bool causal, float sc,
+                          Tensor* lse_out) {
+    if (q.dtype() != DType::Float32)
+        throw Error("scaled_dot_product_attention: a head dim above 128 runs the composed Float32 chain on HIP "
+                    "(BFloat16 inputs need D <= 128)");
+    Tensor S = matmul(q, k.transpose(-1, -2), "QK ^ T") * sc;
+    if (causal) {
+        Tensor bias;
+        {
+            NoGradGuard ng;
+            const Tensor ones = Tensor::ones({1, 1, s.Tq, s.Tk}, DType::Int32, q.device(), "causal_mask_ones");
+            bias = masked_fill(Tensor::zeros({1, 1, s.Tq, s.Tk}, DType::Float32, q.device(), "causal_bias"),
+                               triu(ones, (int)(1 + s.Tk - s.Tq)), -1e9f);
+        }
+        S = S + bias;
+    }
+    if (lse_out) *lse_out = rows_lse(S.contiguous(), s);
+    Tensor P = Softmax(S, -1);
+    return matmul(P, v, "attn@V");
+}
+
 }  // namespace
 
 Tensor scaled_dot_product_attention_lse(const Tensor& q, const Tensor& k, const Tensor& v, bool causal, float scale,
@@ -220,28 +350,30 @@ Tensor scaled_dot_product_attention_lse(const Tensor& q, const Tensor& k, const 
     if (causal && s.Tq > s.Tk) throw Error("scaled_dot_product_attention: causal needs Tq <= Tk");
     const float sc = resolve_scale(scale, s.D);
     if (!(sc > 0.f) || !std::isfinite(sc)) throw Error("scaled_dot_product_attention: scale must be finite and > 0");
-    Tensor out(q.dtype(), {s.B, s.H, s.Tq, s.D}, "attention", q.device(), false);
+    const bool hip = !q.device().is_cpu();
+    if (hip && s.D > 128 && s.B && s.H && s.Tq && s.Tk) return composed_attention(q, k, v, s, causal, sc, lse_out);
     Tensor lse(DType::Float32, {s.B, s.H, s.Tq}, "attention_lse", q.device(), false);
-    if (s.B && s.H && s.Tq && s.Tk) {
-        if (q.device().is_cpu()) {
-            cpu_fwd(q, k, v, s, sc, causal, out, lse);
-        } else {
-            Tensor qa = abi_view(q), ka = abi_view(k), va = abi_view(v);
-            detail::DeviceGuard g(q.device().index);
-            const inf_dtype dt = detail::inf_dt(q.dtype(), "scaled_dot_product_attention");
-            size_t ws_bytes = 0;
-            if (causal)
-                detail::status_check(inf_attn_workspace_bytes(INF_OP_ATTN_FWD, (int)s.B, (int)s.H, (int)s.Tq,
-                                                              (int)s.Tk, (int)s.D, dt, &ws_bytes),
-                                     "inf_attn_workspace_bytes");
-            Workspace ws(ws_bytes, q.device());
-            detail::status_check(
-                inf_attn_fwd(qa.data_ptr(), strides_of(qa), ka.data_ptr(), strides_of(ka), va.data_ptr(), strides_of(va),
-                             out.data_ptr(), strides_of(out), static_cast<float*>(lse.data_ptr()), ws.ptr, ws_bytes,
-                             (int)s.B, (int)s.H, (int)s.Tq, (int)s.Tk, (int)s.D, sc, causal ? 1 : 0, dt,
-                             detail::stream_of(q)),
-                "inf_attn_fwd");
+    if (hip && !fused_head_dim(s.D)) {
+        const size_t Dp = padded_head_dim(s.D);
+        Shape4 sp = s;
+        sp.D = Dp;
+        Tensor qp = pad_head_dim(q, Dp), kp = pad_head_dim(k, Dp), vp = pad_head_dim(v, Dp);
+        Tensor op(q.dtype(), {s.B, s.H, s.Tq, Dp}, "attention_padded", q.device(), false);
+        if (s.B && s.H && s.Tq && s.Tk) hip_fwd(qp, kp, vp, op, lse, sp, sc, causal);
+        Tensor out = unpad_head_dim(op, s.D);
+        if (grad_enabled && (q.requires_grad() || k.requires_grad() || v.requires_grad())) {
+            out.set_requires_grad(true);
+            GetImpl(out)->gradfn() = std::make_shared<AttentionBackward>(q, k, v, lse, causal, sc, qp, kp, vp, op);
         }
+        if (lse_out) *lse_out = lse;
+        return out;
+    }
+    Tensor out(q.dtype(), {s.B, s.H, s.Tq, s.D}, "attention", q.device(), false);
+    if (s.B && s.H && s.Tq && s.Tk) {
+        if (!hip)
+            cpu_fwd(q, k, v, s, sc, causal, out, lse);
+        else
+            hip_fwd(q, k, v, out, lse, s, sc, causal);
     }
     if (grad_enabled && (q.requires_grad() || k.requires_grad() || v.requires_grad())) {
         out.set_requires_grad(true);
@@ -267,31 +399,48 @@ AttentionBackward::AttentionBackward(const Tensor& q, const Tensor& k, const Ten
     set_name("AttentionBackward");
 }
 
+AttentionBackward::AttentionBackward(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& lse,
+                                     bool causal, float scale, const Tensor& q_padded, const Tensor& k_padded,
+                                     const Tensor& v_padded, const Tensor& out_padded)
+    : m_q(q),
+      m_k(k),
+      m_v(v),
+      m_lse(lse),
+      m_qp(q_padded),
+      m_kp(k_padded),
+      m_vp(v_padded),
+      m_op(out_padded),
+      m_causal(causal),
+      m_scale(scale) {
+    set_name("AttentionBackward");
+}
+
 void AttentionBackward::backward() {
     NoGradGuard ng;
     Tensor g = Engine::grad_in(this, 0);
     const Shape4 s = check_qkv(m_q, m_k, m_v, "AttentionBackward");
-    Tensor dq(m_q.dtype(), m_q.shape(), "attention_dq", m_q.device(), false);
-    Tensor dk(m_k.dtype(), m_k.shape(), "attention_dk", m_k.device(), false);
-    Tensor dv(m_v.dtype(), m_v.shape(), "attention_dv", m_v.device(), false);
-    if (m_q.device().is_cpu()) {
-        cpu_bwd(m_q, m_k, m_v, g, s, m_scale, m_causal, dq, dk, dv);
+    Tensor dq, dk, dv;
+    if (m_qp.defined()) {
+        // padded head dim: the fused backward on the padded copies, then the first D columns
+        const size_t Dp = m_qp.shape()[3];
+        Shape4 sp = s;
+        sp.D = Dp;
+        Tensor dqp(m_qp.dtype(), m_qp.shape(), "attention_dq_padded", m_qp.device(), false);
+        Tensor dkp(m_kp.dtype(), m_kp.shape(), "attention_dk_padded", m_kp.device(), false);
+        Tensor dvp(m_vp.dtype(), m_vp.shape(), "attention_dv_padded", m_vp.device(), false);
+        if (s.B && s.H && s.Tq && s.Tk)
+            hip_bwd(m_qp, m_kp, m_vp, m_op, pad_head_dim(g, Dp), m_lse, dqp, dkp, dvp, sp, m_scale, m_causal);
+        dq = unpad_head_dim(dqp, s.D);
+        dk = unpad_head_dim(dkp, s.D);
+        dv = unpad_head_dim(dvp, s.D);
     } else {
-        const inf_dtype dt = detail::inf_dt(m_q.dtype(), "AttentionBackward");
-        size_t ws_bytes = 0;
-        detail::status_check(inf_attn_workspace_bytes(INF_OP_ATTN_BWD, (int)s.B, (int)s.H, (int)s.Tq, (int)s.Tk,
-                                                      (int)s.D, dt, &ws_bytes),
-                             "inf_attn_workspace_bytes");
-        Workspace ws(ws_bytes, m_q.device());
-        Tensor qa = abi_view(m_q), ka = abi_view(m_k), va = abi_view(m_v), oa = abi_view(m_out), ga = abi_view(g);
-        detail::DeviceGuard dg(m_q.device().index);
-        detail::status_check(
-            inf_attn_bwd(qa.data_ptr(), strides_of(qa), ka.data_ptr(), strides_of(ka), va.data_ptr(), strides_of(va),
-                         oa.data_ptr(), strides_of(oa), ga.data_ptr(), strides_of(ga),
-                         static_cast<const float*>(m_lse.data_ptr()), dq.data_ptr(), strides_of(dq), dk.data_ptr(),
-                         strides_of(dk), dv.data_ptr(), strides_of(dv), ws.ptr, ws_bytes, (int)s.B, (int)s.H,
-                         (int)s.Tq, (int)s.Tk, (int)s.D, m_scale, m_causal ? 1 : 0, dt, detail::stream_of(m_q)),
-            "inf_attn_bwd");
+        dq = Tensor(m_q.dtype(), m_q.shape(), "attention_dq", m_q.device(), false);
+        dk = Tensor(m_k.dtype(), m_k.shape(), "attention_dk", m_k.device(), false);
+        dv = Tensor(m_v.dtype(), m_v.shape(), "attention_dv", m_v.device(), false);
+        if (m_q.device().is_cpu())
+            cpu_bwd(m_q, m_k, m_v, g, s, m_scale, m_causal, dq, dk, dv);
+        else
+            hip_bwd(m_q, m_k, m_v, m_out, g, m_lse, dq, dk, dv, s, m_scale, m_causal);
     }
     if (auto e = GetImpl(m_q)->grad_edge()) Engine::accumulate(e.get(), 0, dq);
     if (auto e = GetImpl(m_k)->grad_edge()) Engine::accumulate(e.get(), 0, dk);
@@ -300,6 +449,7 @@ void AttentionBackward::backward() {
 
 void AttentionBackward::release() {
     m_q = m_k = m_v = m_out = m_lse = Tensor();
+    m_qp = m_kp = m_vp = m_op = Tensor();
 }
 
 void AttentionBackward::get_inputs(std::vector<Tensor>& out) const {
@@ -312,9 +462,16 @@ Tensor attention_decode(const Tensor& q, const Tensor& kcache, const Tensor& vca
     const Shape4 s = check_qkv(q, kcache, vcache, "attention_decode");
     if (s.Tq != 1) throw Error("attention_decode: q must be [B, H, 1, D]");
     const float sc = resolve_scale(scale, s.D);
-    if (q.device().is_cpu()) {
+    if (q.device().is_cpu() || s.D > 128) {
         NoGradGuard ng;
         return scaled_dot_product_attention(q, kcache, vcache, false, sc);
+    }
+    if (!fused_head_dim(s.D)) {
+        // a padded copy of the cache prefix per call: correct, not fast
+        const size_t Dp = padded_head_dim(s.D);
+        return unpad_head_dim(attention_decode(pad_head_dim(q, Dp), pad_head_dim(kcache, Dp),
+                                               pad_head_dim(vcache, Dp), sc),
+                              s.D);
     }
     Tensor out(q.dtype(), {s.B, s.H, 1, s.D}, "attention_decode", q.device(), false);
     const inf_dtype dt = detail::inf_dt(q.dtype(), "attention_decode");

@@ -853,8 +853,10 @@ Tensor qkv_attention(const Tensor& qkv, size_t num_heads, bool causal, float sca
     check_float(qkv, "qkv_attention");
     const QKVShape s = qkv_shape(qkv, num_heads);
     const float sc = std::isnan(scale) ? 1.0f / std::sqrt((float)s.D) : scale;
-    if (qkv.device().is_cpu()) {
+    if (qkv.device().is_cpu() || !(s.D == 32 || s.D == 64 || s.D == 128)) {
         // Compose the fused reference chain on views; autograd flows through them.
+        // (HIP head dims the kernels are not built for take the padded or
+        // composed route inside scaled_dot_product_attention.)
         Tensor q = qkv.slice(2, 0, s.C - 1).unflatten(2, {s.H, s.D}).transpose(1, 2);
         Tensor k = qkv.slice(2, s.C, 2 * s.C - 1).unflatten(2, {s.H, s.D}).transpose(1, 2);
         Tensor v = qkv.slice(2, 2 * s.C, 3 * s.C - 1).unflatten(2, {s.H, s.D}).transpose(1, 2);

@@ -244,13 +244,16 @@ static int selftest(Device dev) {
 
 // --------------------------------------------------------------- attention
 static int cmd_attn(int argc, char** argv) {
-    if (argc < 10) throw Error("usage: attn <dir> B H T D f32|bf16 cpu|hip causal [qkv]");
+    if (argc < 10) throw Error("usage: attn <dir> B H T D f32|bf16 cpu|hip causal [qkv|qkvop]");
     const std::string dir = argv[2];
     const size_t B = std::stoul(argv[3]), H = std::stoul(argv[4]), T = std::stoul(argv[5]), D = std::stoul(argv[6]);
     const DType dt = parse_dt(argv[7]);
     const Device dev = parse_dev(argv[8]);
     const bool causal = std::stoi(argv[9]) != 0;
-    const bool qkv_layout = argc > 10 && std::string(argv[10]) == "qkv";
+    // qkv: q, k, v as views of one [B, T, 3C] tensor into scaled_dot_product_attention;
+    // qkvop: the same tensor through qkv_attention (the MultiHeadAttention op), y [B, T, C]
+    const bool qkv_op = argc > 10 && std::string(argv[10]) == "qkvop";
+    const bool qkv_layout = argc > 10 && (std::string(argv[10]) == "qkv" || qkv_op);
     const size_t n = B * H * T * D;
     auto qh = read_f32(dir + "/q.bin", n), kh = read_f32(dir + "/k.bin", n), vh = read_f32(dir + "/v.bin", n),
          gh = read_f32(dir + "/do.bin", n);
@@ -281,9 +284,22 @@ static int cmd_attn(int argc, char** argv) {
         k = heads(C);
         v = heads(2 * C);
     }
-    Tensor lse;
-    Tensor o = scaled_dot_product_attention_lse(q, k, v, causal, NAN, &lse);
-    (o * dO).backward();
+    Tensor lse, o;
+    if (qkv_op) {
+        Tensor y = qkv_attention(qkv, H, causal);  // [B, T, C]
+        Tensor dOy;
+        {
+            NoGradGuard ng;
+            dOy = dO.transpose(1, 2).contiguous().reshape({B, T, H * D});
+        }
+        (y * dOy).backward();
+        NoGradGuard ng;
+        o = y.unflatten(2, {H, D}).transpose(1, 2).contiguous();
+        lse = Tensor::zeros({B, H, T}, DType::Float32, dev);
+    } else {
+        o = scaled_dot_product_attention_lse(q, k, v, causal, NAN, &lse);
+        (o * dO).backward();
+    }
     write_f32(dir + "/o.bin", o.to_host_float());
     write_f32(dir + "/lse.bin", lse.to_host_float());
     if (!qkv_layout) {

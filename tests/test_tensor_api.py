@@ -85,6 +85,14 @@ def test_attention_cpu_qkv_views_bitwise(tmp_path):
         assert np.array_equal(bits(out[n]), bits(ref[n])), n
 
 
+def test_attention_cpu_qkv_op_bitwise(tmp_path):
+    """qkv_attention (the MultiHeadAttention op) on one [B, T, 3C] tensor: y and the gradient
+    of qkv equal the oracle's O, dQ, dK, dV bit for bit."""
+    out, ref = attn_case(tmp_path, 2, 3, 20, 8, "f32", "cpu", True, layout="qkvop")
+    for n in ("o", "dq", "dk", "dv"):
+        assert np.array_equal(bits(out[n]), bits(ref[n])), n
+
+
 def test_softmax_cpu_bitwise(tmp_path):
     x = oracle.randn(7, (6, 50), 3.0)
     g = oracle.randn(8, (6, 50))
@@ -254,6 +262,51 @@ def test_attention_hip_parity(tmp_path, B, H, T, D, dtype, layout):
     for n in ("o", "dq", "dk", "dv"):
         e = oracle.rel_err(out[n], ref[n])
         assert e <= tol, f"{n} rel err {e:.3e}"
+
+
+@gpu
+@pytest.mark.parametrize("B,H,T,D,dtype,layout", [
+    (1, 2, 70, 16, "f32", None),      # zero-padded to 32
+    (2, 2, 100, 48, "f32", None),     # padded to 64
+    (1, 3, 90, 96, "f32", "qkv"),     # padded to 128, q / k / v as views of [B, T, 3C]
+    (2, 3, 77, 48, "f32", "qkvop"),   # padded, through qkv_attention (the MultiHeadAttention op)
+    (1, 2, 80, 80, "bf16", None),     # padded to 128, bf16 inputs
+    (1, 2, 70, 160, "f32", None),     # above 128: the composed chain on HIP ops
+    (2, 2, 50, 256, "f32", "qkvop"),  # composed, through qkv_attention
+])
+def test_attention_hip_other_head_dims(tmp_path, B, H, T, D, dtype, layout):
+    """Head dims the fused kernels are not built for, through the C++ layer on HIP: up to 128 the
+    kernels on zero-padded copies, above 128 the reference's composed chain on the HIP ops.
+    O, dQ, dK, dV (and the LSE where the op returns it) against the oracle."""
+    if not have_gpu():
+        pytest.skip("no GPU")
+    print(f"[case] api_driver attn hip other head dim B{B} H{H} T{T} D{D} {dtype} {layout}", flush=True)
+    out, ref = attn_case(tmp_path, B, H, T, D, dtype, "hip", True, layout)
+    tol = 1e-4 if dtype == "f32" else 2e-2
+    for n in ("o", "dq", "dk", "dv"):
+        e = oracle.rel_err(out[n], ref[n])
+        assert e <= tol, f"{n} rel err {e:.3e}"
+    if layout != "qkvop":
+        assert oracle.rel_err(out["lse"], ref["lse"]) <= (1e-5 if dtype == "f32" else 1e-3)
+
+
+@gpu
+@pytest.mark.parametrize("D,dtype", [(48, "f32"), (80, "bf16"), (160, "f32")])
+def test_decode_hip_other_head_dims(tmp_path, D, dtype):
+    """attention_decode at head dims the decode kernel is not built for (padded up to 128,
+    composed above), against the oracle's decode."""
+    if not have_gpu():
+        pytest.skip("no GPU")
+    print(f"[case] api_driver decode hip D{D} {dtype}", flush=True)
+    B, H, Tk = 2, 3, 300
+    q, kc, vc = oracle.randn(31, (B, H, 1, D)), oracle.randn(32, (B, H, Tk, D)), oracle.randn(33, (B, H, Tk, D))
+    if dtype == "bf16":
+        q, kc, vc = (bf16_round(x) for x in (q, kc, vc))
+    write(tmp_path, q=q, kc=kc, vc=vc)
+    r = run("decode", tmp_path, B, H, Tk, D, dtype, "hip")
+    assert r.returncode == 0, r.stdout + r.stderr
+    e = oracle.rel_err(read(tmp_path, "o", (B, H, 1, D)), oracle.attn_decode(q, kc, vc))
+    assert e <= (1e-4 if dtype == "f32" else 2e-2), f"rel err {e:.3e}"
 
 
 @gpu
