@@ -381,6 +381,34 @@ def test_bf16_query_major_dq(ia):
     assert oracle.rel_err(dv.astype(np.float64).sum(axis=2), sdo) <= TOL_BF16
 
 
+def test_bf16_query_major_dq_end_aligned(ia):
+    """The query-major dQ pass with fewer queries than keys (end-aligned causal mask, Tk - Tq =
+    96): B2 H8 Tq4000 Tk4096 D128 bf16.  Rows < 256 of O, LSE and dQ on two heads against the
+    oracle run on the matching end-aligned prefix (queries [0, 256) against keys [0, 352)), sum_j
+    dV_j = sum_i dO_i over every head, and dQ bit-identical on a second call."""
+    print("[case] bf16 query-major dQ end-aligned B2 H8 Tq4000 Tk4096 D128", flush=True)
+    B, H, Tq, Tk, D = 2, 8, 4000, 4096, 128
+    q, k, v, do = (bf16_round(x) for x in oracle.attn_inputs(B, H, Tq, D, seed=13, Tk=Tk))
+    Q, K, V, dO = (dev(x, torch.bfloat16) for x in (q, k, v, do))
+    o_t, lse_t = ia.attn_fwd(Q, K, V, causal=True)
+    dq1, dk1, dv1 = ia.attn_bwd(Q, K, V, o_t, dO, lse_t, causal=True)
+    dq2, _, _ = ia.attn_bwd(Q, K, V, o_t, dO, lse_t, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(dq1, dq2), "dQ of the query-major pass differs between two calls"
+    o, lse, dq, dv = host(o_t), host(lse_t), host(dq1), host(dv1)
+    assert np.isfinite(dq).all() and np.isfinite(host(dk1)).all() and np.isfinite(dv).all()
+    r, off = 256, Tk - Tq
+    for (b, h) in ((0, 3), (1, H - 1)):
+        hq, hk = (slice(b, b + 1), slice(h, h + 1), slice(0, r)), (slice(b, b + 1), slice(h, h + 1), slice(0, r + off))
+        o_r, lse_r = oracle.attn_fwd(q[hq], k[hk], v[hk])
+        dq_r, _, _ = oracle.attn_bwd(q[hq], k[hk], v[hk], do[hq])
+        assert oracle.rel_err(lse[hq], lse_r) <= 1e-3, f"head {(b, h)} LSE"
+        for name, x, ref in (("O", o[hq], o_r), ("dQ", dq[hq], dq_r)):
+            e = oracle.rel_err(x, ref)
+            assert e <= TOL_BF16, f"head {(b, h)} prefix {name} rel err {e:.3e}"
+    assert oracle.rel_err(dv.astype(np.float64).sum(axis=2), do.astype(np.float64).sum(axis=2)) <= TOL_BF16
+
+
 def test_config2_bf16_full_size_heads(ia):
     """Config 2's bf16-in variant at its full B8 H12 grid (the backward plan depends on B*H):
     three heads against the oracle on the bf16-rounded inputs at 2e-2, and over every head
