@@ -29,6 +29,13 @@ Tensor linear(const Tensor& x, const Tensor& W, const Tensor& b);
 // LayerNorm over the last dimension (layernorm.cpp:33-80, layernorm_kernels.h:48-87).
 Tensor layer_norm(const Tensor& x, const Tensor& gamma, const Tensor& beta, float eps);
 
+// LayerNorm(x + r) with the sum returned through *sum: the residual add and the
+// next LayerNorm of a transformer block.  Equals layer_norm(x + r, ...) (which
+// it runs when a gradient is needed or on the CPU); on HIP without gradients it
+// is one pass (inf_add_layernorm_fwd).  No reference counterpart.
+Tensor add_layer_norm(const Tensor& x, const Tensor& r, const Tensor& gamma, const Tensor& beta, float eps,
+                      Tensor* sum);
+
 // table[ids] for Int32 ids [...] -> [..., dim] (embedding.cpp:52-104).
 Tensor embedding(const Tensor& ids, const Tensor& table);
 

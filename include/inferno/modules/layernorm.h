@@ -14,6 +14,7 @@ public:
     // Parameter access (no reference counterpart; the reference's are private).
     Tensor& gamma() { return m_gamma; }
     Tensor& beta() { return m_beta; }
+    float eps() const { return m_eps; }
 
 private:
     Tensor m_beta;

@@ -257,6 +257,17 @@ int inf_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float al
 int inf_layernorm_fwd(const void* x, int64_t ldx, void* y, int64_t ldy, const float* gamma, const float* beta,
                       float* mean, float* invstd, int64_t rows, int64_t dim, float eps, inf_dtype dt, void* stream);
 
+/* Residual add and LayerNorm in one pass: h = x + r (rounded to dt, stored),
+ * y = LayerNorm(h) as inf_layernorm_fwd computes it -- the same values as an
+ * add followed by inf_layernorm_fwd.  h may be x or r (updated in place); y
+ * must not overlap x, r or h.  No reference counterpart: the reference runs
+ * the transformer block's residual add and the next LayerNorm as two launches
+ * (`x + attn(...)` then LayerNorm::forward, InfernoApp/main.cpp); this is for
+ * inference loops, where each launch costs more than the row's work. */
+int inf_add_layernorm_fwd(const void* x, int64_t ldx, const void* r, int64_t ldr, void* h, int64_t ldh, void* y,
+                          int64_t ldy, const float* gamma, const float* beta, float* mean, float* invstd, int64_t rows,
+                          int64_t dim, float eps, inf_dtype dt, void* stream);
+
 /* LayerNorm backward from the saved mean / invstd: dx, and dgamma = sum_rows
  * dy * xhat, dbeta = sum_rows dy (overwritten, or added to when accumulate).
  * dim % 4 == 0 and dim <= 2048.  Replaces cuda_layernorm_backward

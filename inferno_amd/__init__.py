@@ -52,6 +52,7 @@ EXPORTS = (
     "inf_nn_workspace_bytes",
     "inf_gemm",
     "inf_layernorm_fwd",
+    "inf_add_layernorm_fwd",
     "inf_layernorm_bwd",
     "inf_gelu_fwd",
     "inf_gelu_bwd",
@@ -137,6 +138,7 @@ def lib() -> ctypes.CDLL:
         L.inf_gemm.argtypes = [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64, f32, vp, i64, i64, i64,
                                vp, i32, vp, sz, vp]
         L.inf_layernorm_fwd.argtypes = [vp, i64, vp, i64, vp, vp, vp, vp, i64, i64, f32, i32, vp]
+        L.inf_add_layernorm_fwd.argtypes = [vp, i64, vp, i64, vp, i64, vp, i64, vp, vp, vp, vp, i64, i64, f32, i32, vp]
         L.inf_layernorm_bwd.argtypes = [vp, i64, vp, i64, vp, vp, vp, vp, i64, vp, vp, i32, i64, i64, i32, vp, sz,
                                         vp]
         L.inf_gelu_fwd.argtypes = [vp, vp, i64, i32, vp]
@@ -201,6 +203,7 @@ from .ops import (  # noqa: E402  (torch-facing helpers need lib())
     triu,
 )
 from .nn import (  # noqa: E402
+    add_layernorm_fwd,
     adamw_step,
     adamw_step_multi,
     argmax_rows,

@@ -97,13 +97,16 @@ public:
         Tensor ff = feedforward2.forward(static_cast<const Tensor&>(n));
         return h + ff;
     }
-    // Inference on the next positions with this layer's KV cache.
-    Tensor forward_cached(Tensor& x, KVCache& cache) {
-        Tensor normed = layernorm1.forward(x);
-        Tensor h = x + attn.forward_cached(normed, cache);
-        Tensor normed2 = layernorm2.forward(h);
+    // Inference on the next positions with this layer's KV cache, given x and
+    // normed = LayerNorm-1(x): returns the MLP output and sets *h = x +
+    // attention.  The block's output h + MLP is left to the caller, which adds
+    // it and applies the next LayerNorm in one pass, as this does for h and
+    // LayerNorm-2 (add_layer_norm: one launch instead of an add and a norm).
+    Tensor forward_cached(const Tensor& x, const Tensor& normed, KVCache& cache, Tensor* h) {
+        Tensor a = attn.forward_cached(normed, cache);
+        Tensor normed2 = add_layer_norm(x, a, layernorm2.gamma(), layernorm2.beta(), layernorm2.eps(), h);
         Tensor n = gelu(feedforward1.forward(static_cast<const Tensor&>(normed2)));
-        return h + feedforward2.forward(static_cast<const Tensor&>(n));
+        return feedforward2.forward(static_cast<const Tensor&>(n));
     }
     MultiHeadAttention attn;
     LayerNorm layernorm1, layernorm2;
@@ -153,10 +156,16 @@ public:
         const size_t pos0 = caches.empty() ? 0 : caches[0].length;
         Tensor x = emb1.forward(tokens);
         x = pos_enc.forward_at(x, pos0);
-        for (size_t i = 0; i < blocks.size(); ++i) x = blocks[i]->forward_cached(x, caches[i]);
-        x = layernorm1.forward(x);
-        if (m_tied) return matmul(x, emb1.weight().transpose(0, 1), "logits");
-        return linear1->forward(static_cast<const Tensor&>(x));
+        // normed: the LayerNorm the next block (or the final one) reads
+        Tensor normed = (blocks.empty() ? layernorm1 : blocks[0]->layernorm1).forward(x);
+        for (size_t i = 0; i < blocks.size(); ++i) {
+            Tensor h;
+            Tensor mlp = blocks[i]->forward_cached(x, normed, caches[i], &h);
+            LayerNorm& next = i + 1 < blocks.size() ? blocks[i + 1]->layernorm1 : layernorm1;
+            normed = add_layer_norm(h, mlp, next.gamma(), next.beta(), next.eps(), &x);  // x = h + mlp
+        }
+        if (m_tied) return matmul(normed, emb1.weight().transpose(0, 1), "logits");
+        return linear1->forward(static_cast<const Tensor&>(normed));
     }
     size_t m_heads = 0, m_embed = 0;
     Embedding emb1;

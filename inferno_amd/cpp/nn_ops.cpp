@@ -526,6 +526,41 @@ Tensor layer_norm(const Tensor& x, const Tensor& gamma, const Tensor& beta, floa
     return out;
 }
 
+Tensor add_layer_norm(const Tensor& x, const Tensor& r, const Tensor& gamma, const Tensor& beta, float eps,
+                      Tensor* sum) {
+    if (!x.defined() || !r.defined() || !sum) throw Error("add_layer_norm: undefined input");
+    const bool req = grad_enabled && (x.requires_grad() || r.requires_grad() || gamma.requires_grad() ||
+                                      beta.requires_grad());
+    if (x.device().is_cpu() || req || x.shape() != r.shape() || x.dtype() != r.dtype()) {
+        *sum = x + r;
+        return layer_norm(*sum, gamma, beta, eps);
+    }
+    check_float(x, "add_layer_norm");
+    detail::same_device(x, r, "add_layer_norm");
+    detail::same_device(x, gamma, "add_layer_norm");
+    detail::same_device(x, beta, "add_layer_norm");
+    if (gamma.dtype() != DType::Float32 || beta.dtype() != DType::Float32)
+        throw Error("add_layer_norm: gamma and beta are Float32");
+    const size_t dim = x.ndim() ? x.shape().back() : 0;
+    if (!dim || gamma.numel() != dim || beta.numel() != dim) throw Error("add_layer_norm: parameter size mismatch");
+    Tensor xc = x.contiguous(), rc = r.contiguous(), gc = gamma.contiguous(), bc = beta.contiguous();
+    const size_t rows = xc.numel() / dim;
+    Tensor h(x.dtype(), x.shape(), "residual_sum", x.device(), false);
+    Tensor out(x.dtype(), x.shape(), "layernorm", x.device(), false);
+    if (rows) {
+        DeviceGuard dg(x.device().index);
+        status_check(inf_add_layernorm_fwd(xc.data_ptr(), (int64_t)dim, rc.data_ptr(), (int64_t)dim, h.data_ptr(),
+                                           (int64_t)dim, out.data_ptr(), (int64_t)dim,
+                                           static_cast<const float*>(gc.data_ptr()),
+                                           static_cast<const float*>(bc.data_ptr()), nullptr, nullptr, (int64_t)rows,
+                                           (int64_t)dim, eps, detail::inf_dt(x.dtype(), "add_layer_norm"),
+                                           detail::stream_of(x)),
+                     "inf_add_layernorm_fwd");
+    }
+    *sum = h;
+    return out;
+}
+
 LayerNormBackward::LayerNormBackward(const Tensor& x, const Tensor& gamma, const Tensor& beta, const Tensor& mean,
                                      const Tensor& invstd)
     : m_x(x), m_gamma(gamma), m_beta(beta), m_mean(mean), m_invstd(invstd) {

@@ -96,6 +96,22 @@ int inf_layernorm_fwd(const void* x, int64_t ldx, void* y, int64_t ldy, const fl
     return hip_status(inf::launch_ln_fwd(p, dt == INF_BF16, S(stream)));
 }
 
+int inf_add_layernorm_fwd(const void* x, int64_t ldx, const void* r, int64_t ldr, void* h, int64_t ldh, void* y,
+                          int64_t ldy, const float* gamma, const float* beta, float* mean, float* invstd, int64_t rows,
+                          int64_t dim, float eps, inf_dtype dt, void* stream) {
+    if (!dtype_ok(dt)) return INF_ERR_BAD_DTYPE;
+    if (rows < 0 || dim < 1 || dim > INT32_MAX) return INF_ERR_BAD_SHAPE;
+    if (rows == 0) return INF_OK;
+    if (!x || !r || !h || !y || !gamma || !beta) return INF_ERR_NULL_POINTER;
+    if (ldx < dim || ldr < dim || ldh < dim || ldy < dim) return INF_ERR_BAD_STRIDE;
+    if (!(eps >= 0.f) || !std::isfinite(eps)) return INF_ERR_BAD_SCALE;
+    const size_t va = 4 * (size_t)esz(dt);
+    const int vec = dim % 4 == 0 && ldx % 4 == 0 && ldr % 4 == 0 && ldh % 4 == 0 && ldy % 4 == 0 && aligned(x, va) &&
+                    aligned(r, va) && aligned(h, va) && aligned(y, va) && aligned(gamma, 16) && aligned(beta, 16);
+    inf::LnParams p{x, y, gamma, beta, mean, invstd, rows, ldx, ldy, (int)dim, eps, vec, r, h, ldr, ldh};
+    return hip_status(inf::launch_ln_fwd(p, dt == INF_BF16, S(stream)));
+}
+
 int inf_layernorm_bwd(const void* x, int64_t ldx, const void* dy, int64_t lddy, const float* gamma, const float* mean,
                       const float* invstd, void* dx, int64_t lddx, float* dgamma, float* dbeta, int accumulate,
                       int64_t rows, int64_t dim, inf_dtype dt, void* workspace, size_t ws_bytes, void* stream) {

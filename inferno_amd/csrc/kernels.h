@@ -146,6 +146,9 @@ struct LnParams {         // LayerNorm forward over rows of `dim` (unit column s
     int dim;
     float eps;
     int vec;              // 16-byte rows and parameters: the register kernel
+    const void* r;        // residual added to x first (null: plain LayerNorm) ...
+    void* h;              // ... and the sum x + r, stored in the element type
+    int64_t ldr, ldh;
 };
 
 struct LnBwdParams {

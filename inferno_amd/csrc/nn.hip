@@ -49,6 +49,16 @@ __device__ __forceinline__ float gelu_grad_f(float x) {
 // (layernorm_kernels.h:48-87).  One wave per row; lane l holds columns
 // 4*(64*i + l) .. +3 for i < VPT.
 // ============================================================================
+// With a residual (p.r), the row is first h = x + r, rounded to the element
+// type and stored to p.h, and the LayerNorm reads that rounded h: the same
+// values as an add kernel followed by this one.
+__device__ __forceinline__ f32x4 round_elem(f32x4 v, const float*) { return v; }
+__device__ __forceinline__ f32x4 round_elem(f32x4 v, const uint16_t*) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = bf16_to_f32(f32_to_bf16(v[k]));
+    return v;
+}
+
 template <int VPT, typename E>
 __global__ __launch_bounds__(256) void ln_fwd_kernel(LnParams p) {
     const int lane = threadIdx.x & 63;
@@ -62,6 +72,10 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(LnParams p) {
     for (int i = 0; i < VPT; ++i) {
         const int c = 4 * (64 * i + lane);
         v[i] = (c < dim) ? ld4(x + c) : f4(0.f);
+        if (p.r && c < dim) {
+            v[i] = round_elem(v[i] + ld4((const E*)p.r + row * p.ldr + c), x);
+            st4((E*)p.h + row * p.ldh + c, v[i]);
+        }
         s += hsum4(v[i]);
     }
     const float fdim = (float)dim;
@@ -103,7 +117,18 @@ __global__ __launch_bounds__(256) void ln_fwd_generic_kernel(LnParams p) {
     const int dim = p.dim;
     const typename E::T* x = (const typename E::T*)p.x + row * p.ldx;
     float s = 0.f;
-    for (int c = lane; c < dim; c += 64) s += E::ld(x + c);
+    if (p.r) {
+        // h = x + r first (each lane reads back only the columns it wrote)
+        const typename E::T* r = (const typename E::T*)p.r + row * p.ldr;
+        typename E::T* h = (typename E::T*)p.h + row * p.ldh;
+        for (int c = lane; c < dim; c += 64) {
+            E::st(h + c, E::ld(x + c) + E::ld(r + c));
+            s += E::ld(h + c);
+        }
+        x = h;
+    } else {
+        for (int c = lane; c < dim; c += 64) s += E::ld(x + c);
+    }
     const float mean = wave_sum(s) / (float)dim;
     float q = 0.f;
     for (int c = lane; c < dim; c += 64) {

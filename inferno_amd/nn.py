@@ -55,6 +55,18 @@ def layernorm_fwd(x, gamma, beta, eps=1e-5, stream=None):
     return y, mean, invstd
 
 
+def add_layernorm_fwd(x, r, gamma, beta, eps=1e-5, h=None, stream=None):
+    """h = x + r and y = LayerNorm(h) in one pass (inf_add_layernorm_fwd); h may be x or r."""
+    rows, dim = x.shape
+    h = torch.empty((rows, dim), dtype=x.dtype, device=x.device) if h is None else h
+    y = torch.empty((rows, dim), dtype=x.dtype, device=x.device)
+    st = lib().inf_add_layernorm_fwd(x.data_ptr(), _ld(x), r.data_ptr(), _ld(r), h.data_ptr(), _ld(h), y.data_ptr(),
+                                     _ld(y), gamma.data_ptr(), beta.data_ptr(), None, None, rows, dim, float(eps),
+                                     _dt(x), _stream(stream))
+    _check(st, "inf_add_layernorm_fwd")
+    return h, y
+
+
 def layernorm_bwd(x, dy, gamma, mean, invstd, stream=None):
     """dx, dgamma, dbeta of LayerNorm from the saved statistics."""
     rows, dim = x.shape

@@ -250,6 +250,22 @@ def test_static_decode_validation():
     assert ia.workspace_bytes(ia.OP_ATTN_DECODE, 1, 4032, 1, Tk, D) <= 4 << 20
 
 
+def test_add_layernorm_validation():
+    """inf_add_layernorm_fwd checks its arguments on the host before any HIP call."""
+    L = ia.lib()
+    F = FAKE
+    ok = (F, 64, F, 64, F, 64, F, 64, F, F, None, None, 4, 64, 1e-5, ia.INF_F32, None)
+    assert L.inf_add_layernorm_fwd(*ok[:12], 0, *ok[13:]) == 0  # no rows: nothing to do
+    args = list(ok); args[2] = None
+    assert L.inf_add_layernorm_fwd(*args) == 1  # r missing
+    args = list(ok); args[4] = None
+    assert L.inf_add_layernorm_fwd(*args) == 1  # h missing
+    args = list(ok); args[5] = 32
+    assert L.inf_add_layernorm_fwd(*args) == 3  # h rows shorter than dim
+    args = list(ok); args[15] = 7
+    assert L.inf_add_layernorm_fwd(*args) == 4  # dtype
+
+
 def test_decode_and_softmax_validation():
     L = ia.lib()
     s = dense(2, 2, 1, 64)

@@ -112,6 +112,25 @@ def test_layernorm_parity(ia, rows, dim):
         assert oracle.rel_err(host(db), dbr) < TOL
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("rows,dim", [(32, 768), (257, 770), (8, 4096)])
+def test_add_layernorm_equals_add_then_layernorm(ia, dtype, rows, dim):
+    """inf_add_layernorm_fwd gives bit for bit what an add followed by inf_layernorm_fwd gives
+    (register kernel for dim % 4 == 0, scalar kernel otherwise), also with h written over x."""
+    print(f"[case] add_layernorm {dtype} rows{rows} dim{dim}", flush=True)
+    x, r = dev(rnd(40, (rows, dim), 2.0), dtype), dev(rnd(41, (rows, dim)), dtype)
+    g, b = dev(rnd(42, (dim,)) + 1.0), dev(rnd(43, (dim,)))
+    h_ref = x + r  # torch rounds the fp32 sum to the tensor dtype, as the fused kernel does
+    y_ref, _, _ = ia.layernorm_fwd(h_ref, g, b)
+    h, y = ia.add_layernorm_fwd(x, r, g, b)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h_ref) and torch.equal(y, y_ref)
+    xi = x.clone()
+    h2, y2 = ia.add_layernorm_fwd(xi, r, g, b, h=xi)  # residual stream updated in place
+    torch.cuda.synchronize()
+    assert torch.equal(xi, h_ref) and torch.equal(y2, y_ref)
+
+
 # ----------------------------------------------------------------------- GELU
 @pytest.mark.parametrize("n", [8192 * 3072, 1, 4099])
 def test_gelu_parity(ia, n):
