@@ -352,6 +352,28 @@ def test_config4_long_context(ia, dtype, H):
         assert e <= (tol_lse if name == "LSE" else tol), f"full head {hf} {name} rel err {e:.3e}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("D", [32, 64])
+def test_sharp_softmax_small_head_dims(ia, dtype, D):
+    """Q, K ~ N(0, 3^2) (config 4's sharp softmax: row maxima far above the typical score, large
+    rescale steps in the online softmax) at D = 32 and 64, ragged T = 1200 over several key
+    blocks: the whole forward and backward against the oracle (bf16: on the bf16-rounded inputs)."""
+    print(f"[case] sharp softmax D{D} {dtype}", flush=True)
+    B, H, T = 1, 4, 1200
+    q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=77, qk_sigma=3.0)
+    bf = dtype == torch.bfloat16
+    if bf:
+        q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
+    o, lse, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do, dtype=dtype)
+    o_r, lse_r = oracle.attn_fwd(q, k, v)
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do)
+    tol = TOL_BF16 if bf else TOL_F32
+    assert oracle.rel_err(lse, lse_r) <= (1e-3 if bf else TOL_F32), "LSE"
+    for name, x, r in (("O", o, o_r), ("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
+        e = oracle.rel_err(x, r)
+        assert e <= tol, f"{name} rel err {e:.3e}"
+
+
 def test_bf16_query_major_dq(ia):
     """bf16 at D = 128 with many key blocks and a full grid takes dQ from the query-major pass
     (no atomics): B2 H8 T4096 D128.  Rows < 512 of O, LSE, dQ on two heads against the oracle
