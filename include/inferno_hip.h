@@ -262,8 +262,9 @@ int inf_layernorm_fwd(const void* x, int64_t ldx, void* y, int64_t ldy, const fl
  * add followed by inf_layernorm_fwd.  h may be x or r (updated in place); y
  * must not overlap x, r or h.  No reference counterpart: the reference runs
  * the transformer block's residual add and the next LayerNorm as two launches
- * (`x + attn(...)` then LayerNorm::forward, InfernoApp/main.cpp); this is for
- * inference loops, where each launch costs more than the row's work. */
+ * (`x = x + attn_out` then `layernorm2.forward(x)`, InfernoApp/main.cpp:868-874);
+ * this is for inference loops, where each launch costs more than the row's
+ * work. */
 int inf_add_layernorm_fwd(const void* x, int64_t ldx, const void* r, int64_t ldr, void* h, int64_t ldh, void* y,
                           int64_t ldy, const float* gamma, const float* beta, float* mean, float* invstd, int64_t rows,
                           int64_t dim, float eps, inf_dtype dt, void* stream);
