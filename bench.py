@@ -180,7 +180,7 @@ def main():
     ap.add_argument("--cpu-c4-heads", type=int, default=0,
                     help="time whole config-4 heads on the CPU instead of a row sample (over a minute each)")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16, config-3 and config-4 lines")
+    ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16 and deterministic, config-3 and config-4 lines")
     ap.add_argument("--gpt-steps", type=int, default=5, help="timed steps of the config-3 GPT line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 512 MiB device copy 5 times (HBM-counter calibration)")
@@ -319,6 +319,11 @@ def main():
             "c2_bf16": bench_attn(ia, oracle, torch, np, dev, 8, 12, 1024, 64, 1.0, "bf16"),
             "c4_f32": bench_attn(ia, oracle, torch, np, dev, 1, 16, 8192, 128, 3.0, "f32", steps=5),
             "c4_bf16": bench_attn(ia, oracle, torch, np, dev, 1, 16, 8192, 128, 3.0, "bf16", steps=5),
+            # the opt-in deterministic-dQ mode (query-major dQ pass, no atomics) at config 2
+            "c2_f32_deterministic": bench_attn(ia, oracle, torch, np, dev, 8, 12, 1024, 64, 1.0, "f32",
+                                               deterministic=True),
+            "c2_bf16_deterministic": bench_attn(ia, oracle, torch, np, dev, 8, 12, 1024, 64, 1.0, "bf16",
+                                                deterministic=True),
         }
         torch.cuda.empty_cache()
         out["configs"]["c3_gpt"] = bench_gpt(args.gpt_steps)
@@ -342,10 +347,22 @@ def warm_up(fn, torch, seconds=0.2):
                 return n
 
 
-def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10):
+def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10, deterministic=False):
     """One attention config: fwd+bwd throughput over `steps` back-to-back steps between two
     synchronizations (as `value`), and the fwd / bwd breakdown from HIP events recorded on the
-    launch stream around each call in a second pass (the events add the launch gaps)."""
+    launch stream around each call in a second pass (the events add the launch gaps).  With
+    `deterministic`, the backward runs in the deterministic-dQ mode (inf_set_deterministic)."""
+    previous = ia.set_deterministic(deterministic)
+    try:
+        r = _bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps)
+    finally:
+        ia.set_deterministic(previous)
+    if deterministic:
+        r["deterministic_dq"] = True
+    return r
+
+
+def _bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps):
     tdt = torch.float32 if dtype == "f32" else torch.bfloat16
     q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=42, qk_sigma=qk_sigma)
     Q, K, V, dO = (torch.from_numpy(x).to(dev, tdt) for x in (q, k, v, do))

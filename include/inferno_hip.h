@@ -109,7 +109,8 @@ int inf_attn_fwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
  * multiplybackward.cpp:34-57, transposebackward.cpp:35-51).
  * workspace: at least inf_attn_workspace_bytes(INF_OP_ATTN_BWD, ...) bytes,
  * 256-byte aligned; its contents on entry do not matter.  It holds the row
- * dots dO.O, the fp32 dQ accumulator (bf16), and, for causal shapes whose
+ * dots dO.O, the fp32 dQ accumulator (bf16, unless dq comes from the
+ * query-major pass: inf_set_deterministic), and, for causal shapes whose
  * grid leaves the device unevenly loaded, the partial dK / dV of split key
  * blocks and their arrival counters.  Calls that share one workspace must not
  * overlap.
@@ -120,6 +121,22 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
                  inf_strides sdk, void* dv, inf_strides sdv, void* workspace, size_t ws_bytes,
                  int B, int H, int Tq, int Tk, int D, float scale, int causal, inf_dtype dt,
                  void* stream);
+
+/*
+ * Deterministic dQ (process-wide, off by default; no counterpart in the
+ * reference, whose CPU path sums dQ in a fixed order, cpuops.h:412-431).
+ * inf_attn_bwd normally adds each key block's dQ contribution with fp32
+ * atomics, so the last bits of dq may differ between runs (O, LSE, dK and dV
+ * never do).  With enable != 0, every later inf_attn_bwd call takes dq from a
+ * query-major pass instead: one workgroup per query tile recomputes the
+ * scores and sums its key tiles in key order, the same on every run, at the
+ * cost of two more matrix products per score.  The mode is read once per
+ * call; the backward's workspace size depends on it (bf16 then needs no dQ
+ * accumulator), so query inf_attn_workspace_bytes after setting it.  Returns
+ * the previous setting.
+ */
+int inf_set_deterministic(int enable);
+int inf_get_deterministic(void);
 
 /*
  * Row softmax over the last axis: y = softmax(x) per row of `cols` elements

@@ -66,6 +66,8 @@ EXPORTS = (
     "inf_binary_bcast",
     "inf_argmax_rows",
     "inf_attn_decode_static",
+    "inf_set_deterministic",
+    "inf_get_deterministic",
     "inf_last_error_detail",
 )
 
@@ -154,6 +156,8 @@ def lib() -> ctypes.CDLL:
         L.inf_binary_bcast.argtypes = [i32, vp, vp, vp, i64, i64, i32, vp]
         L.inf_argmax_rows.argtypes = [vp, i64, i64, i64, vp, i32, vp]
         L.inf_attn_decode_static.argtypes = [vp, S, vp, S, vp, S, vp, S, i32, i32, i32, i32, f32, i32, vp]
+        L.inf_set_deterministic.argtypes = [i32]
+        L.inf_get_deterministic.argtypes = []
         for name in EXPORTS[11:-1]:
             getattr(L, name).restype = i32
         L.inf_last_error_detail.argtypes = []
@@ -183,6 +187,17 @@ def nn_workspace_bytes(op: int, rows: int = 0, cols: int = 0) -> int:
     if st:
         raise InfernoError(st, "inf_nn_workspace_bytes")
     return int(out.value)
+
+
+def set_deterministic(enable: bool) -> bool:
+    """Process-wide switch (inf_set_deterministic): every later attention backward takes dQ
+    from the query-major pass, bitwise the same on every run.  Returns the previous setting."""
+    return bool(lib().inf_set_deterministic(1 if enable else 0))
+
+
+def deterministic() -> bool:
+    """Whether the attention backward runs in the deterministic-dQ mode."""
+    return bool(lib().inf_get_deterministic())
 
 
 def default_scale(D: int) -> float:
@@ -229,6 +244,8 @@ __all__ = [
     "softmax_bwd",
     "strides_of",
     "workspace_bytes",
+    "set_deterministic",
+    "deterministic",
     "default_scale",
     "InfernoError",
     "EXPORTS",

@@ -289,11 +289,18 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
         } else {
             ds = f32x16{};
         }
-        // dS block of this wave -> LDS (rows = queries, columns = the 128 keys)
+        // dS block of this wave -> LDS (rows = queries, columns = the 128 keys);
+        // with the query-major dQ pass (dq_direct) there is no dQ product here
+        if (!p.dq_direct) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dSs[8 * (r >> 2) + 4 * g + (r & 3)][wave * 32 + l32] = ds[r];
+            for (int r = 0; r < 16; ++r) dSs[8 * (r >> 2) + 4 * g + (r & 3)][wave * 32 + l32] = ds[r];
+        }
         __syncthreads();
         if constexpr (PF) sstore_q();  // the next tile (zeros after the last one, never read)
+        if (p.dq_direct) {
+            __syncthreads();
+            continue;
+        }
 
         // ---- dQ tile (32 x D) += dS (32 x BK) K (BK x D) ---------------------
         // Each wave takes NDQ / NW adjacent 16x16 blocks; lane group g4
@@ -360,6 +367,175 @@ __global__ __launch_bounds__(256) void bwd_cvt_kernel(BwdParams p) {
     const f32x4 a = *reinterpret_cast<const f32x4*>(p.dq_acc + b * p.sacc.b + h * p.sacc.h +
                                                      i * p.sacc.t + 4 * c4);
     st4((uint16_t*)p.dq + b * p.sdq.b + h * p.sdq.h + i * p.sdq.t + 4 * c4, a);
+}
+
+// Query-major dQ pass, fp32 (the deterministic mode: the main kernel then
+// skips its dQ product).  One workgroup = 4 waves x 32 query rows of one
+// (b, h), laid out as the forward: each lane keeps its query row of Q and dO
+// as the B operand (Q^T, dO^T) in VGPRs, with that row's log-sum-exp and
+// delta; tiles of 32 keys stream through LDS as K and V rows and K^T
+// (double-buffered, one barrier per tile).  Per wave and tile:
+//   S^T = K Q^T, dP^T = V dO^T        v_mfma_f32_32x32x2_f32, A from LDS
+//   P^T = exp2(S^T c - lse log2 e), dS^T = P^T (dP^T - delta)
+//   dQ^T += K^T dS^T                  B = dS^T straight from the accumulators
+//                                     (as the forward feeds P^T to P V)
+// dQ stays in VGPRs and is stored once, times the scale: every element is the
+// sum of its key tiles in key order, with no accumulator, zeroing or atomics,
+// so the result is the same on every run.  It recomputes S and dP (two more
+// products per score than the atomic dQ of the main kernel).
+template <int D>
+__global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void bwd_dq_kernel(BwdParams p) {
+    constexpr int BM = kBwdDqBM;
+    constexpr int BN = 32;               // keys per tile
+    constexpr int HD = D / 2;            // reduction elements per lane half
+    constexpr int NDB = D / 32;          // 32-wide d blocks of dQ^T
+    constexpr int C4 = D / 4;            // 4-element chunks per row
+    constexpr int KS = D + 4;            // K / V row stride in LDS (floats)
+    constexpr int TS = BN + 4;           // K^T row stride in LDS (floats)
+    constexpr int LPT = BN * C4 / 256;   // 4-element loads per thread per tensor per tile
+    static_assert(BM == 128 && BN * C4 % 256 == 0, "4 waves x 32 rows, whole staging passes");
+    static_assert(256 % C4 == 0, "chunk rows must split into thread + load parts");
+
+    __shared__ __attribute__((aligned(16))) float Ks[2][BN][KS];
+    __shared__ __attribute__((aligned(16))) float Vs[2][BN][KS];
+    __shared__ __attribute__((aligned(16))) float Kt[2][D][TS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+
+    const int BH = p.B * p.H;
+    const int w = blockIdx.x;
+    const int qtile = p.n_qtiles - 1 - w / BH;  // the longest causal rows first
+    const int bh = w % BH;
+    const int b = bh / p.H;
+    const int h = bh % p.H;
+
+    const float* Q = (const float*)p.q + b * p.sq.b + h * p.sq.h;
+    const float* K = (const float*)p.k + b * p.sk.b + h * p.sk.h;
+    const float* V = (const float*)p.v + b * p.sv.b + h * p.sv.h;
+    const float* dO = (const float*)p.dout + b * p.sdo.b + h * p.sdo.h;
+
+    const int q0w = qtile * BM + wave * 32;
+    const int qrow = q0w + l32;
+    // B operands: lane (l32, g) holds row qrow, columns g*HD + i.
+    float qf[HD], df[HD];
+    if (qrow < p.Tq) {
+        const float* qs = Q + (int64_t)qrow * p.sq.t + g * HD;
+        const float* ds = dO + (int64_t)qrow * p.sdo.t + g * HD;
+#pragma unroll
+        for (int i = 0; i < HD; i += 4) {
+            const f32x4 a = ld4(qs + i);
+            const f32x4 c = ld4(ds + i);
+            qf[i] = a[0]; qf[i + 1] = a[1]; qf[i + 2] = a[2]; qf[i + 3] = a[3];
+            df[i] = c[0]; df[i + 1] = c[1]; df[i + 2] = c[2]; df[i + 3] = c[3];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < HD; ++i) qf[i] = df[i] = 0.f;
+    }
+    const float Lq = qrow < p.Tq ? p.lse[(int64_t)bh * p.Tq + qrow] * kLog2e : 0.f;
+    const float Dq = qrow < p.Tq ? p.delta[(int64_t)bh * p.Tq + qrow] : 0.f;
+
+    int kv_end = p.Tk;
+    if (p.causal) kv_end = min(p.Tk, qtile * BM + BM + p.off);
+    const int nt = (kv_end + BN - 1) / BN;
+    const int wave_kend = p.causal ? min(kv_end, q0w + 32 + p.off) : kv_end;
+
+    // Chunk f of a tile -> (row f / C4, column chunk f % C4); chunk tid + 256 i
+    // is 256 i / C4 rows below chunk tid.  Rows at or past the resource's end
+    // (<= Tk) read as zeros.
+    f32x4 kr[LPT], vr[LPT];
+    const uint32_t k_voff = (uint32_t)(((int64_t)(tid / C4) * p.sk.t + 4 * (tid % C4)) * 4);
+    const uint32_t v_voff = (uint32_t)(((int64_t)(tid / C4) * p.sv.t + 4 * (tid % C4)) * 4);
+    auto gload = [&](int u) {
+        const int rows = u < nt ? min(p.Tk - u * BN, BN) : 0;
+        const auto rk = row_rsrc(K, p.sk.t, u * BN, rows, D);
+        const auto rv = row_rsrc(V, p.sv.t, u * BN, rows, D);
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            kr[i] = buffer_ld4(rk, k_voff, (uint32_t)((int64_t)(256 * i / C4) * p.sk.t * 4));
+            vr[i] = buffer_ld4(rv, v_voff, (uint32_t)((int64_t)(256 * i / C4) * p.sv.t * 4));
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LPT; ++i) {
+            const int f = tid + 256 * i;
+            const int r = f / C4, c4 = f % C4;
+            *reinterpret_cast<f32x4*>(&Ks[buf][r][4 * c4]) = kr[i];
+            *reinterpret_cast<f32x4*>(&Vs[buf][r][4 * c4]) = vr[i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Kt[buf][4 * c4 + e][r] = kr[i][e];
+        }
+    };
+
+    f32x16 dq[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) dq[i] = f32x16{};
+    const float c = p.c;
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int u = 0; u < nt; ++u) {
+        const int buf = u & 1;
+        const int k0 = u * BN;
+        gload(u + 1);  // zero rows past the last tile: straight-line
+        if (k0 < wave_kend) {
+            f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+            for (int i = 0; i < HD; i += 4) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(&Ks[buf][l32][g * HD + i]);
+                const f32x4 v = *reinterpret_cast<const f32x4*>(&Vs[buf][l32][g * HD + i]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    s = mfma32x32x2(a[j], qf[i + j], s);
+                    dp = mfma32x32x2(v[j], df[i + j], dp);
+                }
+            }
+            // reg r: key k0 + 8 (r / 4) + 4 g + r % 4 of query qrow
+            const bool need_mask = (k0 + BN > p.Tk) || (qtile * BM + BM > p.Tq) || (p.causal && (k0 + BN - 1 > q0w + p.off));
+            const int lim = p.causal ? min(p.Tk - 1, qrow + p.off) : p.Tk - 1;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float pr = fast_exp2(fmaf(s[r], c, -Lq));
+                if (need_mask) {
+                    const int key = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    pr = (key <= lim && qrow < p.Tq) ? pr : 0.f;
+                }
+                s[r] = pr * (dp[r] - Dq);  // dS^T
+            }
+            // dQ^T[d][q] += K^T[d][keys] dS^T[keys][q]: MFMA (j, cc) reduces keys 8j + cc, 8j + 4 + cc
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f32x4 kt[NDB];
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+                    kt[db] = *reinterpret_cast<const f32x4*>(&Kt[buf][db * 32 + l32][8 * j + 4 * g]);
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) dq[db] = mfma32x32x2(kt[db][cc], s[4 * j + cc], dq[db]);
+            }
+        }
+        sstore(buf ^ 1);
+        __syncthreads();
+    }
+    if (qrow < p.Tq) {
+        float* dst = (float*)p.dq + b * p.sdq.b + h * p.sdq.h + (int64_t)qrow * p.sdq.t;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f32x4 val;
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) val[cc] = dq[db][4 * j + cc] * p.scale;
+                st4(dst + db * 32 + 8 * j + 4 * g, val);
+            }
+    }
 }
 
 // ---- split plan (host) ------------------------------------------------------------
@@ -587,6 +763,8 @@ static int launch_bwd_t(const BwdParams& p, hipStream_t s) {
     } else {
         const dim3 grid((unsigned)(p.n_groups ? p.n_groups * bwd_padded_heads(p.B * p.H) : p.n_kblocks * p.B * p.H));
         hipLaunchKernelGGL((bwd_main_kernel<D, E>), grid, dim3(64 * bwd_waves(0, D)), 0, s, p);
+        if (p.dq_direct)
+            hipLaunchKernelGGL((bwd_dq_kernel<D>), dim3((unsigned)(p.n_qtiles * p.B * p.H)), dim3(256), 0, s, p);
     }
     return (int)hipGetLastError();
 }

@@ -706,10 +706,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
     constexpr int NKB = BN / 32;
     constexpr int NDB = D / 32;
     constexpr int C8 = D / 8;
-    constexpr int KTASK = (BN / 2) * C8;  // (key pair, chunk) tasks
+    constexpr int KTASK = (BN / 2) * C8;  // (key pair, chunk) tasks: 128 at D = 32, else 256
     constexpr int KLPT = (KTASK + 255) / 256;
     constexpr int VLPT = BN * C8 / 256;
-    static_assert(BN * C8 % 256 == 0 && KTASK % 256 == 0, "whole staging passes");
+    static_assert(BN * C8 % 256 == 0 && (KTASK % 256 == 0 || KTASK == 128), "whole staging passes");
 
     __shared__ __attribute__((aligned(16))) __bf16 Ks[2][BN][KS];
     __shared__ __attribute__((aligned(16))) __bf16 Vs[2][BN][KS];
@@ -758,6 +758,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
     const __bf16* vt = V;
     bf16x8 ka[KLPT], kb2[KLPT], vr[VLPT];
     const int kp = tid % (BN / 2), kc8 = tid / (BN / 2);
+    const bool k_task = tid < KTASK;  // D = 32: threads 128..255 stage no K
     const uint32_t k_voff = (uint32_t)(((int64_t)(2 * kp) * p.sk.t + 8 * kc8) * 2);
     const uint32_t v_voff = (uint32_t)(((int64_t)(tid / C8) * p.sv.t + 8 * (tid % C8)) * 2);
     auto gload = [&](int rows) {
@@ -766,6 +767,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
 #pragma unroll
         for (int i = 0; i < KLPT; ++i) {
             const uint32_t col = (uint32_t)(8 * (256 * i / (BN / 2)) * 2);
+            ka[i] = kb2[i] = bf16x8{};
+            if (!k_task) continue;
             ka[i] = buffer_ld8bf(rk, k_voff, col);
             kb2[i] = buffer_ld8bf(rk, k_voff, col + (uint32_t)(p.sk.t * 2));
         }
@@ -778,6 +781,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
         const int pos = (k & ~15) | ((k & 4) << 1) | ((k & 8) >> 1) | (k & 3);
 #pragma unroll
         for (int i = 0; i < KLPT; ++i) {
+            if (!k_task) continue;
             const int c8 = kc8 + 256 * i / (BN / 2);
             *reinterpret_cast<bf16x8*>(&Ks[buf][k][8 * c8]) = ka[i];
             *reinterpret_cast<bf16x8*>(&Ks[buf][k + 1][8 * c8]) = kb2[i];
@@ -881,6 +885,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
 int launch_bwd_dq_bf16(const BwdParams& p, hipStream_t s) {
     const dim3 grid((unsigned)(p.n_qtiles * p.B * p.H));
     switch (p.D) {
+        case 32: hipLaunchKernelGGL((bwd_dq_bf16_kernel<32>), grid, dim3(256), 0, s, p); break;
+        case 64: hipLaunchKernelGGL((bwd_dq_bf16_kernel<64>), grid, dim3(256), 0, s, p); break;
         case 128: hipLaunchKernelGGL((bwd_dq_bf16_kernel<128>), grid, dim3(256), 0, s, p); break;
         default: return (int)hipErrorInvalidValue;
     }

@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -18,6 +19,16 @@
 namespace {
 
 constexpr size_t kAlign = 256;
+
+// inf_set_deterministic: every backward takes dQ from the query-major pass.
+std::atomic<int> g_deterministic{0};
+
+// Whether a backward of this shape takes dQ from the query-major pass: always
+// in the deterministic mode, else bf16 shapes where the atomics bound the
+// fused kernel (bwd_dq_direct).
+bool dq_from_pass(int det, int B, int H, int Tq, int Tk, int D, inf_dtype dt) {
+    return det || (dt == INF_BF16 && inf::bwd_dq_direct(B * H, Tq, Tk, D, inf::bwd_keys_per_wg(1, D)));
+}
 
 size_t round_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
@@ -109,6 +120,23 @@ const char* inf_status_string(int status) {
 
 int inf_version(void) { return 200; }
 
+int inf_set_deterministic(int enable) { return g_deterministic.exchange(enable ? 1 : 0); }
+int inf_get_deterministic(void) { return g_deterministic.load(); }
+
+namespace {
+
+size_t bwd_workspace_bytes(int det, int B, int H, int Tq, int Tk, int D, inf_dtype dt) {
+    const size_t bh = (size_t)B * H;
+    size_t n = round_up(bh * Tq * sizeof(float));  // delta
+    if (dt == INF_BF16 && !dq_from_pass(det, B, H, Tq, Tk, D, dt))
+        n += round_up(bh * Tq * (size_t)D * sizeof(float));  // dQ accumulator
+    inf::BwdPlan plan;                                        // causal split plan
+    inf::bwd_plan(B, H, Tq, Tk, D, 1, dt == INF_BF16, &plan);
+    return n + round_up(inf::bwd_split_workspace_bytes(plan, B, H, D));
+}
+
+}  // namespace
+
 int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dtype dt,
                              size_t* out_bytes) {
     if (!out_bytes) return INF_ERR_NULL_POINTER;
@@ -124,16 +152,9 @@ int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dt
             *out_bytes = round_up(inf::fwd_workspace_bytes(plan, B, H, D));
             return INF_OK;
         }
-        case INF_OP_ATTN_BWD: {
-            size_t n = round_up(bh * Tq * sizeof(float));                       // delta
-            if (dt == INF_BF16 && !inf::bwd_dq_direct(B * H, Tq, Tk, D, inf::bwd_keys_per_wg(1, D)))
-                n += round_up(bh * Tq * (size_t)D * sizeof(float));  // dQ accumulator
-            inf::BwdPlan plan;                                                  // causal split plan
-            inf::bwd_plan(B, H, Tq, Tk, D, 1, dt == INF_BF16, &plan);
-            n += round_up(inf::bwd_split_workspace_bytes(plan, B, H, D));
-            *out_bytes = n;
+        case INF_OP_ATTN_BWD:
+            *out_bytes = bwd_workspace_bytes(g_deterministic.load(), B, H, Tq, Tk, D, dt);
             return INF_OK;
-        }
         case INF_OP_ATTN_DECODE: {
             int ns = 1, ch = 0;
             inf::decode_plan(B, H, Tk, D, &ns, &ch);
@@ -196,8 +217,8 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
         (st = check_view(dout, sdo, dt)) || (st = check_out_view(dq, sdq, dt, B, H, Tq, D)) ||
         (st = check_out_view(dk, sdk, dt, B, H, Tk, D)) || (st = check_out_view(dv, sdv, dt, B, H, Tk, D)))
         return st;
-    size_t need = 0;
-    inf_attn_workspace_bytes(INF_OP_ATTN_BWD, B, H, Tq, Tk, D, dt, &need);
+    const int det = g_deterministic.load();  // one reading for the whole call
+    const size_t need = bwd_workspace_bytes(det, B, H, Tq, Tk, D, dt);
     if (!workspace || ws_bytes < need) return INF_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(workspace) % kAlign) return INF_ERR_ALIGNMENT;
 
@@ -223,7 +244,7 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     p.c = scale * 1.4426950408889634f;
     const int bk = inf::bwd_keys_per_wg(dt == INF_BF16, D);
     p.n_kblocks = (Tk + bk - 1) / bk;
-    p.dq_direct = dt == INF_BF16 && inf::bwd_dq_direct(B * H, Tq, Tk, D, bk);
+    p.dq_direct = dq_from_pass(det, B, H, Tq, Tk, D, dt) ? 1 : 0;
     p.n_qtiles = (Tq + inf::kBwdDqBM - 1) / inf::kBwdDqBM;
     if (p.dq_direct) p.dq_acc = nullptr;  // dq is written by the dQ pass
     inf::BwdPlan plan;

@@ -115,6 +115,33 @@ def test_workspace_sizes():
         ia.workspace_bytes(9, 1, 1, 8, 8, 64)
 
 
+def test_deterministic_switch_and_workspace():
+    """inf_set_deterministic returns the previous setting; in the mode, bf16 needs no fp32 dQ
+    accumulator (dq comes from the query-major pass), fp32 the same delta / split workspace."""
+    L = ia.lib()
+    assert not ia.deterministic()
+    shapes = [(8, 12, 1024, 1024, 64), (1, 4, 1024, 1024, 64), (2, 3, 300, 300, 32), (1, 2, 500, 700, 128)]
+    before = {(dt, s): ia.workspace_bytes(ia.OP_ATTN_BWD, *s, dt) for dt in (ia.INF_F32, ia.INF_BF16) for s in shapes}
+    try:
+        assert ia.set_deterministic(True) is False
+        assert ia.deterministic() and L.inf_get_deterministic() == 1
+        assert L.inf_set_deterministic(7) == 1 and L.inf_get_deterministic() == 1  # any non-zero value: on
+        for (dt, s), n in before.items():
+            B, H, Tq = s[0], s[1], s[2]
+            det = ia.workspace_bytes(ia.OP_ATTN_BWD, *s, dt)
+            acc = (B * H * Tq * s[4] * 4 + 255) // 256 * 256
+            assert det == (n - acc if dt == ia.INF_BF16 else n), (dt, s, n, det)
+        # validation is unchanged in the mode (no GPU call is reached)
+        st = dense(1, 1, 8, 64)
+        args = [FAKE, st] * 5 + [FAKE] + [FAKE, st] * 3
+        assert L.inf_attn_bwd(*args, None, 0, 1, 1, 8, 8, 64, 0.125, 1, ia.INF_F32, None) == 6
+        assert L.inf_attn_bwd(*args, FAKE, 1 << 20, 1, 1, 8, 8, 96, 0.125, 1, ia.INF_F32, None) == 5
+    finally:
+        assert ia.set_deterministic(False) is True
+    assert not ia.deterministic()
+    assert all(ia.workspace_bytes(ia.OP_ATTN_BWD, *s, dt) == n for (dt, s), n in before.items())
+
+
 @pytest.mark.parametrize("dt,B,H,T,D,splits", [
     (ia.INF_F32, 8, 12, 1024, 64, False),    # config 2: more workgroups than resident slots
     (ia.INF_F32, 4, 12, 1024, 64, True),
