@@ -179,6 +179,8 @@ def main():
     ap.add_argument("--cpu-c4-rows", type=int, default=512, help="config-4 query rows timed on the CPU")
     ap.add_argument("--cpu-c4-heads", type=int, default=0,
                     help="time whole config-4 heads on the CPU instead of a row sample (over a minute each)")
+    ap.add_argument("--deterministic", action="store_true",
+                    help="run the main line's backward in the deterministic-dQ mode (inf_set_deterministic)")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16 and deterministic, config-3 and config-4 lines")
     ap.add_argument("--gpt-steps", type=int, default=5, help="timed steps of the config-3 GPT line")
@@ -211,6 +213,7 @@ def main():
     B, H, T, D = 8, 12, 1024, 64
     dt = torch.float32 if args.dtype == "f32" else torch.bfloat16
     dev = torch.device("cuda:0")
+    ia.set_deterministic(args.deterministic)  # before sizing the backward's workspace
     q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=42)
     if args.dtype == "bf16":
         q, k, v, do = (oracle.bf16_to_f32(oracle.round_bf16(x)) for x in (q, k, v, do))
@@ -288,6 +291,7 @@ def main():
         "config": {"workload": "causal self-attention fwd+bwd, B=8 H=12 T=1024 D=64 (BASELINE config 2)",
                    "B": B, "H": H, "T": T, "D": D, "causal": True, "scale": ia.default_scale(D)},
         "frac_of_peak": round(value / peak, 4),
+        "deterministic_dq": bool(args.deterministic),
         "timings": {"fwd": pct(fwd_all), "bwd": pct(bwd_all), "fwd+bwd": pct(step_all)},
         "roofline": {
             "bound": "mfma",
@@ -310,6 +314,13 @@ def main():
         },
     }
 
+    if args.deterministic:
+        # the query-major dQ pass replaces the atomic dQ product (and, for bf16, the conversion
+        # pass); the counter-measured traffic above is the default mode's
+        out["roofline"]["kernel"] = "bwd: bwd_pre + bwd_main (no dQ) + bwd_dq (one inf_attn_bwd call)"
+        out["roofline"]["traffic"] = None
+        del out["roofline"]["traffic_by_kernel"]
+        ia.set_deterministic(False)
     if not args.no_decode:
         out["decode"] = bench_decode(ia, oracle, torch, np, dev)
     if not args.no_extras:
