@@ -271,6 +271,35 @@ def test_strided_qkv_view(ia, dtype, D, T):
         assert e <= tol, f"{name} rel err {e:.3e}"
 
 
+@pytest.mark.parametrize("D,T", [(64, 150), (32, 97), (128, 130)])
+def test_bf16_rows_8_byte_aligned(ia, D, T):
+    """bf16 views whose rows are 8- but not 16-byte aligned (the C-ABI's minimum): O, dO and dq
+    at a 4-element offset in their buffers; dq against the oracle, and equal to that of
+    aligned views within one bf16 rounding step (its fp32 atomic sum is order-dependent)."""
+    print(f"[case] bf16 8-byte aligned rows D{D} T{T}", flush=True)
+    B, H = 2, 2
+    q, k, v, do = (bf16_round(x) for x in oracle.attn_inputs(B, H, T, D, seed=23))
+    Q, K, V, dO = (dev(x, torch.bfloat16) for x in (q, k, v, do))
+    o, lse = ia.attn_fwd(Q, K, V)
+    n = B * H * T * D
+
+    def shifted(t):
+        buf = torch.full((n + 4,), float("nan"), device="cuda", dtype=torch.bfloat16)
+        view = buf[4:].view(B, H, T, D)
+        if t is not None:
+            view.copy_(t)
+        assert view.data_ptr() % 16 == 8
+        return view
+
+    o8, do8, dq8 = shifted(o), shifted(dO), shifted(None)
+    ia.attn_bwd(Q, K, V, o8, do8, lse, dq=dq8)
+    dq, dk, dv = ia.attn_bwd(Q, K, V, o, dO, lse)
+    torch.cuda.synchronize()
+    dq_r, _, _ = oracle.attn_bwd(q, k, v, do)
+    assert oracle.rel_err(host(dq8), dq_r) <= TOL_BF16
+    assert oracle.rel_err(host(dq8), host(dq)) <= 1e-2
+
+
 def test_config2_full_size_heads(ia):
     """Config 2 (B8 H12 T1024 D64) at full size on the GPU; three heads checked against the oracle."""
     print("[case] config2 full size", flush=True)
