@@ -108,6 +108,44 @@ def test_deterministic_parity(ia, dt, causal, B, H, Tq, Tk, D):
     assert oracle.rel_err(host(first[0]), host(base[0]), floor=1e-2) <= (1e-2 if bf else 1e-5)
 
 
+def _random_cases(n=16, seed=77):
+    """Seeded draws: B, H, ragged Tq <= Tk (causal, end-aligned) or any Tq, Tk (non-causal),
+    D in {32, 64, 128}, fp32 and bf16 alternating."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        causal = bool(rng.integers(0, 4))
+        D = int(rng.choice([32, 64, 128]))
+        B, H = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+        Tq = int(rng.integers(1, 600))
+        Tk = Tq + int(rng.integers(0, 300)) if causal else int(rng.integers(1, 700))
+        cases.append(("bf16" if i % 2 else "f32", causal, B, H, Tq, Tk, D))
+    return cases
+
+
+@pytest.mark.parametrize("dt,causal,B,H,Tq,Tk,D", _random_cases())
+def test_deterministic_random_shapes(ia, dt, causal, B, H, Tq, Tk, D):
+    """The mode at seeded random shapes: dQ against the oracle and bit-identical on a second call."""
+    print(f"[case] deterministic random {dt} causal={causal} B{B} H{H} Tq{Tq} Tk{Tk} D{D}", flush=True)
+    bf = dt == "bf16"
+    dtype = torch.bfloat16 if bf else torch.float32
+    q, k, v, do = oracle.attn_inputs(B, H, Tq, D, seed=1300 + Tq + 5 * Tk + D, Tk=Tk)
+    if bf:
+        q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do, causal=causal)
+    Q, K, V, dO = (dev(x, dtype) for x in (q, k, v, do))
+    ia.set_deterministic(True)
+    o, lse = ia.attn_fwd(Q, K, V, causal=causal)
+    first = bwd(ia, Q, K, V, o, dO, lse, causal)
+    second = bwd(ia, Q, K, V, o, dO, lse, causal)
+    torch.cuda.synchronize()
+    tol = TOL_BF16 if bf else TOL_F32
+    for name, x, r in zip(("dQ", "dK", "dV"), first, (dq_r, dk_r, dv_r)):
+        e = oracle.rel_err(host(x), r, floor=1e-2)
+        assert e <= tol, f"{name} rel err {e:.3e}"
+    assert torch.equal(first[0], second[0]), "dQ differs between two deterministic calls"
+
+
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_deterministic_config2_full_size(ia, dt):
     """Config 2 (B8 H12 T1024 D64) in the mode: three heads against the oracle, dQ of every head
