@@ -8,12 +8,14 @@
 // is given, in which case it is the reference's separate Linear "linear1".
 //
 //   gpt bench [--layers L] [--dmodel C] [--heads H] [--ctx T] [--vocab V]
-//             [--batch B] [--steps K] [--warmup W] [--untied]
+//             [--batch B] [--steps K] [--warmup W] [--untied] [--deterministic]
 //       random-init weights N(0, 0.02) (biases 0, LayerNorm gamma 1 / beta 0),
 //       tokens uniform in [0, V), targets = tokens shifted by one, AdamW
 //       lr 3e-4; times K training steps (forward, cross-entropy, backward,
 //       AdamW, zero_grad) on hip:0 and prints one JSON line with tokens/s and
-//       the attention share of the step time.
+//       the attention share of the step time.  --deterministic (any command)
+//       takes the attention backward's dQ from the query-major pass
+//       (inf_set_deterministic), the same bits on every run.
 //   gpt generate [--layers L] [--dmodel C] [--heads H] [--vocab V] [--ctx T]
 //                [--batch B] [--prompt P] [--new N]
 //       greedy generation with one KV cache per layer on hip:0 (prefill of a
@@ -29,6 +31,8 @@
 //       training step; writes loss.bin, grad_<name>.bin (before the update) and
 //       param_<name>.bin (after it).
 #include <hip/hip_runtime_api.h>
+
+#include "inferno_hip.h"
 
 #include <algorithm>
 #include <chrono>
@@ -673,6 +677,7 @@ static int run_bench(int argc, char** argv) {
 
 int main(int argc, char** argv) {
     try {
+        if (flag(argc, argv, "--deterministic")) inf_set_deterministic(1);
         if (argc >= 2 && std::strcmp(argv[1], "bench") == 0) return run_bench(argc, argv);
         if (argc >= 2 && std::strcmp(argv[1], "generate") == 0) return run_generate(argc, argv);
         if (argc >= 4 && std::strcmp(argv[1], "decode-check") == 0) {

@@ -37,10 +37,10 @@ def make_case(tmp_path, L, C, H, T, V, B, seed=7):
     return params, tokens, targets
 
 
-def run_app(tmp_path, device):
+def run_app(tmp_path, device, *extra):
     if not APP.exists():
         pytest.skip("inferno_amd/gpt not built (run __graft_entry__.build())")
-    r = subprocess.run([str(APP), "step", str(tmp_path), device], capture_output=True, text=True, timeout=600)
+    r = subprocess.run([str(APP), "step", str(tmp_path), device, *extra], capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stdout + r.stderr
 
 
@@ -102,11 +102,14 @@ def test_gpt_step_cpu_matches_oracle(tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("L,C,H,T,V,B", [(2, 64, 2, 64, 128, 2), (1, 128, 2, 33, 96, 3)])
-def test_gpt_step_hip_matches_oracle(tmp_path, L, C, H, T, V, B):
-    print(f"[case] gpt step hip L{L} C{C} H{H} T{T} V{V} B{B}", flush=True)
+@pytest.mark.parametrize("L,C,H,T,V,B,extra", [(2, 64, 2, 64, 128, 2, ()), (1, 128, 2, 33, 96, 3, ()),
+                                               (2, 64, 2, 64, 128, 2, ("--deterministic",))])
+def test_gpt_step_hip_matches_oracle(tmp_path, L, C, H, T, V, B, extra):
+    """One HIP training step against the oracle step (the last case with the attention
+    backward in the deterministic-dQ mode, set through the app's --deterministic)."""
+    print(f"[case] gpt step hip L{L} C{C} H{H} T{T} V{V} B{B} {' '.join(extra)}", flush=True)
     params, tokens, targets = make_case(tmp_path, L, C, H, T, V, B)
-    run_app(tmp_path, "hip")
+    run_app(tmp_path, "hip", *extra)
     check_against_oracle(tmp_path, params, tokens, targets, L, C, H)
 
 
