@@ -60,7 +60,7 @@ def _host_cpu():
     return model
 
 
-def cpu_baseline(B, H, T, D, heads: int, c4_rows: int = 512, c4_heads: int = 0):
+def cpu_baseline(B, H, T, D, heads: int, c4_rows: int = 256, c4_heads: int = 0):
     """Time the restated reference CPU path on one pinned core: `heads` heads of config 2
     (fwd+bwd), the whole config-5 decode step, a row sample of config 4, and an estimate of the
     config-3 step.
@@ -176,7 +176,7 @@ def main():
                     help="seconds of untimed steps before the W warm-up steps (clock ramp)")
     ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--cpu-heads", type=int, default=12, help="heads in the CPU-baseline sample (0 = skip)")
-    ap.add_argument("--cpu-c4-rows", type=int, default=512, help="config-4 query rows timed on the CPU")
+    ap.add_argument("--cpu-c4-rows", type=int, default=256, help="config-4 query rows timed on the CPU")
     ap.add_argument("--cpu-c4-heads", type=int, default=0,
                     help="time whole config-4 heads on the CPU instead of a row sample (over a minute each)")
     ap.add_argument("--deterministic", action="store_true",
