@@ -132,8 +132,10 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
  * scores and sums its key tiles in key order, the same on every run, at the
  * cost of two more matrix products per score.  The mode is read once per
  * call; the backward's workspace size depends on it (bf16 then needs no dQ
- * accumulator), so query inf_attn_workspace_bytes after setting it.  Returns
- * the previous setting.
+ * accumulator), so query inf_attn_workspace_bytes after setting it.  It also
+ * makes inf_embedding_bwd sum each row in token order instead of with fp32
+ * atomics, so with both a training step of the GPT model built on these calls
+ * is bitwise reproducible.  Returns the previous setting.
  */
 int inf_set_deterministic(int enable);
 int inf_get_deterministic(void);
@@ -324,8 +326,10 @@ int inf_embedding_fwd(const int32_t* ids, int64_t n_tokens, const void* table, i
                       inf_dtype dt, void* stream);
 
 /* dtable[ids[t], :] += dout[t, :] (fp32, atomic); zero_first clears dtable
- * first.  Replaces cuda_scatter_add_embedding (src/inferno/cuda/cudaops.h:68)
- * behind EmbeddingBackward. */
+ * first.  In the deterministic mode (inf_set_deterministic, dim <= 16384) each
+ * row of dtable is instead summed in token order by one workgroup, the same
+ * bits on every run.  Replaces cuda_scatter_add_embedding
+ * (src/inferno/cuda/cudaops.h:68) behind EmbeddingBackward. */
 int inf_embedding_bwd(const int32_t* ids, int64_t n_tokens, const float* dout, int64_t vocab, int64_t dim,
                       float* dtable, int zero_first, void* stream);
 

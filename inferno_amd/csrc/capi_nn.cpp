@@ -205,6 +205,11 @@ int inf_embedding_bwd(const int32_t* ids, int64_t n_tokens, const float* dout, i
     if (!dtable) return INF_ERR_NULL_POINTER;
     if (n_tokens > 0 && (!ids || !dout)) return INF_ERR_NULL_POINTER;
     if (!aligned(dtable, 16) || (dout && !aligned(dout, 16))) return INF_ERR_ALIGNMENT;
+    if (inf_get_deterministic() && dim <= 16384) {
+        // each row summed in token order by one workgroup (no atomics, no fill)
+        inf::EmbParams p{ids, nullptr, dout, dtable, n_tokens, vocab, dim};
+        return hip_status(inf::launch_embed_bwd_det(p, zero_first, S(stream)));
+    }
     if (zero_first) {
         const int e = inf::launch_fill(dtable, vocab * dim, 4, 0u, S(stream));
         if (e) return INF_ERR_HIP;

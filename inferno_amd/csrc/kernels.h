@@ -245,6 +245,8 @@ int launch_ce_fwd(const CeParams& p, float* loss, int bf16, hipStream_t s);
 int launch_ce_bwd(const CeParams& p, int bf16, hipStream_t s);
 int launch_embed_fwd(const EmbParams& p, int bf16, hipStream_t s);
 int launch_embed_bwd(const EmbParams& p, hipStream_t s);
+// Deterministic embedding backward (rows summed in token order); dim <= 16384.
+int launch_embed_bwd_det(const EmbParams& p, int zero_first, hipStream_t s);
 int launch_adamw(const AdamWParams& a, int bf16, hipStream_t s);
 int launch_adamw_multi(const AdamWMultiParams& a, int bf16, hipStream_t s);
 int launch_argmax_rows(const void* x, int64_t rows, int64_t cols, int64_t ld, int32_t* out, int bf16, hipStream_t s);

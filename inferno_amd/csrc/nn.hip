@@ -446,6 +446,39 @@ __global__ __launch_bounds__(256) void embed_bwd_kernel(EmbParams p) {
     unsafeAtomicAdd(d + 3, g[3]);
 }
 
+// Deterministic variant (the library's deterministic mode): workgroup w owns
+// vocab rows [w R, w R + R) in an LDS accumulator and walks the tokens in
+// order, adding the gradient row of each token whose id falls in its range, so
+// every row of dtable is its tokens' sum in token order.  Thread i owns
+// columns i, i + 256, ... of every row, so no two threads touch one word and
+// no barrier is needed.  The id of each token is wave-uniform: read once per
+// 16 tokens and tested per token, with no divergent branch.
+__global__ __launch_bounds__(256) void embed_bwd_det_kernel(EmbParams p, int rows_per_wg, int zero_first) {
+    extern __shared__ float acc[];  // rows_per_wg * dim
+    const int64_t v0 = (int64_t)blockIdx.x * rows_per_wg;
+    const int rows = (int)min((int64_t)rows_per_wg, p.vocab - v0);
+    const int dim = (int)p.dim;
+    float* dt = (float*)p.out + v0 * dim;
+    for (int r = 0; r < rows; ++r)
+        for (int c = threadIdx.x; c < dim; c += 256) acc[r * dim + c] = zero_first ? 0.f : dt[(int64_t)r * dim + c];
+    constexpr int U = 16;
+    for (int64_t t0 = 0; t0 < p.n_tokens; t0 += U) {
+        int id[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) id[u] = t0 + u < p.n_tokens ? p.ids[t0 + u] : -1;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t r = (int64_t)id[u] - v0;
+            if (id[u] >= 0 && id[u] < p.vocab && r >= 0 && r < rows) {
+                const float* g = (const float*)p.dout + (t0 + u) * p.dim;
+                for (int c = threadIdx.x; c < dim; c += 256) acc[r * dim + c] += g[c];
+            }
+        }
+    }
+    for (int r = 0; r < rows; ++r)
+        for (int c = threadIdx.x; c < dim; c += 256) dt[(int64_t)r * dim + c] = acc[r * dim + c];
+}
+
 // ============================================================================
 // AdamW (adamw.h:67-111, one parameter tensor per launch):
 //   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2;
@@ -739,6 +772,16 @@ int launch_embed_fwd(const EmbParams& p, int bf16, hipStream_t s) {
 int launch_embed_bwd(const EmbParams& p, hipStream_t s) {
     const dim3 grid(blocks_for(p.n_tokens * (p.dim / 4), 256));
     hipLaunchKernelGGL(embed_bwd_kernel, grid, dim3(256), 0, s, p);
+    return (int)hipGetLastError();
+}
+
+int launch_embed_bwd_det(const EmbParams& p, int zero_first, hipStream_t s) {
+    // rows per workgroup: up to 64 KB of LDS accumulator, at most 32 rows
+    const int rows = (int)std::max<int64_t>(1, std::min<int64_t>(32, 16384 / p.dim));
+    const size_t lds = (size_t)rows * p.dim * sizeof(float);
+    if (lds > 65536) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(embed_bwd_det_kernel, dim3(blocks_for(p.vocab, rows)), dim3(256), lds, s, p, rows,
+                       zero_first ? 1 : 0);
     return (int)hipGetLastError();
 }
 

@@ -174,6 +174,41 @@ def test_embedding_parity(ia):
     assert np.array_equal(host(dt), onn.embedding_bwd(ids, gout, vocab))
 
 
+@pytest.mark.parametrize("vocab,dim,n", [(8192, 768, 8192), (1000, 100, 3000), (37, 16384, 50)])
+def test_embedding_bwd_deterministic(ia, vocab, dim, n):
+    """The deterministic mode's embedding backward sums each row in token order, as the
+    oracle's CPU loop does: bit-identical to the oracle for arbitrary fp32 gradients (repeated
+    ids and ids outside [0, vocab) included), and, accumulating into an existing dtable, to the
+    same sequential sum started from that table."""
+    print(f"[case] embedding bwd deterministic vocab{vocab} dim{dim} n{n}", flush=True)
+    rng = np.random.default_rng(vocab + dim)
+    ids = rng.integers(0, vocab, n).astype(np.int32)
+    ids[: n // 4] = 3                       # one row collects a quarter of the tokens
+    ids[n // 4 : n // 4 + 5] = [-1, vocab, vocab + 7, -100, 2 ** 31 - 1]  # skipped
+    gout = rng.standard_normal((n, dim)).astype(np.float32)
+    I, G = dev(ids), dev(gout)
+    prev = ia.set_deterministic(True)
+    try:
+        dt = ia.embedding_bwd(I, G, vocab)
+        dt2 = ia.embedding_bwd(I, G, vocab)
+        base = rng.standard_normal((vocab, dim)).astype(np.float32)
+        acc = dev(base)
+        st = ia.lib().inf_embedding_bwd(I.data_ptr(), n, G.data_ptr(), vocab, dim, acc.data_ptr(), 0,
+                                        torch.cuda.current_stream().cuda_stream)
+        assert st == 0
+        torch.cuda.synchronize()
+    finally:
+        ia.set_deterministic(prev)
+    assert torch.equal(dt, dt2)
+    ok = (ids >= 0) & (ids < vocab)  # the oracle's loop takes valid ids only
+    assert np.array_equal(host(dt), onn.embedding_bwd(ids[ok], gout[ok], vocab))
+    want = base.copy()
+    for t in range(n):  # the same fp32 additions in token order
+        if 0 <= ids[t] < vocab:
+            want[ids[t]] += gout[t]
+    assert np.array_equal(host(acc), want)
+
+
 # ---------------------------------------------------------------------- AdamW
 @pytest.mark.parametrize("step", [1, 3])
 def test_adamw_parity(ia, step):
