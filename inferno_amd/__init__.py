@@ -191,7 +191,8 @@ def nn_workspace_bytes(op: int, rows: int = 0, cols: int = 0) -> int:
 
 def set_deterministic(enable: bool) -> bool:
     """Process-wide switch (inf_set_deterministic): every later attention backward takes dQ
-    from the query-major pass, bitwise the same on every run.  Returns the previous setting."""
+    from the query-major pass and every embedding backward sums its rows in token order, bitwise
+    the same on every run.  Returns the previous setting."""
     return bool(lib().inf_set_deterministic(1 if enable else 0))
 
 

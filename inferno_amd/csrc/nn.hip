@@ -450,33 +450,44 @@ __global__ __launch_bounds__(256) void embed_bwd_kernel(EmbParams p) {
 // vocab rows [w R, w R + R) in an LDS accumulator and walks the tokens in
 // order, adding the gradient row of each token whose id falls in its range, so
 // every row of dtable is its tokens' sum in token order.  Thread i owns
-// columns i, i + 256, ... of every row, so no two threads touch one word and
-// no barrier is needed.  The id of each token is wave-uniform: read once per
-// 16 tokens and tested per token, with no divergent branch.
+// columns i, i + 256, ... of every row, so no two threads touch one word.  The
+// ids are scanned 256 at a time (one per thread); each wave's matches go to LDS
+// as a ballot mask, and the workgroup then takes the matched tokens in order.
 __global__ __launch_bounds__(256) void embed_bwd_det_kernel(EmbParams p, int rows_per_wg, int zero_first) {
     extern __shared__ float acc[];  // rows_per_wg * dim
+    __shared__ uint64_t s_mask[2][4];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
     const int64_t v0 = (int64_t)blockIdx.x * rows_per_wg;
     const int rows = (int)min((int64_t)rows_per_wg, p.vocab - v0);
     const int dim = (int)p.dim;
     float* dt = (float*)p.out + v0 * dim;
     for (int r = 0; r < rows; ++r)
-        for (int c = threadIdx.x; c < dim; c += 256) acc[r * dim + c] = zero_first ? 0.f : dt[(int64_t)r * dim + c];
-    constexpr int U = 16;
-    for (int64_t t0 = 0; t0 < p.n_tokens; t0 += U) {
-        int id[U];
+        for (int c = tid; c < dim; c += 256) acc[r * dim + c] = zero_first ? 0.f : dt[(int64_t)r * dim + c];
+    int buf = 0;
+    for (int64_t t0 = 0; t0 < p.n_tokens; t0 += 256, buf ^= 1) {
+        const int64_t t = t0 + tid;
+        const int id = t < p.n_tokens ? p.ids[t] : -1;
+        const int64_t r = (int64_t)id - v0;
+        const bool mine = id >= 0 && id < p.vocab && r >= 0 && r < rows;
+        const uint64_t m = __ballot(mine);
+        if ((tid & 63) == 0) s_mask[buf][wave] = m;
+        __syncthreads();  // the masks of this chunk are visible; the other buffer is free again
 #pragma unroll
-        for (int u = 0; u < U; ++u) id[u] = t0 + u < p.n_tokens ? p.ids[t0 + u] : -1;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t r = (int64_t)id[u] - v0;
-            if (id[u] >= 0 && id[u] < p.vocab && r >= 0 && r < rows) {
-                const float* g = (const float*)p.dout + (t0 + u) * p.dim;
-                for (int c = threadIdx.x; c < dim; c += 256) acc[r * dim + c] += g[c];
+        for (int w = 0; w < 4; ++w) {
+            uint64_t mw = s_mask[buf][w];
+            while (mw) {
+                const int bit = __builtin_ctzll(mw);
+                mw &= mw - 1;
+                const int64_t tt = t0 + 64 * w + bit;
+                const int rr = (int)((int64_t)p.ids[tt] - v0);
+                const float* g = (const float*)p.dout + tt * p.dim;
+                for (int c = tid; c < dim; c += 256) acc[rr * dim + c] += g[c];
             }
         }
     }
     for (int r = 0; r < rows; ++r)
-        for (int c = threadIdx.x; c < dim; c += 256) dt[(int64_t)r * dim + c] = acc[r * dim + c];
+        for (int c = tid; c < dim; c += 256) dt[(int64_t)r * dim + c] = acc[r * dim + c];
 }
 
 // ============================================================================
