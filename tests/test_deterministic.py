@@ -146,6 +146,33 @@ def test_deterministic_random_shapes(ia, dt, causal, B, H, Tq, Tk, D):
     assert torch.equal(first[0], second[0]), "dQ differs between two deterministic calls"
 
 
+@pytest.mark.parametrize("dt,D,T", [("f32", 64, 150), ("bf16", 64, 150), ("f32", 128, 97), ("bf16", 32, 211)])
+def test_deterministic_strided_qkv_view(ia, dt, D, T):
+    """The mode on q/k/v read straight out of a [B, T, 3, H, D] projection buffer and dq/dk/dv
+    written into a gradient buffer of the same layout (the C++ layer's qkv_attention)."""
+    print(f"[case] deterministic strided views {dt} D{D} T{T}", flush=True)
+    dtype = torch.bfloat16 if dt == "bf16" else torch.float32
+    B, H = 2, 3
+    q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=31)
+    if dt == "bf16":
+        q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
+    buf = torch.empty((B, T, 3, H, D), device="cuda", dtype=dtype)
+    gbuf = torch.full((B, T, 3, H, D), float("nan"), device="cuda", dtype=dtype)
+    for i, x in enumerate((q, k, v)):
+        buf[:, :, i] = dev(x, dtype).transpose(1, 2)
+    Q, K, V = (buf[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    dQ, dK, dV = (gbuf[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    ia.set_deterministic(True)
+    o, lse = ia.attn_fwd(Q, K, V)
+    ia.attn_bwd(Q, K, V, o, dev(do, dtype), lse, dq=dQ, dk=dK, dv=dV)
+    torch.cuda.synchronize()
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do)
+    tol = TOL_BF16 if dt == "bf16" else TOL_F32
+    for name, x, r in (("dQ", dQ, dq_r), ("dK", dK, dk_r), ("dV", dV, dv_r)):
+        e = oracle.rel_err(host(x), r)
+        assert e <= tol, f"{name} rel err {e:.3e}"
+
+
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_deterministic_config2_full_size(ia, dt):
     """Config 2 (B8 H12 T1024 D64) in the mode: three heads against the oracle, dQ of every head
