@@ -2,7 +2,8 @@
 //
 // Kernel 1 (bwd_pre): delta[i] = sum_d dO[i,d] * O[i,d] per query row (the
 // row dot that SoftmaxBackward computes as sum_j dP_ij P_ij), and zeroes the
-// fp32 dQ accumulator.
+// fp32 dQ accumulator.  (The bf16 main kernel at D <= 64 forms delta itself,
+// and then this pass only zeroes.)
 //
 // Kernel 2 (bwd_main): one workgroup = 4 waves = 128 keys of one (b, h); each
 // wave owns 32 keys and keeps K and V for them in VGPRs plus its dK^T and dV^T
@@ -56,16 +57,21 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdParams p) {
         bh = row / p.Tq;
         i = row % p.Tq;
         const int64_t b = bh / p.H, h = bh % p.H;
-        const f32x4 o4 = ld4((const E*)p.o + b * p.so.b + h * p.so.h + i * p.so.t + 4 * c4);
-        const f32x4 d4 = ld4((const E*)p.dout + b * p.sdo.b + h * p.sdo.h + i * p.sdo.t + 4 * c4);
-        s = o4[0] * d4[0] + o4[1] * d4[1] + o4[2] * d4[2] + o4[3] * d4[3];
+        if (p.pre_delta) {
+            const f32x4 o4 = ld4((const E*)p.o + b * p.so.b + h * p.so.h + i * p.so.t + 4 * c4);
+            const f32x4 d4 = ld4((const E*)p.dout + b * p.sdo.b + h * p.sdo.h + i * p.sdo.t + 4 * c4);
+            s = o4[0] * d4[0] + o4[1] * d4[1] + o4[2] * d4[2] + o4[3] * d4[3];
+        }
         if (!p.dq_direct)
             *reinterpret_cast<f32x4*>(p.dq_acc + b * p.sacc.b + h * p.sacc.h + i * p.sacc.t + 4 * c4) =
                 f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // (p.pre_delta is uniform: the whole grid takes or skips the exchange)
+    if (p.pre_delta) {
 #pragma unroll
-    for (int m = TPR / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
-    if (row < rows && c4 == 0) p.delta[row] = s;
+        for (int m = TPR / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
+        if (row < rows && c4 == 0) p.delta[row] = s;
+    }
     if (blockIdx.x == 0)
         for (int i = tid; i < p.n_split * p.B * p.H; i += 256) p.counters[i] = 0u;
 }
@@ -746,7 +752,12 @@ size_t bwd_split_workspace_bytes(const BwdPlan& plan, int B, int H, int D) {
 }
 
 template <int D, typename E>
-static int launch_bwd_t(const BwdParams& p, hipStream_t s) {
+static int launch_bwd_t(const BwdParams& p_in, hipStream_t s) {
+    BwdParams p = p_in;
+    // The bf16 main kernel at D <= 64 forms delta itself while staging each
+    // query tile; bwd_pre then only zeroes, unless the query-major dQ pass
+    // (which reads delta) follows.
+    p.pre_delta = (sizeof(E) == 2 && D <= 64) ? p.dq_direct : 1;
     constexpr int RPB = 256 / (D / 4);
     const int64_t rows = (int64_t)p.B * p.H * p.Tq;
     const dim3 pre_grid((unsigned)((rows + RPB - 1) / RPB));

@@ -103,7 +103,6 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     const __bf16* dO = (const __bf16*)p.dout + b * p.sdo.b + h * p.sdo.h;
     float* dQa = p.dq_acc + b * p.sacc.b + h * p.sacc.h;
     const float* LSE = p.lse + (int64_t)bh * p.Tq;
-    const float* DL = p.delta + (int64_t)bh * p.Tq;
 
     const int k0 = kblk * BK;
     const int k0w = k0 + wave * 32;
@@ -159,13 +158,19 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     // at the barrier before the dQ product reads dS.  (With single buffers and
     // two barriers per tile the kernel measured 6% slower at config 2.)
     bf16x8 ra[QLPT], rb[QLPT];
-    float r_lse = 0.f, r_dl = 0.f;
+    float r_lse = 0.f;
     // Loads through buffer resources over rows [q0, lim) (<= Tq): rows past
     // them read as zeros, with no address arithmetic or branch per load; raw
-    // values only, so no arithmetic waits on the loads here.  Whether chunk f
-    // is of Q or dO is uniform over each wave for every head dim (QTASK is a
-    // multiple of 64), which keeps the selected resource in SGPRs.
+    // values only, so no arithmetic waits on the loads here.  Chunk f is a
+    // (row pair, chunk) task of Q (f < QTASK) or dO (f < 2 QTASK), or, on the
+    // threads the two leave free, a (row, chunk) task of the row dot
+    // delta = rowsum(dO * O) (ra = O, rb = dO): delta is formed here instead
+    // of in a pass over O and dO before the kernel.  The kind is uniform over
+    // each wave for every head dim (QTASK is a multiple of 64), which keeps
+    // the selected resources in SGPRs.
     static_assert(QTASK % 64 == 0, "Q / dO split must be wave-uniform");
+    static_assert(4 * QTASK == NT, "Q, dO and delta tasks fill the workgroup once");
+    const __bf16* Ob = (const __bf16*)p.o + b * p.so.b + h * p.so.h;
     auto gload_q = [&](int q0, int lim) {
         const int rows = min(lim - q0, BQ);
         const auto rq = row_rsrc(Q, p.sq.t, q0, rows, D);
@@ -174,8 +179,15 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
         for (int i = 0; i < QLPT; ++i) {
             const int f = tid + NT * i;
             ra[i] = rb[i] = bf16x8{};
-            if (f >= 2 * QTASK) continue;
-            const int which = __builtin_amdgcn_readfirstlane(f / QTASK);  // 0: Q, 1: dO
+            const int which = __builtin_amdgcn_readfirstlane(f / QTASK);  // 0: Q, 1: dO, 2-3: delta
+            if (which >= 2) {
+                const int rem = f - 2 * QTASK;
+                const int row = rem / C8, c8 = rem % C8;
+                const auto ro = row_rsrc(Ob, p.so.t, q0, rows, D);
+                ra[i] = buffer_ld8bf(ro, (uint32_t)(((int64_t)row * p.so.t + 8 * c8) * 2), 0);
+                rb[i] = buffer_ld8bf(rdo, (uint32_t)(((int64_t)row * p.sdo.t + 8 * c8) * 2), 0);
+                continue;
+            }
             const int rem = f % QTASK;
             const int qp = rem % (BQ / 2), c8 = rem / (BQ / 2);
             const int64_t st = which ? p.sdo.t : p.sq.t;
@@ -186,7 +198,6 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
         }
         // lanes past the tile's rows (all but the first BQ threads) read zeros
         r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
-        r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
     };
     auto sstore_q = [&](int sb) {
         __bf16(*Qs)[QS] = Qs2[sb];
@@ -198,8 +209,18 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
             const int f = tid + NT * i;
-            if (f >= 2 * QTASK) continue;
             const int which = f / QTASK;
+            if (which >= 2) {
+                // delta of row `row`: this lane's 8 products, then the sum over
+                // the C8 adjacent lanes of the row (DPP), in a fixed order
+                const int rem = f - 2 * QTASK;
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d = fmaf((float)ra[i][e], (float)rb[i][e], d);
+                d = group_sum<C8>(d);
+                if (rem % C8 == 0) dl_s[rem / C8] = d;
+                continue;
+            }
             const int rem = f % QTASK;
             const int qp = rem % (BQ / 2), c8 = rem / (BQ / 2);
             __bf16(*rows)[QS] = which ? dOs : Qs;
@@ -217,10 +238,7 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
                 *reinterpret_cast<bf16x2*>(&cols[8 * c8 + e][pos]) = pr;
             }
         }
-        if (tid < BQ) {
-            lse_s[tid] = r_lse * kLseStage;
-            dl_s[tid] = r_dl;
-        }
+        if (tid < BQ) lse_s[tid] = r_lse * kLseStage;
     };
 
     gload_q(q_begin, p.Tq);

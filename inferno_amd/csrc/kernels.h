@@ -95,6 +95,7 @@ struct BwdParams {
     float scale, c;
     int n_kblocks;
     int dq_direct;          // bf16: dQ from the query-major pass (no accumulator, no atomics)
+    int pre_delta;          // bwd_pre computes delta (set by the launcher: off where no kernel reads it)
     int n_qtiles;           // query tiles of kBwdDqBM rows (dQ pass)
     // split plan (n_groups == 0: workgroup w takes key block w / (B*H), all its tiles)
     int n_groups, n_split;
