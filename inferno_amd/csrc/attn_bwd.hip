@@ -2,7 +2,7 @@
 //
 // Kernel 1 (bwd_pre): delta[i] = sum_d dO[i,d] * O[i,d] per query row (the
 // row dot that SoftmaxBackward computes as sum_j dP_ij P_ij), and zeroes the
-// fp32 dQ accumulator.  (The main kernels at D <= 64 form delta themselves,
+// fp32 dQ accumulator.  (The bf16 main kernel at D <= 64 forms delta itself,
 // and then this pass only zeroes.)
 //
 // Kernel 2 (bwd_main): one workgroup = 4 waves = 128 keys of one (b, h); each
@@ -131,6 +131,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
     const E* dO = (const E*)p.dout + b * p.sdo.b + h * p.sdo.h;
     float* dQa = p.dq_acc + b * p.sacc.b + h * p.sacc.h;
     const float* LSE = p.lse + (int64_t)bh * p.Tq;
+    const float* DL = p.delta + (int64_t)bh * p.Tq;
 
     const int k0 = kblk * BK;
     const int k0w = k0 + wave * 32;
@@ -190,32 +191,22 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
     constexpr bool PF = D <= 64;
     static_assert(NT % C4 == 0, "chunk rows must split into thread + load parts");
     static_assert(sizeof(E) == 4, "fp32 storage (bf16 has its own kernel)");
-    // With PF, delta = rowsum(dO * O) is formed here from the staged dO chunks
-    // and the matching O chunks (a dot per chunk, then a DPP sum over the C4
-    // adjacent lanes of the row) instead of in a pass over O and dO before the
-    // kernel (config 2 -0.5%, D = 32 -2%); at D = 128 the extra loads sit in
-    // the unprefetched path (3% slower) and bwd_pre forms it.
-    f32x4 ra[QLPT], rd[QLPT], ro[QLPT];
+    f32x4 ra[QLPT], rd[QLPT];
     float r_lse = 0.f, r_dl = 0.f;
-    const float* DL = p.delta + (int64_t)bh * p.Tq;
-    const E* Ob = (const E*)p.o + b * p.so.b + h * p.so.h;
-    const uint32_t o_voff = (uint32_t)(((int64_t)(tid / C4) * p.so.t + 4 * (tid % C4)) * 4);
     const uint32_t q_voff = (uint32_t)(((int64_t)(tid / C4) * p.sq.t + 4 * (tid % C4)) * 4);
     const uint32_t do_voff = (uint32_t)(((int64_t)(tid / C4) * p.sdo.t + 4 * (tid % C4)) * 4);
     auto gload_q = [&](int q0, int lim) {
         const int rows = min(lim - q0, BQ);
         const auto rq = row_rsrc((const float*)Q, p.sq.t, q0, rows, D);
         const auto rdo = row_rsrc((const float*)dO, p.sdo.t, q0, rows, D);
-        const auto rob = row_rsrc((const float*)Ob, p.so.t, q0, rows, D);
 #pragma unroll
         for (int i = 0; i < QLPT; ++i) {
             ra[i] = buffer_ld4(rq, q_voff, (uint32_t)((int64_t)(NT * i / C4) * p.sq.t * 4));
             rd[i] = buffer_ld4(rdo, do_voff, (uint32_t)((int64_t)(NT * i / C4) * p.sdo.t * 4));
-            if constexpr (PF) ro[i] = buffer_ld4(rob, o_voff, (uint32_t)((int64_t)(NT * i / C4) * p.so.t * 4));
         }
         // lanes past the tile's rows (all but the first BQ threads) read zeros
         r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
-        if constexpr (!PF) r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
+        r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
     };
     auto sstore_q = [&]() {
 #pragma unroll
@@ -223,18 +214,10 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
             const int f = tid + NT * i;
             *reinterpret_cast<f32x4*>(&Qs[f / C4][4 * (f % C4)]) = ra[i];
             *reinterpret_cast<f32x4*>(&dOs[f / C4][4 * (f % C4)]) = rd[i];
-            if constexpr (PF) {
-                float d = rd[i][0] * ro[i][0];
-                d = fmaf(rd[i][1], ro[i][1], d);
-                d = fmaf(rd[i][2], ro[i][2], d);
-                d = fmaf(rd[i][3], ro[i][3], d);
-                d = group_sum<C4>(d);
-                if (f % C4 == 0) dl_s[f / C4] = d;
-            }
         }
         if (tid < BQ) {
             lse_s[tid] = r_lse;  // natural-log LSE; scaled by log2(e) where it is read
-            if constexpr (!PF) dl_s[tid] = r_dl;
+            dl_s[tid] = r_dl;
         }
     };
     if constexpr (PF) {
@@ -771,10 +754,10 @@ size_t bwd_split_workspace_bytes(const BwdPlan& plan, int B, int H, int D) {
 template <int D, typename E>
 static int launch_bwd_t(const BwdParams& p_in, hipStream_t s) {
     BwdParams p = p_in;
-    // The main kernels at D <= 64 form delta themselves while staging each
-    // query tile; bwd_pre then only zeroes, unless the
-    // query-major dQ pass (which reads delta) follows.
-    p.pre_delta = D <= 64 ? p.dq_direct : 1;
+    // The bf16 main kernel at D <= 64 forms delta itself while staging each
+    // query tile; bwd_pre then only zeroes, unless the query-major dQ pass
+    // (which reads delta) follows.
+    p.pre_delta = (sizeof(E) == 2 && D <= 64) ? p.dq_direct : 1;
     constexpr int RPB = 256 / (D / 4);
     const int64_t rows = (int64_t)p.B * p.H * p.Tq;
     const dim3 pre_grid((unsigned)((rows + RPB - 1) / RPB));
