@@ -35,10 +35,11 @@ HBM_PEAK_GBS = 8000.0
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script, scaled by what the same
 # counters read for a plain device copy (FETCH_SIZE x2.00, WRITE_SIZE x1.00).  fp32 bwd_main
 # runs the split plan (partial dK / dV written and read back); the bf16 call adds the dQ
-# conversion pass.
+# conversion pass, and its pre pass only zeroes the dQ accumulator (the bf16 main kernel forms
+# delta from O and dO itself).
 BWD_TRAFFIC = {
     "f32": {"bwd_pre": 50.40e6 + 25.56e6, "bwd_main": 202.27e6 + 201.35e6},
-    "bf16": {"bwd_pre": 25.23e6 + 25.56e6, "bwd_main": 66.10e6 + 102.57e6, "bwd_cvt": 25.22e6 + 12.58e6},
+    "bf16": {"bwd_pre": 0.06e6 + 25.17e6, "bwd_main": 82.15e6 + 107.62e6, "bwd_cvt": 25.22e6 + 12.58e6},
 }
 
 METRIC = "causal attn fwd+bwd TFLOP/s (B8 H12 T1024 D64 fp32) + % of MFMA peak"
