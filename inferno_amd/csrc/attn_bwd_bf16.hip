@@ -218,7 +218,7 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
 #pragma unroll
                 for (int e = 0; e < 8; ++e) d = fmaf((float)ra[i][e], (float)rb[i][e], d);
                 d = group_sum<C8>(d);
-                if (rem % C8 == 0) dl_s[rem / C8] = d;
+                if (rem % C8 == 0) dl_s[rem / C8] = -d;  // staged negated: the dP accumulator starts at -delta
                 continue;
             }
             const int rem = f % QTASK;
@@ -282,14 +282,23 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
                 qa[kk] = *reinterpret_cast<const bf16x8*>(&Qs[l32][16 * kk + 8 * g]);
                 da[kk] = *reinterpret_cast<const bf16x8*>(&dOs[l32][16 * kk + 8 * g]);
             }
-            // all eight operand reads are issued before the first MFMA (the
+            // dP starts at -delta of its row (register r: query row
+            // 8 (r / 4) + 4 g + r % 4), so dS = P * dP needs no subtraction
+            f32x16 dp0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 nd = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) dp0[4 * j + cc] = nd[cc];
+            }
+            // all operand reads are issued before the first MFMA (the
             // scheduler would otherwise pair each read with its MFMA and wait
             // out one LDS latency per product)
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int kk = 0; kk < NKK; ++kk) {
                 s = mfma32x32x16bf16(qa[kk], kf[kk], kk == 0 ? f32x16{} : s);  // zero accumulator as an operand
-                dp = mfma32x32x16bf16(da[kk], vf[kk], kk == 0 ? f32x16{} : dp);
+                dp = mfma32x32x16bf16(da[kk], vf[kk], kk == 0 ? dp0 : dp);
             }
             // transposed Q / dO operands of the dV / dK products, read while P and dS are formed
             bf16x8 ado[2][NDB], aq[2][NDB];
@@ -309,7 +318,6 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLseRead;
-                    const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
 #pragma unroll
                     for (int cc = 0; cc < 4; ++cc) {
                         const int r = 4 * j + cc;
@@ -320,7 +328,7 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
                             pr = vis ? pr : 0.f;
                         }
                         pb[r >> 3][r & 7] = (__bf16)pr;
-                        dsb[r >> 3][r & 7] = (__bf16)(pr * (dp[r] - Dl[cc]));
+                        dsb[r >> 3][r & 7] = (__bf16)(pr * dp[r]);
                     }
                 }
             };
