@@ -76,6 +76,19 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdParams p) {
         for (int i = tid; i < p.n_split * p.B * p.H; i += 256) p.counters[i] = 0u;
 }
 
+// bwd_pre without delta (the bf16 main kernel at D <= 64 forms it): the fp32
+// dQ accumulator is one dense [B, H, Tq, D] block, so it is cleared as a flat
+// array (16-byte stores over a grid-stride loop), with the split plan's
+// arrival counters.
+__global__ __launch_bounds__(256) void bwd_zero_kernel(BwdParams p) {
+    const int64_t n4 = (int64_t)p.B * p.H * p.Tq * p.D / 4;
+    f32x4* acc = reinterpret_cast<f32x4*>(p.dq_acc);
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256)
+        acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < p.n_split * p.B * p.H; i += 256) p.counters[i] = 0u;
+}
+
 template <int D>
 struct BwdTile {
     static constexpr int NW = bwd_waves(0, D);  // waves per workgroup, 32 keys each
@@ -761,7 +774,14 @@ static int launch_bwd_t(const BwdParams& p_in, hipStream_t s) {
     constexpr int RPB = 256 / (D / 4);
     const int64_t rows = (int64_t)p.B * p.H * p.Tq;
     const dim3 pre_grid((unsigned)((rows + RPB - 1) / RPB));
-    hipLaunchKernelGGL((bwd_pre_kernel<D, E>), pre_grid, dim3(256), 0, s, p);
+    if (!p.pre_delta && !p.dq_direct) {
+        // zeroing only: a few grid-stride workgroups per CU
+        const int64_t n4 = rows * D / 4;
+        const unsigned zb = (unsigned)std::min<int64_t>((n4 + 255) / 256, 2048);
+        hipLaunchKernelGGL(bwd_zero_kernel, dim3(zb), dim3(256), 0, s, p);
+    } else {
+        hipLaunchKernelGGL((bwd_pre_kernel<D, E>), pre_grid, dim3(256), 0, s, p);
+    }
     if constexpr (sizeof(E) == 2) {
         const int e = launch_bwd_main_bf16(p, s);
         if (e) return e;
