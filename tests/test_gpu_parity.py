@@ -247,7 +247,9 @@ def test_prefix_invariance_bitwise(ia, dtype, T, D, cuts):
                                      (torch.bfloat16, 64, 150), (torch.bfloat16, 32, 211)])
 def test_strided_qkv_view(ia, dtype, D, T):
     """q/k/v read straight out of a [B, T, 3, H, D] projection buffer and dq/dk/dv
-    written straight into a gradient buffer of the same layout (no copies)."""
+    written straight into a gradient buffer of the same layout (no copies); O written into,
+    and O and dO read back from, [B, T, H, D] buffers (the module's [B, T, C] layout), which
+    the backward's delta = rowsum(dO * O) reads through their strides."""
     print(f"[case] strided views {dtype} D{D} T{T}", flush=True)
     B, H = 2, 3
     q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=5)
@@ -260,8 +262,12 @@ def test_strided_qkv_view(ia, dtype, D, T):
     Q, K, V = (buf[:, :, i].permute(0, 2, 1, 3) for i in range(3))
     dQ, dK, dV = (gbuf[:, :, i].permute(0, 2, 1, 3) for i in range(3))
     assert not Q.is_contiguous() and Q.stride(2) == 3 * H * D
-    o, lse = ia.attn_fwd(Q, K, V)
-    ia.attn_bwd(Q, K, V, o, dev(do, dtype), lse, dq=dQ, dk=dK, dv=dV)
+    o = torch.full((B, T, H, D), float("nan"), device="cuda", dtype=dtype).permute(0, 2, 1, 3)
+    dO = torch.empty((B, T, H, D), device="cuda", dtype=dtype).permute(0, 2, 1, 3)
+    dO.copy_(dev(do, dtype))
+    assert o.stride(2) == H * D and dO.stride(2) == H * D
+    o, lse = ia.attn_fwd(Q, K, V, out=o)
+    ia.attn_bwd(Q, K, V, o, dO, lse, dq=dQ, dk=dK, dv=dV)
     torch.cuda.synchronize()
     o_r, _ = oracle.attn_fwd(q, k, v)
     dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do)
