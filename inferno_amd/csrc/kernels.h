@@ -83,7 +83,7 @@ struct BwdParams {
     const void* o;
     const void* dout;
     const float* lse;     // dense [B,H,Tq]
-    float* delta;         // workspace, dense [B,H,Tq]: rowsum(dO * O)
+    float* delta;         // workspace, dense [B,H,Tq]: rowsum(dO * O) (unused where the main kernel forms it)
     float* dq_acc;        // fp32 dQ accumulation (dq itself for fp32)
     View4 sacc;           // strides of dq_acc
     void* dq;
@@ -100,7 +100,7 @@ struct BwdParams {
     // split plan (n_groups == 0: workgroup w takes key block w / (B*H), all its tiles)
     int n_groups, n_split;
     float* part;            // n_slots * B*H * 2*D*(keys per workgroup) floats (lane-major accumulators)
-    unsigned* counters;     // n_split * B*H, zeroed by bwd_pre
+    unsigned* counters;     // n_split * B*H, zeroed by bwd_pre / bwd_zero
     BwdGroup groups[kMaxBwdGroups];
 };
 
