@@ -13,24 +13,39 @@
 //   O^T:  B = P^T[8 keys][q] -- straight from the S^T accumulators: MFMA m of
 //         a 32-key block takes registers 8m..8m+7, i.e. keys
 //         16m + 4g + {0..3} and 16m + 8 + 4g + {0..3} (converted to bf16)
-//         A = V^T[d][the same 8 keys] -- V is stored transposed in LDS (keys
-//         contiguous per head-dim row), so this is two 8-byte reads.
-// The transpose happens once per tile while staging: each thread takes a key
-// pair and 8 head-dim columns and writes 8 dwords that pack (V[2k][d],
-// V[2k+1][d]).  Softmax statistics and the row sum stay fp32; P enters the
-// MFMA rounded to bf16.
+//         A = V^T[d][the same 8 keys] -- V is staged row-major like K and
+//         read transposed by gfx950's ds_read_b64_tr_b16: in each group of 16
+//         lanes, output lane i, element k is element i % 4 of the 8 bytes
+//         that lane 4k + i / 4 addresses.  With those 16 lanes addressing 4 key
+//         rows x 4 chunks of 4 head-dim columns (row r0 + s / 4, columns
+//         d0 + 4 (s % 4) for lane s), lane i receives column d0 + i of the 4
+//         rows: two such reads (keys 16m + 4g + {0..3}, then + 8) are the
+//         operand, the same two 8-byte reads per MFMA as a transposed copy
+//         would need, without transposing stores while staging.
+// Softmax statistics and the row sum stay fp32; P enters the MFMA rounded to
+// bf16.
 #include "common.h"
 #include "kernels.h"
 
 namespace inf {
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 at an LDS address (8-byte aligned).
+__device__ __forceinline__ bf16x4 ds_read_tr16(const __bf16* p) {
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                          (__attribute__((address_space(3))) s16x4*)(p)));
+}
 
 template <int D>
 struct FwdBf16Tile {
     static constexpr int BN = kFwdBf16BN;  // keys per tile
     static constexpr int KS = D + 8;    // K row stride in LDS (bf16 elements)
-    static constexpr int VS = BN + 4;   // V^T row stride in LDS (bf16 elements)
+    // V row stride (bf16): a transposed read's 4 rows x 32 bytes must fall in
+    // disjoint banks, i.e. a stride of 36 (D = 64), 72 or 24 (D = 128 / 32)
+    // dwords modulo 64.
+    static constexpr int VS = D == 64 ? D + 8 : D + 16;
 };
 
 // SPLIT: the launch carries a split plan (groups, partial slots); the
@@ -46,12 +61,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     constexpr int NDB = D / 32;          // 32-wide head-dim blocks of O^T
     constexpr int C8 = D / 8;            // 8-element chunks per row
     constexpr int KLPT = BN * C8 / 256;  // K chunks per thread per tile
-    constexpr int VTASKS = (BN / 2) * C8;      // V (key pair, chunk) tasks per tile
-    constexpr int VLPT = (VTASKS + 255) / 256;  // ... per thread
     static_assert(BN * C8 % 256 == 0, "K staging assumes whole passes");
 
     __shared__ __attribute__((aligned(16))) __bf16 Ks[2][BN][KS];
-    __shared__ __attribute__((aligned(16))) __bf16 Vt[2][D][VS];
+    __shared__ __attribute__((aligned(16))) __bf16 Vs[2][BN][VS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -113,9 +126,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     const int64_t kstep = (int64_t)BN * p.sk.t, vstep = (int64_t)BN * p.sv.t;
     const __bf16* kt = K + (int64_t)kb0 * p.sk.t;
     const __bf16* vt = V + (int64_t)kb0 * p.sv.t;
-    bf16x8 kr[KLPT], va[VLPT], vb[VLPT];
+    bf16x8 kr[KLPT], vr[KLPT];
     const uint32_t k_voff = (uint32_t)(((int64_t)(tid / C8) * p.sk.t + 8 * (tid % C8)) * 2);
-    const uint32_t v_voff = (uint32_t)(((int64_t)(2 * (tid % (BN / 2))) * p.sv.t + 8 * (tid / (BN / 2))) * 2);
+    const uint32_t v_voff = (uint32_t)(((int64_t)(tid / C8) * p.sv.t + 8 * (tid % C8)) * 2);
     auto gload = [&](int rows) {
         const auto rk = row_rsrc(kt, p.sk.t, 0, rows, D);
         const auto rv = row_rsrc(vt, p.sv.t, 0, rows, D);
@@ -123,12 +136,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
         for (int i = 0; i < KLPT; ++i)
             kr[i] = buffer_ld8bf(rk, k_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sk.t * 2));
 #pragma unroll
-        for (int i = 0; i < VLPT; ++i) {
-            if (tid + 256 * i >= VTASKS) continue;
-            const uint32_t col = (uint32_t)(8 * (256 * i / (BN / 2)) * 2);
-            va[i] = buffer_ld8bf(rv, v_voff, col);
-            vb[i] = buffer_ld8bf(rv, v_voff, col + (uint32_t)(p.sv.t * 2));
-        }
+        for (int i = 0; i < KLPT; ++i)
+            vr[i] = buffer_ld8bf(rv, v_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sv.t * 2));
     };
     auto sstore = [&](int buf) {
 #pragma unroll
@@ -136,22 +145,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
             const int f = tid + 256 * i;
             const int row = f / C8, c8 = f % C8;
             *reinterpret_cast<bf16x8*>(&Ks[buf][row][8 * c8]) = kr[i];
-        }
-#pragma unroll
-        for (int i = 0; i < VLPT; ++i) {
-            const int f = tid + 256 * i;
-            const int kp = f % (BN / 2), c8 = f / (BN / 2);
-            if (f >= VTASKS) continue;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-                bf16x2 pr;
-                pr[0] = va[i][e];
-                pr[1] = vb[i][e];
-                *reinterpret_cast<bf16x2*>(&Vt[buf][8 * c8 + e][2 * kp]) = pr;
-            }
+            *reinterpret_cast<bf16x8*>(&Vs[buf][row][8 * c8]) = vr[i];
         }
     };
+
+    // transposed V reads: this lane's key-row offset and column offset
+    const int tr_row = (lane & 15) >> 2;
+    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     f32x16 o[NDB];
 #pragma unroll
@@ -234,9 +234,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
                     const int key = kb * 32 + 16 * mm + 4 * g;
 #pragma unroll
                     for (int db = 0; db < NDB; ++db) {
-                        const __bf16* vrow = &Vt[buf][db * 32 + l32][0];
-                        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow + key);
-                        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + key + 8);
+                        // lane (group G = lane / 16, i = lane % 16) addresses key row
+                        // key + i / 4, columns db*32 + 16 (G % 2) + 4 (i % 4); it receives
+                        // column db*32 + l32 of keys key + {0..3} (then + 8 + {0..3})
+                        const __bf16* vp = &Vs[buf][key + tr_row][db * 32 + tr_col];
+                        const bf16x4 lo = ds_read_tr16(vp);
+                        const bf16x4 hi = ds_read_tr16(vp + 8 * VS);
                         const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                         o[db] = mfma32x32x16bf16(a, pb[kb][mm], o[db]);
                     }
