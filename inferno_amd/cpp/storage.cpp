@@ -69,10 +69,13 @@ HIPStorage::HIPStorage(size_t nbytes, int device_index) : m_nbytes(nbytes), m_de
             return;
         }
     }
+    // An error that an earlier HIP call left pending is raised here, named,
+    // instead of being cleared with this allocation's own out-of-memory status.
+    detail::hip_check(hipGetLastError(), "HIP error pending from an earlier call (before hipMallocAsync)");
     detail::DeviceGuard g(device_index);
     hipError_t e = hipMallocAsync(&m_ptr, cls, detail::stream_for(device_index));
     if (e == hipErrorOutOfMemory) {
-        (void)hipGetLastError();
+        (void)hipGetLastError();  // this allocation's own failure: release the cache and retry once
         {
             std::lock_guard<std::mutex> lk(c.mu);
             release_cache(c, device_index);

@@ -622,13 +622,18 @@ static double cu_makespan(const std::vector<double>& cost, int cus_per_xcd, int 
 }
 
 // Resident backward workgroups per CU, and CUs per XCD, on the current device.
-static void bwd_slots(int D, int bf16, int* per_cu, int* cus_per_xcd) {
+// An error left pending by an earlier HIP call on this thread is returned
+// (named in the detail text) instead of being cleared by the queries here.
+static int bwd_slots(int D, int bf16, int* per_cu, int* cus_per_xcd) {
     static std::mutex mu;
     static std::map<std::array<int, 3>, std::pair<int, int>> cache;
+    const hipError_t pending = hipGetLastError();
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess) {
-        (void)hipGetLastError();
+        (void)hipGetLastError();  // no device (a CPU-only host sizing workspaces): MI355X defaults
         dev = -1;
+    } else if (pending != hipSuccess) {
+        return report_pending_error(pending, "attention backward planner");
     }
     std::lock_guard<std::mutex> lk(mu);
     const std::array<int, 3> key{dev, D, bf16};
@@ -647,12 +652,13 @@ static void bwd_slots(int D, int bf16, int* per_cu, int* cus_per_xcd) {
                 e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<128, float>, 64 * bwd_waves(0, 128), 0);
             if (bf16) e = (hipError_t)bwd_main_bf16_occupancy(D, &o);
             if (e == hipSuccess && o > 0) occ = o;
-            (void)hipGetLastError();
+            (void)hipGetLastError();  // a failed query of ours: the defaults stand
         }
         it = cache.emplace(key, std::make_pair(occ, std::max(1, cus / 8))).first;
     }
     *per_cu = it->second.first;
     *cus_per_xcd = it->second.second;
+    return 0;
 }
 
 static void bwd_plan_compute(int B, int H, int Tq, int Tk, int D, int bf16, int per_cu, int cus_per_xcd,
@@ -734,12 +740,12 @@ static void bwd_plan_compute(int B, int H, int Tq, int Tk, int D, int bf16, int 
     out->n_slots = n_slots;
 }
 
-void bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan* out) {
+int bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan* out) {
     *out = BwdPlan{};
     out->bk = bwd_keys_per_wg(bf16, D);
-    if (!causal) return;
+    if (!causal) return 0;
     int per_cu = 0, cus_per_xcd = 0;
-    bwd_slots(D, bf16, &per_cu, &cus_per_xcd);
+    if (const int e = bwd_slots(D, bf16, &per_cu, &cus_per_xcd)) return e;
     static std::mutex mu;
     static std::map<std::array<int, 7>, BwdPlan> cache;
     const std::array<int, 7> key{B * H, Tq, Tk, D, bf16, per_cu, cus_per_xcd};
@@ -748,13 +754,14 @@ void bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan
         auto it = cache.find(key);
         if (it != cache.end()) {
             *out = it->second;
-            return;
+            return 0;
         }
     }
     bwd_plan_compute(B, H, Tq, Tk, D, bf16 ? 1 : 0, per_cu, cus_per_xcd, out);
     std::lock_guard<std::mutex> lk(mu);
     if (cache.size() > 256) cache.clear();
     cache[key] = *out;
+    return 0;
 }
 
 size_t bwd_split_workspace_bytes(const BwdPlan& plan, int B, int H, int D) {

@@ -467,18 +467,26 @@ static double fwd_makespan(const int* cost, int n_groups, int BH, int slots_per_
 struct FwdSlots {
     int per_xcd, cus;
 };
-static FwdSlots fwd_slots(int D, int bf16) {
+// An error left pending by an earlier HIP call on this thread is returned
+// (named in the detail text) instead of being cleared by the queries here.
+static int fwd_slots(int D, int bf16, FwdSlots* out) {
     static std::mutex mu;
     static std::map<std::array<int, 3>, FwdSlots> cache;
+    const hipError_t pending = hipGetLastError();
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess) {
-        (void)hipGetLastError();
+        (void)hipGetLastError();  // no device (a CPU-only host sizing workspaces): MI355X defaults
         dev = -1;
+    } else if (pending != hipSuccess) {
+        return report_pending_error(pending, "attention forward planner");
     }
     std::lock_guard<std::mutex> lk(mu);
     const std::array<int, 3> key{dev, D, bf16};
     auto it = cache.find(key);
-    if (it != cache.end()) return it->second;
+    if (it != cache.end()) {
+        *out = it->second;
+        return 0;
+    }
     // MI355X: 256 CUs; fp32: two D <= 64 workgroups per CU, one at D = 128.
     int cus = 256, per_cu = bf16 ? (D >= 128 ? 2 : 4) : (D >= 128 ? 1 : 2);
     if (dev >= 0) {
@@ -490,11 +498,12 @@ static FwdSlots fwd_slots(int D, int bf16) {
         else if (D == 64) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<64, float>, 256, 0);
         else if (D == 128) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, attn_fwd_kernel<128, float>, 256, 0);
         if (e == hipSuccess && occ > 0) per_cu = occ;
-        (void)hipGetLastError();
+        (void)hipGetLastError();  // a failed query of ours: the defaults stand
     }
     const FwdSlots slots{std::max(1, cus * per_cu / 8), cus};
     cache[key] = slots;
-    return slots;
+    *out = slots;
+    return 0;
 }
 
 // Causal forward split plan.  Without a split the query tiles run heaviest
@@ -614,11 +623,12 @@ static void fwd_plan_compute(int B, int H, int Tq, int Tk, int D, int bf16, FwdS
     out->n_slots = ns;
 }
 
-void fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan* out) {
+int fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan* out) {
     *out = FwdPlan{};
     bf16 = bf16 ? 1 : 0;
-    if (!causal || (D != 32 && D != 64 && D != 128)) return;
-    const FwdSlots slots = fwd_slots(D, bf16);
+    if (!causal || (D != 32 && D != 64 && D != 128)) return 0;
+    FwdSlots slots{};
+    if (const int e = fwd_slots(D, bf16, &slots)) return e;
     static std::mutex mu;
     static std::map<std::array<int, 7>, FwdPlan> cache;
     const std::array<int, 7> key{B * H, Tq, Tk, D, bf16, slots.per_xcd, slots.cus};
@@ -627,13 +637,14 @@ void fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan
         auto it = cache.find(key);
         if (it != cache.end()) {
             *out = it->second;
-            return;
+            return 0;
         }
     }
     fwd_plan_compute(B, H, Tq, Tk, D, bf16, slots, out);
     std::lock_guard<std::mutex> lk(mu);
     if (cache.size() > 256) cache.clear();
     cache[key] = *out;
+    return 0;
 }
 
 size_t fwd_workspace_bytes(const FwdPlan& plan, int B, int H, int D) {

@@ -96,6 +96,12 @@ thread_local std::string t_detail;
 
 namespace inf {
 void set_error_detail(const std::string& msg) { t_detail = msg; }
+
+int report_pending_error(hipError_t e, const char* where) {
+    set_error_detail(std::string(where) + ": HIP error pending from an earlier call: " + hipGetErrorName(e) + " (" +
+                     hipGetErrorString(e) + "); nothing launched");
+    return (int)e;
+}
 }  // namespace inf
 
 extern "C" {
@@ -125,14 +131,16 @@ int inf_get_deterministic(void) { return g_deterministic.load(); }
 
 namespace {
 
-size_t bwd_workspace_bytes(int det, int B, int H, int Tq, int Tk, int D, inf_dtype dt) {
+// INF_OK, or INF_ERR_HIP when an earlier call left a HIP error pending.
+int bwd_workspace_bytes(int det, int B, int H, int Tq, int Tk, int D, inf_dtype dt, size_t* out) {
     const size_t bh = (size_t)B * H;
     size_t n = round_up(bh * Tq * sizeof(float));  // delta
     if (dt == INF_BF16 && !dq_from_pass(det, B, H, Tq, Tk, D, dt))
         n += round_up(bh * Tq * (size_t)D * sizeof(float));  // dQ accumulator
     inf::BwdPlan plan;                                        // causal split plan
-    inf::bwd_plan(B, H, Tq, Tk, D, 1, dt == INF_BF16, &plan);
-    return n + round_up(inf::bwd_split_workspace_bytes(plan, B, H, D));
+    if (inf::bwd_plan(B, H, Tq, Tk, D, 1, dt == INF_BF16, &plan)) return INF_ERR_HIP;
+    *out = n + round_up(inf::bwd_split_workspace_bytes(plan, B, H, D));
+    return INF_OK;
 }
 
 }  // namespace
@@ -148,13 +156,12 @@ int inf_attn_workspace_bytes(int op, int B, int H, int Tq, int Tk, int D, inf_dt
     switch (op) {
         case INF_OP_ATTN_FWD: {
             inf::FwdPlan plan;
-            inf::fwd_plan(B, H, Tq, Tk, D, 1, dt == INF_BF16, &plan);
+            if (inf::fwd_plan(B, H, Tq, Tk, D, 1, dt == INF_BF16, &plan)) return INF_ERR_HIP;
             *out_bytes = round_up(inf::fwd_workspace_bytes(plan, B, H, D));
             return INF_OK;
         }
         case INF_OP_ATTN_BWD:
-            *out_bytes = bwd_workspace_bytes(g_deterministic.load(), B, H, Tq, Tk, D, dt);
-            return INF_OK;
+            return bwd_workspace_bytes(g_deterministic.load(), B, H, Tq, Tk, D, dt, out_bytes);
         case INF_OP_ATTN_DECODE: {
             int ns = 1, ch = 0;
             inf::decode_plan(B, H, Tk, D, &ns, &ch);
@@ -185,7 +192,7 @@ int inf_attn_fwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     p.c = scale * 1.4426950408889634f;
     p.n_qtiles = (Tq + inf::kFwdBM - 1) / inf::kFwdBM;
     inf::FwdPlan plan;
-    inf::fwd_plan(B, H, Tq, Tk, D, p.causal, dt == INF_BF16, &plan);
+    if (inf::fwd_plan(B, H, Tq, Tk, D, p.causal, dt == INF_BF16, &plan)) return INF_ERR_HIP;
     const size_t need = inf::fwd_workspace_bytes(plan, B, H, D);
     if (need && (!workspace || ws_bytes < need)) return INF_ERR_WORKSPACE;
     if (need && reinterpret_cast<uintptr_t>(workspace) % kAlign) return INF_ERR_ALIGNMENT;
@@ -218,7 +225,8 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
         (st = check_out_view(dk, sdk, dt, B, H, Tk, D)) || (st = check_out_view(dv, sdv, dt, B, H, Tk, D)))
         return st;
     const int det = g_deterministic.load();  // one reading for the whole call
-    const size_t need = bwd_workspace_bytes(det, B, H, Tq, Tk, D, dt);
+    size_t need = 0;
+    if ((st = bwd_workspace_bytes(det, B, H, Tq, Tk, D, dt, &need))) return st;
     if (!workspace || ws_bytes < need) return INF_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(workspace) % kAlign) return INF_ERR_ALIGNMENT;
 
@@ -248,7 +256,7 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     p.n_qtiles = (Tq + inf::kBwdDqBM - 1) / inf::kBwdDqBM;
     if (p.dq_direct) p.dq_acc = nullptr;  // dq is written by the dQ pass
     inf::BwdPlan plan;
-    inf::bwd_plan(B, H, Tq, Tk, D, p.causal, dt == INF_BF16, &plan);
+    if (inf::bwd_plan(B, H, Tq, Tk, D, p.causal, dt == INF_BF16, &plan)) return INF_ERR_HIP;
     if (plan.n_groups) {
         size_t offset = round_up(bh * Tq * sizeof(float));
         if (dt == INF_BF16 && !p.dq_direct) offset += round_up(bh * Tq * (size_t)D * sizeof(float));

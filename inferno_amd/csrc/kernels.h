@@ -52,7 +52,8 @@ struct FwdPlan {
     int n_split = 0;
     int split_qt[kMaxFwdGroups / 2], split_slot0[kMaxFwdGroups / 2], split_count[kMaxFwdGroups / 2];
 };
-void fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan* out);
+// Returns 0, or the HIP error an earlier call left pending (see report_pending_error).
+int fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan* out);
 size_t fwd_workspace_bytes(const FwdPlan& plan, int B, int H, int D);
 
 // Backward work split: a group is one key block's query-tile range [t0, t1)
@@ -72,7 +73,8 @@ struct BwdPlan {
     int bk = 0;  // keys per workgroup of the kernel the plan is for
     BwdGroup groups[kMaxBwdGroups];
 };
-void bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan* out);
+// Returns 0, or the HIP error an earlier call left pending (see report_pending_error).
+int bwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, BwdPlan* out);
 // Bytes of the split plan's workspace: partials then counters (0 without a split).
 size_t bwd_split_workspace_bytes(const BwdPlan& plan, int B, int H, int D);
 
@@ -229,6 +231,10 @@ int launch_gemm(const GemmArgs& g, hipStream_t s);
 
 // Thread-local text about the last failure inside the library (inf_last_error_detail).
 void set_error_detail(const std::string& msg);
+// Names a HIP error that an earlier, unrelated call left pending on this
+// thread (found before a query of ours would clear it) in the detail text,
+// and returns it, so the entry point fails with INF_ERR_HIP and launches nothing.
+int report_pending_error(hipError_t e, const char* where);
 
 constexpr int kLnBwdMaxBlocks = 512;  // stage-1 workgroups of the LayerNorm backward
 constexpr int kColChunk = 32;         // rows per partial of the column sum
@@ -266,7 +272,8 @@ int launch_attn_decode(const DecodeParams& p, int bf16, hipStream_t s);
 void decode_plan(int B, int H, int Tk, int D, int* nsplit, int* chunk);
 // The static scratch of inf_attn_decode_static (4 MiB: every shape whose
 // B*H*nsplit*(D+2) floats fit; the plan keeps B*H*nsplit below 8192, so only
-// some D = 128 shapes with 4033 <= B*H*nsplit <= 8191 need more), and its
+// D = 128 shapes with 8066 <= B*H*nsplit <= 8191 need more: 4 MiB holds 8065
+// rows of 130 floats), and its
 // device address on the current device (looked up once per device).
 constexpr size_t kDecodeScratchBytes = (size_t)4 << 20;
 int decode_scratch(float** out);

@@ -51,9 +51,12 @@ def attn_fwd(q, k, v, causal=True, scale=None, out=None, lse=None, workspace=Non
         out = torch.empty((B, H, Tq, D), dtype=q.dtype, device=q.device)
     if lse is None:
         lse = torch.empty((B, H, Tq), dtype=torch.float32, device=q.device)
-    nbytes = workspace_bytes(OP_ATTN_FWD, B, H, Tq, Tk, D, _dt(q)) if causal else 0
-    if workspace is None and nbytes:
-        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    # a caller-supplied workspace is passed as is (the C-ABI checks its size):
+    # no sizing round trip on that path
+    if workspace is None and causal:
+        nbytes = workspace_bytes(OP_ATTN_FWD, B, H, Tq, Tk, D, _dt(q))
+        if nbytes:
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
     st = lib().inf_attn_fwd(
@@ -74,8 +77,8 @@ def attn_bwd(q, k, v, o, dout, lse, causal=True, scale=None, dq=None, dk=None, d
     dq = torch.empty_like(q, memory_format=torch.contiguous_format) if dq is None else dq
     dk = torch.empty_like(k, memory_format=torch.contiguous_format) if dk is None else dk
     dv = torch.empty_like(v, memory_format=torch.contiguous_format) if dv is None else dv
-    nbytes = workspace_bytes(OP_ATTN_BWD, B, H, Tq, Tk, D, _dt(q))
     if workspace is None:
+        nbytes = workspace_bytes(OP_ATTN_BWD, B, H, Tq, Tk, D, _dt(q))
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     st = lib().inf_attn_bwd(
         q.data_ptr(), strides_of(q), k.data_ptr(), strides_of(k), v.data_ptr(), strides_of(v),
@@ -95,8 +98,8 @@ def attn_decode(q, kcache, vcache, scale=None, out=None, workspace=None, stream=
     scale = default_scale(D) if scale is None else float(scale)
     if out is None:
         out = torch.empty((B, H, 1, D), dtype=q.dtype, device=q.device)
-    nbytes = workspace_bytes(OP_ATTN_DECODE, B, H, 1, Tk, D, _dt(q))
     if workspace is None:
+        nbytes = workspace_bytes(OP_ATTN_DECODE, B, H, 1, Tk, D, _dt(q))
         workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
     st = lib().inf_attn_decode(
         q.data_ptr(), strides_of(q), kcache.data_ptr(), strides_of(kcache), vcache.data_ptr(),

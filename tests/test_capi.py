@@ -273,8 +273,12 @@ def test_static_decode_validation():
     assert L.inf_attn_decode_static(FAKE, sq, FAKE, skv, FAKE, skv, FAKE, sq, B, H, Tk, D, 0.125, ia.INF_F32,
                                     None) == 6
     assert b"static scratch" in L.inf_last_error_detail()
-    # 4032 rows: 4032 * 2 * 130 * 4 bytes fit
+    # 4032 rows: 4032 * 2 * 130 * 4 bytes fit; 4033 rows (8066 partial rows of 130 floats) do not
     assert ia.workspace_bytes(ia.OP_ATTN_DECODE, 1, 4032, 1, Tk, D) <= 4 << 20
+    assert ia.workspace_bytes(ia.OP_ATTN_DECODE, 1, 4033, 1, Tk, D) > 4 << 20
+    sq, skv = dense(1, 4033, 1, D), dense(1, 4033, Tk, D)
+    assert L.inf_attn_decode_static(FAKE, sq, FAKE, skv, FAKE, skv, FAKE, sq, 1, 4033, Tk, D, 0.125, ia.INF_F32,
+                                    None) == 6
 
 
 def test_add_layernorm_validation():
