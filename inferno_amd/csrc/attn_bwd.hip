@@ -122,6 +122,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
     __shared__ __attribute__((aligned(16))) float Kts[D][KTS];
     __shared__ __attribute__((aligned(16))) float lse_s[BQ];
     __shared__ __attribute__((aligned(16))) float dl_s[BQ];
+    __shared__ __attribute__((aligned(16))) float dlo_s[BQ];  // low part of the short rows' delta (else 0)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -145,6 +146,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
     float* dQa = p.dq_acc + b * p.sacc.b + h * p.sacc.h;
     const float* LSE = p.lse + (int64_t)bh * p.Tq;
     const float* DL = p.delta + (int64_t)bh * p.Tq;
+    const float* DLO = p.delta_lo + (int64_t)bh * p.Tq;
 
     const int k0 = kblk * BK;
     const int k0w = k0 + wave * 32;
@@ -165,20 +167,6 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
     } else {
 #pragma unroll
         for (int i = 0; i < HD; ++i) kf[i] = vf[i] = 0.f;
-    }
-
-    // K^T of the whole key block in LDS, for the dQ product.
-#pragma unroll
-    for (int i = 0; i < KLPT; ++i) {
-        const int f = tid + NT * i;
-        const int r = f / C4;
-        const int c4 = f % C4;
-        f32x4 val = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (k0 + r < p.Tk) val = ld4(K + (int64_t)(k0 + r) * p.sk.t + 4 * c4);
-        Kts[4 * c4 + 0][r] = val[0];
-        Kts[4 * c4 + 1][r] = val[1];
-        Kts[4 * c4 + 2][r] = val[2];
-        Kts[4 * c4 + 3][r] = val[3];
     }
 
     f32x16 dv_acc[NDB], dk_acc[NDB];
@@ -205,7 +193,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
     static_assert(NT % C4 == 0, "chunk rows must split into thread + load parts");
     static_assert(sizeof(E) == 4, "fp32 storage (bf16 has its own kernel)");
     f32x4 ra[QLPT], rd[QLPT];
-    float r_lse = 0.f, r_dl = 0.f;
+    float r_lse = 0.f, r_dl = 0.f, r_dlo = 0.f;
     const uint32_t q_voff = (uint32_t)(((int64_t)(tid / C4) * p.sq.t + 4 * (tid % C4)) * 4);
     const uint32_t do_voff = (uint32_t)(((int64_t)(tid / C4) * p.sdo.t + 4 * (tid % C4)) * 4);
     auto gload_q = [&](int q0, int lim) {
@@ -220,6 +208,9 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
         // lanes past the tile's rows (all but the first BQ threads) read zeros
         r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
         r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
+        // rows past the short ones (and every row outside key block 0) read 0
+        const int n_sh = kblk == 0 ? max(0, min(p.n_short - q0, rows)) : 0;
+        r_dlo = buffer_ld1(row_rsrc(DLO, 1, q0, n_sh, 1), (uint32_t)tid * 4, 0);
     };
     auto sstore_q = [&]() {
 #pragma unroll
@@ -231,8 +222,82 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
         if (tid < BQ) {
             lse_s[tid] = r_lse;  // natural-log LSE; scaled by log2(e) where it is read
             dl_s[tid] = r_dl;
+            dlo_s[tid] = r_dlo;
         }
     };
+    // Short rows (bwd_split.h): before the main loop, their delta from this
+    // block's own S and dP.  Per short tile each wave forms S^T and dP^T of its
+    // 32 keys (the main loop's chains with the operands swapped, so lane
+    // (l32, g) holds query q0 + l32 and keys 8 (r / 4) + 4 g + r % 4 of the
+    // wave), the weights e = exp2(S c - lse log2 e) (1 for a one-key row's
+    // key), and per query sum(e) and sum(e dP) in fp64 (exact products) over
+    // its registers and the lane pair (l32, l32 + 32); the workgroup's first
+    // BQ threads add the waves' sums in wave order and store delta = sum(e dP)
+    // / sum(e) as hi + lo.  Each tile's loads are issued while the previous one
+    // computes; the main loop's first barrier orders the last sums' reads
+    // before it writes the dS tile they sit in.
+    const int qs_end = kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short tiles: [q_begin, qs_end)
+    if (q_begin < qs_end) {
+        double* part = reinterpret_cast<double*>(&dSs[0][0]);  // [NW][BQ] pairs (sum e, sum e dP)
+        static_assert(2 * NW * BQ * sizeof(double) <= sizeof(dSs), "the sums fit the dS tile");
+        gload_q(q_begin, p.Tq);
+        for (int q0 = q_begin; q0 < qs_end; q0 += BQ) {
+            sstore_q();
+            __syncthreads();
+            if (q0 + BQ < qs_end) gload_q(q0 + BQ, p.Tq);
+            double l = 0.0, w = 0.0;
+            if ((!p.causal || (q0 + BQ - 1 + p.off >= k0w)) && k0w < p.Tk) {
+                f32x16 st, dpt;
+#pragma unroll
+                for (int i = 0; i < HD; i += 4) {
+                    const f32x4 qa = *reinterpret_cast<const f32x4*>(&Qs[l32][g * HD + i]);
+                    const f32x4 da = *reinterpret_cast<const f32x4*>(&dOs[l32][g * HD + i]);
+                    st = mfma32x32x2(kf[i + 0], qa[0], i == 0 ? f32x16{} : st);
+                    dpt = mfma32x32x2(vf[i + 0], da[0], i == 0 ? f32x16{} : dpt);
+                    st = mfma32x32x2(kf[i + 1], qa[1], st);
+                    dpt = mfma32x32x2(vf[i + 1], da[1], dpt);
+                    st = mfma32x32x2(kf[i + 2], qa[2], st);
+                    dpt = mfma32x32x2(vf[i + 2], da[2], dpt);
+                    st = mfma32x32x2(kf[i + 3], qa[3], st);
+                    dpt = mfma32x32x2(vf[i + 3], da[3], dpt);
+                }
+                const int qi = q0 + l32;
+                const float L = lse_s[l32] * kLog2e;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int kj = k0w + 8 * (r >> 2) + 4 * g + (r & 3);
+                    const bool vis = (qi < p.Tq) && (kj < p.Tk) && (!p.causal || kj <= qi + p.off);
+                    const float e = bwd_short_weight(p, qi, vis, fast_exp2(fmaf(st[r], c, -L)));
+                    l += (double)e;
+                    w += (double)e * (double)dpt[r];
+                }
+            }
+            l += __shfl_xor(l, 32);
+            w += __shfl_xor(w, 32);
+            if (g == 0) {
+                part[2 * (wave * BQ + l32)] = l;
+                part[2 * (wave * BQ + l32) + 1] = w;
+            }
+            __syncthreads();
+            if (tid < BQ) bwd_short_delta_store<NW, BQ>(p, bh, q0 + tid, part + 2 * tid);
+        }
+    }
+
+    // K^T of the whole key block in LDS, for the dQ product.
+#pragma unroll
+    for (int i = 0; i < KLPT; ++i) {
+        const int f = tid + NT * i;
+        const int r = f / C4;
+        const int c4 = f % C4;
+        f32x4 val = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (k0 + r < p.Tk) val = ld4(K + (int64_t)(k0 + r) * p.sk.t + 4 * c4);
+        Kts[4 * c4 + 0][r] = val[0];
+        Kts[4 * c4 + 1][r] = val[1];
+        Kts[4 * c4 + 2][r] = val[2];
+        Kts[4 * c4 + 3][r] = val[3];
+    }
+
+
     if constexpr (PF) {
         gload_q(q_begin, p.Tq);
         sstore_q();
@@ -274,6 +339,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
                 for (int j = 0; j < 4; ++j) {
                     const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLog2e;
                     const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
+                    const f32x4 Dlo = *reinterpret_cast<const f32x4*>(&dlo_s[8 * j + 4 * g]);
 #pragma unroll
                     for (int cc = 0; cc < 4; ++cc) {
                         const int r = 4 * j + cc;
@@ -284,7 +350,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
                             pr = vis ? pr : 0.f;
                         }
                         s[r] = pr;
-                        ds[r] = pr * (dp[r] - Dl[cc]);
+                        ds[r] = pr * ((dp[r] - Dl[cc]) - Dlo[cc]);
                     }
                 }
             };
@@ -457,6 +523,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void bwd_dq_kernel(BwdParams
     }
     const float Lq = qrow < p.Tq ? p.lse[(int64_t)bh * p.Tq + qrow] * kLog2e : 0.f;
     const float Dq = qrow < p.Tq ? p.delta[(int64_t)bh * p.Tq + qrow] : 0.f;
+    const float Dqlo = bwd_short_row(p, qrow) ? p.delta_lo[(int64_t)bh * p.Tq + qrow] : 0.f;
 
     int kv_end = p.Tk;
     if (p.causal) kv_end = min(p.Tk, qtile * BM + BM + p.off);
@@ -525,7 +592,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void bwd_dq_kernel(BwdParams
                     const int key = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
                     pr = (key <= lim && qrow < p.Tq) ? pr : 0.f;
                 }
-                s[r] = pr * (dp[r] - Dq);  // dS^T
+                s[r] = pr * ((dp[r] - Dq) - Dqlo);  // dS^T
             }
             // dQ^T[d][q] += K^T[d][keys] dS^T[keys][q]: MFMA (j, cc) reduces keys 8j + cc, 8j + 4 + cc
 #pragma unroll
@@ -578,6 +645,9 @@ static constexpr double kBwdPairGain = 0.08;  // throughput gained per extra res
 // the device's size.
 static constexpr double kBwdOverhead[2] = {0.3, 5.0};
 static constexpr double kBwdFixup[2] = {0.4, 8.0};
+// The short-row prologue of key block 0 (the S and dP chains of each short
+// query tile, run once more to form delta) per short tile, in the same units.
+static constexpr double kBwdShortTile[2] = {0.55, 0.5};
 
 static double share_rate(size_t k) { return k <= 1 ? 1.0 : (1.0 + kBwdPairGain * (double)(k - 1)) / (double)k; }
 
@@ -675,16 +745,33 @@ static void bwd_plan_compute(int B, int H, int Tq, int Tk, int D, int bf16, int 
         nt[(size_t)j] = (Tq + kBwdBQ - 1) / kBwdBQ - t0[(size_t)j];
         max_nt = std::max(max_nt, nt[(size_t)j]);
     }
+    // query tiles [0, s_tiles) of key block 0 hold its short rows and run the prologue
+    const int s_tiles = (bwd_short_rows(Tq, Tk, 1, bk) + kBwdBQ - 1) / kBwdBQ;
     struct G { double cost; int kb, a, b, chunk, n; };
-    auto build = [&](int ch, std::vector<G>& g) {
+    // A key block of more than ch tiles is split into ceil(n / ch) chunks of
+    // near-equal cost, block 0's short tiles counted with the prologue's share
+    // pro.  The chunk size is chosen with pro = 0: counting the prologue there
+    // moved the choice to plans measured slower (config 2 fp32: ch 27-31, which
+    // leave key block 1 whole, +6-10%), while cutting block 0 at the weighted
+    // midpoint recovered half of the prologue's cost at the chosen size.
+    auto build = [&](int ch, double pro, std::vector<G>& g) {
         g.clear();
         for (int j = 0; j < nkb; ++j) {
-            const int n = nt[(size_t)j];
+            const int n = nt[(size_t)j], s = j == 0 ? s_tiles : 0;
             const int k = n > ch ? (n + ch - 1) / ch : 1;
+            auto work = [&](int t) { return (double)t + pro * std::min(t, s); };  // tiles [0, t)
+            int a = 0;
             for (int c = 0; c < k; ++c) {
-                const int a = (int)((int64_t)n * c / k), b = (int)((int64_t)n * (c + 1) / k);
-                g.push_back({(double)(b - a) + kBwdOverhead[bf16] + (k > 1 ? kBwdFixup[bf16] : 0.0), j, t0[(size_t)j] + a,
-                             t0[(size_t)j] + b, c, k});
+                int e = n;
+                if (c + 1 < k) {  // the cut nearest cost share c + 1, leaving a tile for each later chunk
+                    const double target = work(n) * (c + 1) / k;
+                    e = a + 1;
+                    while (e < n - (k - c - 1) && work(e) < target) ++e;
+                    if (e > a + 1 && target - work(e - 1) < work(e) - target) --e;
+                }
+                const double cost = work(e) - work(a) + kBwdOverhead[bf16] + (k > 1 ? kBwdFixup[bf16] : 0.0);
+                g.push_back({cost, j, t0[(size_t)j] + a, t0[(size_t)j] + e, c, k});
+                a = e;
             }
         }
         std::stable_sort(g.begin(), g.end(), [](const G& x, const G& y) { return x.cost > y.cost; });
@@ -699,12 +786,12 @@ static void bwd_plan_compute(int B, int H, int Tq, int Tk, int D, int bf16, int 
         return cu_makespan(cost, cus_per_xcd, per_cu);
     };
     std::vector<G> g;
-    build(max_nt, g);
+    build(max_nt, 0.0, g);
     const double base = makespan(g, BH);
     double best = base * 0.97;
     int best_ch = 0;
     for (int ch = max_nt - 1; ch >= std::max(2, max_nt / 8); --ch) {
-        build(ch, g);
+        build(ch, 0.0, g);
         int n_split = 0;
         for (const G& x : g) n_split += x.chunk == 0 && x.n > 1;
         if ((int)g.size() > kMaxBwdGroups || n_split == 0) continue;
@@ -715,15 +802,15 @@ static void bwd_plan_compute(int B, int H, int Tq, int Tk, int D, int bf16, int 
         }
     }
     if (!best_ch) return;
-    build(best_ch, g);
-    std::vector<int> split_of((size_t)nkb, -1), slot0((size_t)nkb, 0);
+    build(best_ch, kBwdShortTile[bf16], g);
+    std::vector<int> chunks((size_t)nkb, 1), split_of((size_t)nkb, -1), slot0((size_t)nkb, 0);
+    for (const G& x : g) chunks[(size_t)x.kb] = x.n;
     int n_split = 0, n_slots = 0;
     for (int j = 0; j < nkb; ++j) {
-        const int n = nt[(size_t)j];
-        if (n > best_ch) {
+        if (chunks[(size_t)j] > 1) {
             split_of[(size_t)j] = n_split++;
             slot0[(size_t)j] = n_slots;
-            n_slots += (n + best_ch - 1) / best_ch;
+            n_slots += chunks[(size_t)j];
         }
     }
     for (const G& x : g) {

@@ -42,7 +42,123 @@ __device__ __forceinline__ f32x4 mfma16x16x32bf16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int D>
+// Short rows' delta (bwd_split.h) for the key-block-0 workgroup, before its
+// main loop, query-major from LDS.  K and V of the block's first BK keys and a
+// batch of PR short query rows of Q and dO are staged in LDS (over the main
+// loop's arrays, which are not live yet), then wave w takes the row tile of RT
+// rows at batch + RT w: lane (lr, gq) holds row q = tile + lr, with its Q and
+// dO values (the B operand, the main loop's k order) in registers, and walks
+// the tile's visible keys in key tiles of RT keys, K and V rows (the A
+// operand) read from LDS.  S^T and dP^T come from the main loop's MFMA shape
+// with A and B swapped: the same products in the same k order.  Each lane adds
+// e and e * dP over its keys in key order in fp64, the row's lane groups are
+// added in a fixed pattern, and the row's first lane stores delta = sum(e dP)
+// / sum(e) as hi + lo to the workspace and, for the D <= 64 kernel, -hi to sdl
+// (its staging reads it from there).  No barrier between the staging and the
+// end of a batch.
+//   M32 = true:  v_mfma_f32_32x32x16_bf16, RT = 32, lane (l32, g) supplies
+//                columns 16 kk + 8 g .. + 7, register r is key 8 (r/4) + 4 g + r%4
+//   M32 = false: v_mfma_f32_16x16x32_bf16, RT = 16, lane (l16, g4) supplies
+//                columns 32 kk + 8 g4 .. + 7, register r is key 4 g4 + r
+template <int D, int NW, int BK, int PR, int PSTR, bool M32>
+__device__ __forceinline__ void bwd_short_prologue(const BwdParams& p, int bh, const __bf16* Q, const __bf16* K,
+                                                   const __bf16* V, const __bf16* dO, int q_begin, int qs_end,
+                                                   __bf16 (*ks)[PSTR], __bf16 (*vs)[PSTR], __bf16 (*qs)[PSTR],
+                                                   __bf16 (*ds)[PSTR], float* sdl) {
+    constexpr int NT = 64 * NW;
+    constexpr int RT = M32 ? 32 : 16;
+    constexpr int NCH = M32 ? D / 16 : D / 32;  // MFMAs per product
+    constexpr int CW = M32 ? 16 : 32;           // columns per MFMA
+    constexpr int NR = M32 ? 16 : 4;            // output registers
+    constexpr int C8 = D / 8;                   // 16-byte chunks per row
+    static_assert(PR == NW * RT, "one row tile per wave per batch");
+    typedef typename std::conditional<M32, f32x16, f32x4>::type Acc;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = M32 ? (lane & 31) : (lane & 15);
+    const int gq = M32 ? (lane >> 5) : (lane >> 4);
+    const float c = p.c;
+    // K and V of the keys these rows can see (at most the block), staged once
+    const int kmax = p.causal ? min(p.Tk, min(qs_end, p.Tq) - 1 + p.off + 1) : p.Tk;  // <= BK
+    {
+        const auto rk = row_rsrc(K, p.sk.t, 0, kmax, D);
+        const auto rv = row_rsrc(V, p.sv.t, 0, kmax, D);
+        for (int f = tid; f < BK * C8; f += NT) {
+            const int r = f / C8, c8 = f % C8;
+            *reinterpret_cast<bf16x8*>(&ks[r][8 * c8]) = buffer_ld8bf(rk, (uint32_t)(((int64_t)r * p.sk.t + 8 * c8) * 2), 0);
+            *reinterpret_cast<bf16x8*>(&vs[r][8 * c8]) = buffer_ld8bf(rv, (uint32_t)(((int64_t)r * p.sv.t + 8 * c8) * 2), 0);
+        }
+    }
+    for (int b0 = q_begin; b0 < qs_end; b0 += PR) {
+        {
+            const int nrow = min(p.Tq - b0, PR);
+            const auto rq = row_rsrc(Q, p.sq.t, b0, nrow, D);
+            const auto rdo = row_rsrc(dO, p.sdo.t, b0, nrow, D);
+            for (int f = tid; f < PR * C8; f += NT) {
+                const int r = f / C8, c8 = f % C8;
+                *reinterpret_cast<bf16x8*>(&qs[r][8 * c8]) = buffer_ld8bf(rq, (uint32_t)(((int64_t)r * p.sq.t + 8 * c8) * 2), 0);
+                *reinterpret_cast<bf16x8*>(&ds[r][8 * c8]) = buffer_ld8bf(rdo, (uint32_t)(((int64_t)r * p.sdo.t + 8 * c8) * 2), 0);
+            }
+        }
+        __syncthreads();
+        const int t0 = b0 + RT * wave;
+        if (t0 < qs_end) {
+            const int row = t0 + lr;
+            bf16x8 qf[NCH], df[NCH];
+#pragma unroll
+            for (int kk = 0; kk < NCH; ++kk) {
+                qf[kk] = *reinterpret_cast<const bf16x8*>(&qs[RT * wave + lr][CW * kk + 8 * gq]);
+                df[kk] = *reinterpret_cast<const bf16x8*>(&ds[RT * wave + lr][CW * kk + 8 * gq]);
+            }
+            const float L = row < p.Tq ? p.lse[(int64_t)bh * p.Tq + row] * kLog2e : 0.f;
+            const int kend = p.causal ? min(p.Tk, min(t0 + RT - 1, p.Tq - 1) + p.off + 1) : p.Tk;
+            double le = 0.0, we = 0.0;
+            for (int u = 0; u * RT < kend; ++u) {
+                Acc s, dp;
+#pragma unroll
+                for (int kk = 0; kk < NCH; ++kk) {
+                    const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&ks[u * RT + lr][CW * kk + 8 * gq]);
+                    const bf16x8 va = *reinterpret_cast<const bf16x8*>(&vs[u * RT + lr][CW * kk + 8 * gq]);
+                    if constexpr (M32) {
+                        s = mfma32x32x16bf16(ka, qf[kk], kk == 0 ? Acc{} : s);
+                        dp = mfma32x32x16bf16(va, df[kk], kk == 0 ? Acc{} : dp);
+                    } else {
+                        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[kk], kk == 0 ? Acc{} : s, 0, 0, 0);
+                        dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, df[kk], kk == 0 ? Acc{} : dp, 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    const int key = u * RT + (M32 ? 8 * (r >> 2) + 4 * gq + (r & 3) : 4 * gq + r);
+                    const bool vis = key < p.Tk && row < p.Tq && (!p.causal || key <= row + p.off);
+                    const float e = bwd_short_weight(p, row, vis, fast_exp2(fmaf(s[r], c, -L)));
+                    le += (double)e;
+                    we += (double)e * (double)dp[r];
+                }
+            }
+            if constexpr (!M32) {
+                le += __shfl_xor(le, 16);
+                we += __shfl_xor(we, 16);
+            }
+            le += __shfl_xor(le, 32);
+            we += __shfl_xor(we, 32);
+            if (gq == 0 && bwd_short_row(p, row)) {
+                const double dl = we / le;
+                const float hi = (float)dl;
+                p.delta[(int64_t)bh * p.Tq + row] = hi;
+                p.delta_lo[(int64_t)bh * p.Tq + row] = (float)(dl - (double)hi);
+                if (sdl) sdl[row] = -hi;
+            }
+        }
+        __syncthreads();  // the batch's rows are read before the next batch overwrites them
+    }
+}
+
+// DWS: every query row is short (Tk within one key block), so the staging
+// takes delta from the workspace for every row instead of forming it from O
+// and dO.
+template <int D, bool DWS>
 __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || D >= 128) ? 1 : 2) void bwd_main_bf16_kernel(BwdParams p) {
     constexpr int NW = bwd_bf16_waves(D);  // waves per workgroup, 32 keys each
     constexpr int NT = 64 * NW;            // threads
@@ -72,15 +188,38 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     constexpr float kLseStage = D == 64 ? kLog2e : 1.f;
     constexpr float kLseRead = D == 64 ? 1.f : kLog2e;
 
-    // staged query tile and dS double-buffered: one barrier per tile
-    __shared__ __attribute__((aligned(16))) __bf16 Qs2[2][BQ][QS];
-    __shared__ __attribute__((aligned(16))) __bf16 dOs2[2][BQ][QS];
-    __shared__ __attribute__((aligned(16))) __bf16 QTs2[2][D][TS];
-    __shared__ __attribute__((aligned(16))) __bf16 dOTs2[2][D][TS];
-    __shared__ __attribute__((aligned(16))) __bf16 dSs2[2][BQ][SS];
-    __shared__ __attribute__((aligned(16))) __bf16 KTs[D][KTS];
-    __shared__ __attribute__((aligned(16))) float lse_s2[2][BQ];
-    __shared__ __attribute__((aligned(16))) float dl_s2[2][BQ];
+    // LDS: the main loop's arrays (staged query tile and dS double-buffered:
+    // one barrier per tile) and, over the same bytes, the short-row prologue's
+    // (K and V of the key block, a batch of short Q / dO rows)
+    constexpr int PSTR = D + 8;  // prologue row stride (bf16)
+    constexpr int PR = 32 * NW;  // prologue rows per batch
+    struct MainLds {
+        __bf16 Qs2[2][BQ][QS];
+        __bf16 dOs2[2][BQ][QS];
+        __bf16 QTs2[2][D][TS];
+        __bf16 dOTs2[2][D][TS];
+        __bf16 dSs2[2][BQ][SS];
+        __bf16 KTs[D][KTS];
+        float lse_s2[2][BQ];
+        float dl_s2[2][BQ];
+    };
+    struct ProLds {
+        __bf16 k[BK][PSTR], v[BK][PSTR], q[PR][PSTR], d[PR][PSTR];
+    };
+    __shared__ __attribute__((aligned(16))) union {
+        MainLds m;
+        ProLds pr;
+    } lds;
+    auto& Qs2 = lds.m.Qs2;
+    auto& dOs2 = lds.m.dOs2;
+    auto& QTs2 = lds.m.QTs2;
+    auto& dOTs2 = lds.m.dOTs2;
+    auto& dSs2 = lds.m.dSs2;
+    auto& KTs = lds.m.KTs;
+    auto& lse_s2 = lds.m.lse_s2;
+    auto& dl_s2 = lds.m.dl_s2;
+    // minus the short rows' delta, rows [0, n_short) (n_short <= BK unless DWS)
+    __shared__ float sdl_s[BK];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -120,25 +259,6 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
         }
     }
 
-    // K^T of the key block (keys contiguous per d row), for dQ.
-#pragma unroll
-    for (int i = 0; i < KLPT; ++i) {
-        const int f = tid + NT * i;
-        if (f >= KTASK) continue;
-        const int kp = f % (BK / 2), c8 = f / (BK / 2);
-        const int r0 = k0 + 2 * kp;
-        const bf16x8 a = r0 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)r0 * p.sk.t + 8 * c8) : bf16x8{};
-        const bf16x8 c = r0 + 1 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)(r0 + 1) * p.sk.t + 8 * c8)
-                                       : bf16x8{};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            bf16x2 pr;
-            pr[0] = a[e];
-            pr[1] = c[e];
-            *reinterpret_cast<bf16x2*>(&KTs[8 * c8 + e][2 * kp]) = pr;
-        }
-    }
-
     f32x16 dv_acc[NDB], dk_acc[NDB];
 #pragma unroll
     for (int i = 0; i < NDB; ++i) {
@@ -159,6 +279,7 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     // two barriers per tile the kernel measured 6% slower at config 2.)
     bf16x8 ra[QLPT], rb[QLPT];
     float r_lse = 0.f;
+    float r_dl[QLPT];  // DWS: the delta tasks' rows' delta from the workspace
     // Loads through buffer resources over rows [q0, lim) (<= Tq): rows past
     // them read as zeros, with no address arithmetic or branch per load; raw
     // values only, so no arithmetic waits on the loads here.  Chunk f is a
@@ -171,7 +292,10 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     static_assert(QTASK % 64 == 0, "Q / dO split must be wave-uniform");
     static_assert(4 * QTASK == NT, "Q, dO and delta tasks fill the workgroup once");
     const __bf16* Ob = (const __bf16*)p.o + b * p.so.b + h * p.so.h;
+    const float* DLs = p.delta + (int64_t)bh * p.Tq;
+    int staged_q0 = 0;  // first row of the tile in the staging registers
     auto gload_q = [&](int q0, int lim) {
+        staged_q0 = q0;
         const int rows = min(lim - q0, BQ);
         const auto rq = row_rsrc(Q, p.sq.t, q0, rows, D);
         const auto rdo = row_rsrc(dO, p.sdo.t, q0, rows, D);
@@ -183,9 +307,13 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
             if (which >= 2) {
                 const int rem = f - 2 * QTASK;
                 const int row = rem / C8, c8 = rem % C8;
-                const auto ro = row_rsrc(Ob, p.so.t, q0, rows, D);
-                ra[i] = buffer_ld8bf(ro, (uint32_t)(((int64_t)row * p.so.t + 8 * c8) * 2), 0);
-                rb[i] = buffer_ld8bf(rdo, (uint32_t)(((int64_t)row * p.sdo.t + 8 * c8) * 2), 0);
+                if constexpr (DWS) {
+                    r_dl[i] = buffer_ld1(row_rsrc(DLs, 1, q0, rows, 1), (uint32_t)row * 4, 0);
+                } else {
+                    const auto ro = row_rsrc(Ob, p.so.t, q0, rows, D);
+                    ra[i] = buffer_ld8bf(ro, (uint32_t)(((int64_t)row * p.so.t + 8 * c8) * 2), 0);
+                    rb[i] = buffer_ld8bf(rdo, (uint32_t)(((int64_t)row * p.sdo.t + 8 * c8) * 2), 0);
+                }
                 continue;
             }
             const int rem = f % QTASK;
@@ -214,11 +342,20 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
                 // delta of row `row`: this lane's 8 products, then the sum over
                 // the C8 adjacent lanes of the row (DPP), in a fixed order
                 const int rem = f - 2 * QTASK;
-                float d = 0.f;
+                if constexpr (DWS) {
+                    if (rem % C8 == 0) dl_s[rem / C8] = -r_dl[i];
+                } else {
+                    float d = 0.f;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) d = fmaf((float)ra[i][e], (float)rb[i][e], d);
-                d = group_sum<C8>(d);
-                if (rem % C8 == 0) dl_s[rem / C8] = -d;  // staged negated: the dP accumulator starts at -delta
+                    for (int e = 0; e < 8; ++e) d = fmaf((float)ra[i][e], (float)rb[i][e], d);
+                    d = group_sum<C8>(d);
+                    if (rem % C8 == 0) {
+                        // staged negated: the dP accumulator starts at -delta; a
+                        // short row's (formed by the prologue) comes from sdl_s
+                        const int qi = staged_q0 + rem / C8;
+                        dl_s[rem / C8] = kblk == 0 && bwd_short_row(p, qi) ? sdl_s[qi] : -d;
+                    }
+                }
                 continue;
             }
             const int rem = f % QTASK;
@@ -240,6 +377,31 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
         }
         if (tid < BQ) lse_s[tid] = r_lse * kLseStage;
     };
+
+    // Short rows (bwd_split.h): their delta before the main loop.
+    const int qs_end = kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short rows: [q_begin, qs_end)
+    if (q_begin < qs_end)
+        bwd_short_prologue<D, NW, BK, PR, PSTR, true>(p, bh, Q, K, V, dO, q_begin, qs_end, lds.pr.k, lds.pr.v,
+                                                      lds.pr.q, lds.pr.d, DWS ? nullptr : sdl_s);
+
+    // K^T of the key block (keys contiguous per d row), for dQ.
+#pragma unroll
+    for (int i = 0; i < KLPT; ++i) {
+        const int f = tid + NT * i;
+        if (f >= KTASK) continue;
+        const int kp = f % (BK / 2), c8 = f / (BK / 2);
+        const int r0 = k0 + 2 * kp;
+        const bf16x8 a = r0 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)r0 * p.sk.t + 8 * c8) : bf16x8{};
+        const bf16x8 c = r0 + 1 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)(r0 + 1) * p.sk.t + 8 * c8)
+                                       : bf16x8{};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            bf16x2 pr;
+            pr[0] = a[e];
+            pr[1] = c[e];
+            *reinterpret_cast<bf16x2*>(&KTs[8 * c8 + e][2 * kp]) = pr;
+        }
+    }
 
     gload_q(q_begin, p.Tq);
     sstore_q(0);
@@ -445,14 +607,35 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     constexpr int KLPT = (KTASK + NT - 1) / NT;
     static_assert(2 * QTASK == NT, "one Q / dO staging task per thread");
 
-    __shared__ __attribute__((aligned(16))) __bf16 Qs2[2][BQ][QS];
-    __shared__ __attribute__((aligned(16))) __bf16 dOs2[2][BQ][QS];
-    __shared__ __attribute__((aligned(16))) __bf16 QTs2[2][D][TS];
-    __shared__ __attribute__((aligned(16))) __bf16 dOTs2[2][D][TS];
-    __shared__ __attribute__((aligned(16))) __bf16 dSs2[2][BQ][SS];
-    __shared__ __attribute__((aligned(16))) __bf16 KTs[D][KTS];
-    __shared__ __attribute__((aligned(16))) float lse_s2[2][BQ];
-    __shared__ __attribute__((aligned(16))) float dl_s2[2][BQ];
+    // LDS: the main loop's arrays and, over the same bytes, the short-row
+    // prologue's (K and V of the key block, a batch of short Q / dO rows)
+    constexpr int PSTR = D + 8;  // prologue row stride (bf16)
+    constexpr int PR = 16 * NW;  // prologue rows per batch
+    struct MainLds {
+        __bf16 Qs2[2][BQ][QS];
+        __bf16 dOs2[2][BQ][QS];
+        __bf16 QTs2[2][D][TS];
+        __bf16 dOTs2[2][D][TS];
+        __bf16 dSs2[2][BQ][SS];
+        __bf16 KTs[D][KTS];
+        float lse_s2[2][BQ];
+        float dl_s2[2][BQ];
+    };
+    struct ProLds {
+        __bf16 k[BK][PSTR], v[BK][PSTR], q[PR][PSTR], d[PR][PSTR];
+    };
+    __shared__ __attribute__((aligned(16))) union {
+        MainLds m;
+        ProLds pr;
+    } lds;
+    auto& Qs2 = lds.m.Qs2;
+    auto& dOs2 = lds.m.dOs2;
+    auto& QTs2 = lds.m.QTs2;
+    auto& dOTs2 = lds.m.dOTs2;
+    auto& dSs2 = lds.m.dSs2;
+    auto& KTs = lds.m.KTs;
+    auto& lse_s2 = lds.m.lse_s2;
+    auto& dl_s2 = lds.m.dl_s2;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -488,25 +671,6 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
             vf[kk] = *reinterpret_cast<const bf16x8*>(V + (int64_t)key * p.sv.t + 32 * kk + 8 * g4);
         } else {
             kf[kk] = vf[kk] = bf16x8{};
-        }
-    }
-
-    // K^T of the key block (keys contiguous per d row), for dQ.
-#pragma unroll
-    for (int i = 0; i < KLPT; ++i) {
-        const int f = tid + NT * i;
-        if (f >= KTASK) continue;
-        const int kp = f % (BK / 2), c8 = f / (BK / 2);
-        const int r0 = k0 + 2 * kp;
-        const bf16x8 a = r0 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)r0 * p.sk.t + 8 * c8) : bf16x8{};
-        const bf16x8 c = r0 + 1 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)(r0 + 1) * p.sk.t + 8 * c8)
-                                       : bf16x8{};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            bf16x2 pr;
-            pr[0] = a[e];
-            pr[1] = c[e];
-            *reinterpret_cast<bf16x2*>(&KTs[8 * c8 + e][2 * kp]) = pr;
         }
     }
 
@@ -558,6 +722,31 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
             dl_s2[sb][tid] = r_dl;
         }
     };
+
+    // Short rows (bwd_split.h): their delta before the main loop.
+    const int qs_end = kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short rows: [q_begin, qs_end)
+    if (q_begin < qs_end)
+        bwd_short_prologue<D, NW, BK, PR, PSTR, false>(p, bh, Q, K, V, dO, q_begin, qs_end, lds.pr.k, lds.pr.v,
+                                                       lds.pr.q, lds.pr.d, nullptr);
+
+    // K^T of the key block (keys contiguous per d row), for dQ.
+#pragma unroll
+    for (int i = 0; i < KLPT; ++i) {
+        const int f = tid + NT * i;
+        if (f >= KTASK) continue;
+        const int kp = f % (BK / 2), c8 = f / (BK / 2);
+        const int r0 = k0 + 2 * kp;
+        const bf16x8 a = r0 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)r0 * p.sk.t + 8 * c8) : bf16x8{};
+        const bf16x8 c = r0 + 1 < p.Tk ? *reinterpret_cast<const bf16x8*>(K + (int64_t)(r0 + 1) * p.sk.t + 8 * c8)
+                                       : bf16x8{};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            bf16x2 pr;
+            pr[0] = a[e];
+            pr[1] = c[e];
+            *reinterpret_cast<bf16x2*>(&KTs[8 * c8 + e][2 * kp]) = pr;
+        }
+    }
 
     gload_q(q_begin, p.Tq);
     sstore_q(0);
@@ -921,18 +1110,26 @@ int launch_bwd_dq_bf16(const BwdParams& p, hipStream_t s) {
 
 int bwd_main_bf16_occupancy(int D, int* blocks_per_cu) {
     switch (D) {
-        case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<32>, 64 * bwd_bf16_waves(32), 0);
-        case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<64>, 64 * bwd_bf16_waves(64), 0);
+        case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<32, false>, 64 * bwd_bf16_waves(32), 0);
+        case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<64, false>, 64 * bwd_bf16_waves(64), 0);
         case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_w16_kernel<128>, 512, 0);
         default: return (int)hipErrorInvalidValue;
     }
 }
 
 int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s) {
+    // every row short (Tk within the key block): delta from the workspace for all
+    const bool dws = p.n_short >= p.Tq;
     const dim3 grid((unsigned)(p.n_groups ? p.n_groups * bwd_padded_heads(p.B * p.H) : p.n_kblocks * p.B * p.H));
     switch (p.D) {
-        case 32: hipLaunchKernelGGL((bwd_main_bf16_kernel<32>), grid, dim3(64 * bwd_bf16_waves(32)), 0, s, p); break;
-        case 64: hipLaunchKernelGGL((bwd_main_bf16_kernel<64>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p); break;
+        case 32:
+            if (dws) hipLaunchKernelGGL((bwd_main_bf16_kernel<32, true>), grid, dim3(64 * bwd_bf16_waves(32)), 0, s, p);
+            else hipLaunchKernelGGL((bwd_main_bf16_kernel<32, false>), grid, dim3(64 * bwd_bf16_waves(32)), 0, s, p);
+            break;
+        case 64:
+            if (dws) hipLaunchKernelGGL((bwd_main_bf16_kernel<64, true>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p);
+            else hipLaunchKernelGGL((bwd_main_bf16_kernel<64, false>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p);
+            break;
         case 128: hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128>), grid, dim3(512), 0, s, p); break;
         default: return (int)hipErrorInvalidValue;
     }

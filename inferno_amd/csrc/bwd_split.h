@@ -69,6 +69,66 @@ __device__ __forceinline__ BwdWork bwd_work(const BwdParams& p) {
     return r;
 }
 
+// ---- rows whose visible keys all lie in key block 0 ----------------------------
+//
+// SoftmaxBackward forms dS_ij = P_ij (dP_ij - sum_k P_ik dP_ik) from its own
+// P and dP (softmaxbackward.h:109-128 in the reference): with one visible key
+// P = 1 and dS = 0 exactly, and with few keys or a near one-hot softmax dS is
+// a small difference.  The fused kernels take delta = rowsum(dO * O) instead,
+// which is the same sum in exact arithmetic but rounds differently (and, for
+// bf16, reads O rounded to bf16), so on such rows dQ and dK would carry that
+// rounding at the scale of |dO . O|.  Query rows [0, n_short) see only keys of
+// key block 0 (causal: i + off < keys per workgroup; non-causal: Tk within one
+// block), so a block-0 workgroup holds all of their scores.  Before its main
+// loop it forms their delta itself: S and dP with the MFMA shape of its main
+// loop, e = exp2(S c - lse log2 e) as the main loop forms P, and delta =
+// sum_j e_j dP_j / sum_j e_j, the softmax of the row normalised over its own
+// keys as the reference's e / sum is.  (The main loop's P sums to 1 only
+// within the log-sum-exp's rounding, ~1e-6 at sharp scores; a near one-hot
+// row's dP_max - delta is of the size 1 - P_max, so delta from the
+// unnormalised P would carry that rounding magnified by 1 / (1 - P_max).)
+// The sums are taken in fp64 and delta is stored as hi + lo, two fp32 values:
+// one fp32 delta would round dP - delta at 2^-24 |dP| (1e-4 relative at P_max
+// = 1 - 1e-3), while dP - hi is exact (the two are within a factor of two) and
+// the fp32 kernels' - lo keeps the result to the rounding of dS itself.  A row
+// whose only visible key is key 0 weighs it 1, so its delta equals its dP bit
+// for bit and dS = P (dP - delta) = 0 exactly, as in the reference.  The
+// delta goes to the workspace, where the main loop (and the query-major dQ
+// pass) read it; the prologue runs before the accumulators and the main
+// loop's prefetch are live, so it leaves the main loop's registers alone.
+
+// Whether query row i is one whose delta the block-0 workgroup forms, and
+// whether its only visible key is key 0.
+__device__ __forceinline__ bool bwd_short_row(const BwdParams& p, int i) { return i < p.n_short; }
+__device__ __forceinline__ bool bwd_one_key_row(const BwdParams& p, int i) {
+    return p.causal ? i + p.off == 0 : p.Tk == 1;
+}
+
+// The weight of key j in short row i's delta: e = exp2(S c - lse log2 e) when
+// visible (vis), 1 for the one key of a one-key row, else 0.
+__device__ __forceinline__ float bwd_short_weight(const BwdParams& p, int i, bool vis, float e) {
+    return vis ? (bwd_one_key_row(p, i) ? 1.f : e) : 0.f;
+}
+
+// Short row i's delta from NW per-wave pairs (sum e, sum e dP) in fp64,
+// spaced 2 * STRIDE doubles apart (wave order): delta = sum(e dP) / sum(e)
+// stored as hi (the fp32 nearest) + lo (the rest, rounded).  Rows outside the
+// short ones store nothing.
+template <int NW, int STRIDE>
+__device__ __forceinline__ void bwd_short_delta_store(const BwdParams& p, int bh, int i, const double* sums) {
+    if (!bwd_short_row(p, i)) return;
+    double l = 0.0, w = 0.0;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+        l += sums[2 * STRIDE * v];
+        w += sums[2 * STRIDE * v + 1];
+    }
+    const double dl = w / l;
+    const float hi = (float)dl;
+    p.delta[(int64_t)bh * p.Tq + i] = hi;
+    p.delta_lo[(int64_t)bh * p.Tq + i] = (float)(dl - (double)hi);
+}
+
 // For a split key block: store this workgroup's dK^T and dV^T accumulators
 // (N f32x16 per lane each, NT threads) as its partial, count the arrival, and,
 // in the last workgroup to arrive, replace the accumulators by the

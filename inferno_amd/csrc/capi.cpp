@@ -134,7 +134,7 @@ namespace {
 // INF_OK, or INF_ERR_HIP when an earlier call left a HIP error pending.
 int bwd_workspace_bytes(int det, int B, int H, int Tq, int Tk, int D, inf_dtype dt, size_t* out) {
     const size_t bh = (size_t)B * H;
-    size_t n = round_up(bh * Tq * sizeof(float));  // delta
+    size_t n = 2 * round_up(bh * Tq * sizeof(float));  // delta and its low part (short rows)
     if (dt == INF_BF16 && !dq_from_pass(det, B, H, Tq, Tk, D, dt))
         n += round_up(bh * Tq * (size_t)D * sizeof(float));  // dQ accumulator
     inf::BwdPlan plan;                                        // causal split plan
@@ -238,8 +238,9 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     const size_t bh = (size_t)B * H;
     char* ws = static_cast<char*>(workspace);
     p.delta = reinterpret_cast<float*>(ws);
+    p.delta_lo = reinterpret_cast<float*>(ws + round_up(bh * Tq * sizeof(float)));
     if (dt == INF_BF16) {
-        p.dq_acc = reinterpret_cast<float*>(ws + round_up(bh * Tq * sizeof(float)));
+        p.dq_acc = reinterpret_cast<float*>(ws + 2 * round_up(bh * Tq * sizeof(float)));
         p.sacc = inf::View4{(int64_t)H * Tq * D, (int64_t)Tq * D, (int64_t)D};
     } else {
         p.dq_acc = static_cast<float*>(dq);
@@ -252,13 +253,14 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     p.c = scale * 1.4426950408889634f;
     const int bk = inf::bwd_keys_per_wg(dt == INF_BF16, D);
     p.n_kblocks = (Tk + bk - 1) / bk;
+    p.n_short = inf::bwd_short_rows(Tq, Tk, p.causal, bk);
     p.dq_direct = dq_from_pass(det, B, H, Tq, Tk, D, dt) ? 1 : 0;
     p.n_qtiles = (Tq + inf::kBwdDqBM - 1) / inf::kBwdDqBM;
     if (p.dq_direct) p.dq_acc = nullptr;  // dq is written by the dQ pass
     inf::BwdPlan plan;
     if (inf::bwd_plan(B, H, Tq, Tk, D, p.causal, dt == INF_BF16, &plan)) return INF_ERR_HIP;
     if (plan.n_groups) {
-        size_t offset = round_up(bh * Tq * sizeof(float));
+        size_t offset = 2 * round_up(bh * Tq * sizeof(float));
         if (dt == INF_BF16 && !p.dq_direct) offset += round_up(bh * Tq * (size_t)D * sizeof(float));
         const size_t part_bytes = (size_t)plan.n_slots * bh * 2 * (size_t)D * plan.bk * sizeof(float);
         p.part = reinterpret_cast<float*>(ws + offset);

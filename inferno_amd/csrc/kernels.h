@@ -86,6 +86,7 @@ struct BwdParams {
     const void* dout;
     const float* lse;     // dense [B,H,Tq]
     float* delta;         // workspace, dense [B,H,Tq]: rowsum(dO * O) (unused where the main kernel forms it)
+    float* delta_lo;      // workspace, dense [B,H,Tq]: the short rows' delta is delta + delta_lo (bwd_split.h)
     float* dq_acc;        // fp32 dQ accumulation (dq itself for fp32)
     View4 sacc;           // strides of dq_acc
     void* dq;
@@ -99,6 +100,7 @@ struct BwdParams {
     int dq_direct;          // bf16: dQ from the query-major pass (no accumulator, no atomics)
     int pre_delta;          // bwd_pre computes delta (set by the launcher: off where no kernel reads it)
     int n_qtiles;           // query tiles of kBwdDqBM rows (dQ pass)
+    int n_short;            // rows [0, n_short) see only keys of key block 0 (bwd_short_rows)
     // split plan (n_groups == 0: workgroup w takes key block w / (B*H), all its tiles)
     int n_groups, n_split;
     float* part;            // n_slots * B*H * 2*D*(keys per workgroup) floats (lane-major accumulators)
@@ -316,6 +318,14 @@ constexpr int bwd_waves(int bf16, int D) { return bf16 && D == 64 ? 8 : 4; }
 constexpr int bwd_bf16_waves(int D) { return bwd_waves(1, D); }
 inline int bwd_keys_per_wg(int bf16, int D) { return bf16 && D == 128 ? 128 : 32 * bwd_waves(bf16, D); }
 constexpr int kBwdBQ = 32;       // query rows per backward inner step
+// Leading query rows whose visible keys all lie in key block 0 (keys_per_wg
+// keys): their softmax-backward row dot is formed inside the block-0
+// workgroup from its own P and dP (bwd_split.h).
+inline int bwd_short_rows(int Tq, int Tk, int causal, int keys_per_wg) {
+    if (!causal) return Tk <= keys_per_wg ? Tq : 0;
+    const int64_t r = (int64_t)keys_per_wg - ((int64_t)Tk - Tq);
+    return (int)(r < 0 ? 0 : (r > Tq ? Tq : r));
+}
 constexpr int kBwdDqBM = 128;    // query rows per workgroup of the query-major dQ pass
 int launch_bwd_dq_bf16(const BwdParams& p, hipStream_t s);
 // bf16 at D = 128: dQ from a query-major pass instead of fp32 atomics when a

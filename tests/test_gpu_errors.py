@@ -48,7 +48,9 @@ def test_workspace_query_reports_pending_error(ia, op):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_attention_calls_report_pending_error(ia, dtype):
-    """inf_attn_fwd / inf_attn_bwd with a caller workspace (no sizing call before them)."""
+    """inf_attn_fwd / inf_attn_bwd with every output and the workspace allocated beforehand, so
+    that the pending error is left right before the C-ABI call (torch's own calls would report
+    it first)."""
     print(f"[case] pending error attention {dtype}", flush=True)
     B, H, T, D = 1, 2, 256, 64
     dt = ia.INF_BF16 if dtype == torch.bfloat16 else ia.INF_F32
@@ -58,16 +60,18 @@ def test_attention_calls_report_pending_error(ia, dtype):
     bws = torch.empty(max(ia.workspace_bytes(ia.OP_ATTN_BWD, B, H, T, T, D, dt), 256),
                       dtype=torch.uint8, device="cuda")
     o, lse = ia.attn_fwd(q, k, v, workspace=fws)
+    o2, lse2 = torch.empty_like(o), torch.empty_like(lse)
+    grads = [torch.empty_like(x) for x in (q, k, v)]
     torch.cuda.synchronize()
     leave_pending_error()
     with pytest.raises(ia.InfernoError) as ex:
-        ia.attn_fwd(q, k, v, workspace=fws)
+        ia.attn_fwd(q, k, v, out=o2, lse=lse2, workspace=fws)
     assert ex.value.status == INF_ERR_HIP
-    o2, lse2 = ia.attn_fwd(q, k, v, workspace=fws)
+    ia.attn_fwd(q, k, v, out=o2, lse=lse2, workspace=fws)
     leave_pending_error()
     with pytest.raises(ia.InfernoError) as ex:
-        ia.attn_bwd(q, k, v, o, do, lse, workspace=bws)
+        ia.attn_bwd(q, k, v, o, do, lse, dq=grads[0], dk=grads[1], dv=grads[2], workspace=bws)
     assert ex.value.status == INF_ERR_HIP
-    ia.attn_bwd(q, k, v, o, do, lse, workspace=bws)
+    ia.attn_bwd(q, k, v, o, do, lse, dq=grads[0], dk=grads[1], dv=grads[2], workspace=bws)
     torch.cuda.synchronize()
     assert torch.equal(o, o2) and torch.equal(lse, lse2)

@@ -173,7 +173,7 @@ def test_bwd_split_plan(ia, dtype, B, H, Tq, Tk, D):
 
 def _random_cases(n=24, seed=2024):
     """Seeded draws over the shape space: B, H, ragged Tq <= Tk (causal, end-aligned) or any
-    Tq, Tk (non-causal), D in {32, 64, 128}; fp32 and bf16 alternate."""
+    Tq, Tk (non-causal), D in {32, 64, 128}; fp32 and bf16 alternate; N(0, 1) inputs."""
     rng = np.random.default_rng(seed)
     cases = []
     for i in range(n):
@@ -182,18 +182,33 @@ def _random_cases(n=24, seed=2024):
         B, H = int(rng.integers(1, 3)), int(rng.integers(1, 4))
         Tq = int(rng.integers(1, 500))
         Tk = Tq + int(rng.integers(0, 300)) if causal else int(rng.integers(1, 600))
-        cases.append(("bf16" if i % 2 else "f32", causal, B, H, Tq, Tk, D))
+        cases.append(("bf16" if i % 2 else "f32", causal, B, H, Tq, Tk, D, 1.0))
     return cases
 
 
-@pytest.mark.parametrize("dt,causal,B,H,Tq,Tk,D", _random_cases())
-def test_random_shapes(ia, dt, causal, B, H, Tq, Tk, D):
+def _short_row_cases(n=16, seed=77):
+    """Seeded draws where dS cancels: one or two query rows (Tq in {1, 2}) against at most 66
+    keys, with sharp scores (Q, K ~ N(0, 3^2)): few visible keys or a near one-hot softmax."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        causal = bool(rng.integers(0, 3))  # two in three causal
+        D = int(rng.choice([32, 64, 128]))
+        B, H = int(rng.integers(1, 3)), int(rng.integers(1, 5))
+        Tq = int(rng.integers(1, 3))
+        Tk = int(rng.integers(Tq, 67)) if causal else int(rng.integers(1, 67))
+        cases.append(("bf16" if i % 2 else "f32", causal, B, H, Tq, Tk, D, 3.0))
+    return cases
+
+
+@pytest.mark.parametrize("dt,causal,B,H,Tq,Tk,D,sigma", _random_cases() + _short_row_cases())
+def test_random_shapes(ia, dt, causal, B, H, Tq, Tk, D, sigma):
     """Forward and backward at seeded random shapes against the oracle (O, dQ, dK, dV within
     the dtype's bar of max|ref|, floored at 1e-2; LSE within 1e-4 / 1e-3)."""
-    print(f"[case] random {dt} causal={causal} B{B} H{H} Tq{Tq} Tk{Tk} D{D}", flush=True)
+    print(f"[case] random {dt} causal={causal} B{B} H{H} Tq{Tq} Tk{Tk} D{D} sigma{sigma}", flush=True)
     bf = dt == "bf16"
     dtype = torch.bfloat16 if bf else torch.float32
-    q, k, v, do = oracle.attn_inputs(B, H, Tq, D, seed=500 + Tq + 7 * Tk + D, Tk=Tk)
+    q, k, v, do = oracle.attn_inputs(B, H, Tq, D, seed=500 + Tq + 7 * Tk + D, qk_sigma=sigma, Tk=Tk)
     if bf:
         q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
     o_r, lse_r = oracle.attn_fwd(q, k, v, causal=causal)
@@ -209,24 +224,54 @@ def test_random_shapes(ia, dt, causal, B, H, Tq, Tk, D):
         assert e <= tol, f"{name} rel err {e:.3e}"
 
 
+def attn_bwd_f64(q, k, v, do, causal=True):
+    """dQ, dK, dV of the same inputs evaluated in float64 (softmax normalised over the visible
+    keys, delta = sum_j P_j dP_j): the exact values the fp32 evaluations approximate."""
+    q, k, v, do = (np.asarray(x, np.float64) for x in (q, k, v, do))
+    Tq, Tk, D = q.shape[2], k.shape[2], q.shape[3]
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    s = np.matmul(q, np.swapaxes(k, -1, -2)) * scale
+    if causal:
+        s = np.where(np.arange(Tk)[None, :] <= np.arange(Tq)[:, None] + (Tk - Tq), s, -np.inf)
+    pr = np.exp(s - s.max(-1, keepdims=True))
+    pr /= pr.sum(-1, keepdims=True)
+    dp = np.matmul(do, np.swapaxes(v, -1, -2))
+    ds = pr * (dp - (pr * dp).sum(-1, keepdims=True))
+    return (np.matmul(ds, k) * scale, np.matmul(np.swapaxes(ds, -1, -2), q) * scale,
+            np.matmul(np.swapaxes(pr, -1, -2), do))
+
+
+@pytest.mark.parametrize("mode", ["default", "deterministic"])
 @pytest.mark.parametrize("dt,causal,B,H,Tq,Tk,D,sigma,seed", [
     ("f32", True, 2, 3, 1, 1, 128, 3.0, 9029), ("f32", True, 3, 3, 1, 1, 128, 1.0, 9379),
     ("f32", True, 2, 5, 1, 1, 128, 1.0, 9194), ("f32", True, 1, 1, 2, 66, 128, 3.0, 9306),
     ("f32", True, 2, 2, 2, 2, 32, 3.0, 9335), ("f32", True, 2, 4, 1, 1, 64, 3.0, 9001),
+    ("f32", False, 1, 3, 5, 1, 64, 1.0, 9002),
     ("bf16", False, 1, 1, 2, 2, 32, 1.0, 9033), ("bf16", True, 1, 1, 1, 2, 128, 1.0, 9152),
+    ("bf16", True, 2, 3, 1, 1, 128, 1.0, 9153), ("bf16", True, 2, 3, 3, 3, 64, 3.0, 9154),
 ])
-def test_cancelling_rows(ia, dt, causal, B, H, Tq, Tk, D, sigma, seed):
+def test_cancelling_rows(ia, mode, dt, causal, B, H, Tq, Tk, D, sigma, seed):
     """Rows whose dS cancels: one or two visible keys, or a near one-hot softmax.  The
-    reference's dS = P (dP - sum_j P_j dP_j) then cancels (exactly to 0 with one key, because it
-    subtracts the value it computed), so dQ and dK are small against dV.  The fused kernels form
-    delta = rowsum(dO * O) in another order than dP, and for bf16 from O rounded to bf16 (2^-9),
-    so dQ, dK there carry that rounding at the scale of |dO . O|.  The bar is the north star's:
-    max-abs error within the dtype's tolerance (1e-4 fp32, 2e-2 bf16) of the backward's output
-    scale (max |dQ|, |dK|, |dV| of the reference).  Measured against dQ's or dK's own maximum
-    (floored at 1e-2) these read up to 3.5e-4 (fp32) and 3.9e-2 (bf16); they are the only shapes
-    outside the usual bars in randomized sweeps of 600 shapes, and the kernels of the start of
-    the round gave the same values bit for bit."""
-    print(f"[case] cancelling rows {dt} causal={causal} B{B} H{H} Tq{Tq} Tk{Tk} D{D} sigma{sigma}", flush=True)
+    reference forms dS = P (dP - sum_j P_j dP_j) from its own P and dP, which cancels exactly to
+    0 with one visible key.  Rows whose visible keys all lie in one backward workgroup's key
+    block take delta = sum_j P_j dP_j from the kernel's own P and dP (one visible key: P = 1).
+
+    Bar: the per-tensor one (max-abs error within 1e-4 / 2e-2 of the tensor's own maximum,
+    floored at 1e-2) for O, dQ, dK, dV against the oracle, and for dQ, dK, dV also against a
+    float64 evaluation of the same inputs.  A near one-hot row's dS is a difference of the size
+    1 - P_max, which fp32 rounding of the row dot perturbs at 1e-4 relative in any evaluation:
+    where the oracle itself lies more than half the bar from the float64 values (one shape
+    here, seed 9306: 6.6e-5), two fp32 evaluations can differ by the bar from rounding alone,
+    and that shape is held to the bar against the float64 values only.
+
+    On the one-key shapes (every row of Tq = Tk = 1, or Tk = 1 non-causal) the reference's dQ
+    and dK are exactly 0, and so are the kernels' where dS is formed as P (dP - delta) from the
+    dP that delta was summed from: dK for fp32 and for bf16 at D = 128 (the bf16 kernel at
+    D <= 64 starts its dP product at -delta, which rounds differently), and dQ as well where the
+    same kernel also forms dQ (the default mode), or where the query-major pass forms dP with the
+    same fp32 MFMA (fp32 deterministic mode)."""
+    print(f"[case] cancelling rows {mode} {dt} causal={causal} B{B} H{H} Tq{Tq} Tk{Tk} D{D} sigma{sigma}",
+          flush=True)
     bf = dt == "bf16"
     tol = TOL_BF16 if bf else TOL_F32
     q, k, v, do = oracle.attn_inputs(B, H, Tq, D, seed=seed, qk_sigma=sigma, Tk=Tk)
@@ -234,14 +279,75 @@ def test_cancelling_rows(ia, dt, causal, B, H, Tq, Tk, D, sigma, seed):
         q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
     o_r, lse_r = oracle.attn_fwd(q, k, v, causal=causal)
     dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do, causal=causal)
-    o, lse, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do, causal=causal, dtype=torch.bfloat16 if bf else torch.float32)
+    exact = attn_bwd_f64(q, k, v, do, causal=causal)
+    ia.set_deterministic(mode == "deterministic")
+    try:
+        o, lse, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do, causal=causal,
+                                         dtype=torch.bfloat16 if bf else torch.float32)
+    finally:
+        ia.set_deterministic(False)
     assert oracle.rel_err(lse, lse_r) <= (1e-3 if bf else TOL_F32)
-    assert oracle.rel_err(o, o_r, floor=1e-2) <= tol
-    assert oracle.rel_err(dv, dv_r, floor=1e-2) <= tol
-    scale = max(np.abs(dq_r).max(), np.abs(dk_r).max(), np.abs(dv_r).max())
-    for name, x, r in (("dQ", dq, dq_r), ("dK", dk, dk_r)):
-        err = float(np.abs(np.asarray(x, np.float64) - r).max())
-        assert err <= tol * scale, f"{name} max-abs err {err:.3e} > {tol} x {scale:.3e}"
+    e = oracle.rel_err(o, o_r, floor=1e-2)
+    assert e <= tol, f"O rel err {e:.3e}"
+    for name, x, r, xx in (("dQ", dq, dq_r, exact[0]), ("dK", dk, dk_r, exact[1]), ("dV", dv, dv_r, exact[2])):
+        e_x = oracle.rel_err(x, xx, floor=1e-2)
+        assert e_x <= tol, f"{name} rel err {e_x:.3e} against float64"
+        dev = oracle.rel_err(r, xx, floor=1e-2)  # the oracle's own rounding
+        e = oracle.rel_err(x, r, floor=1e-2)
+        print(f"  {name}: {e:.2e} against the oracle, {e_x:.2e} against float64 (oracle {dev:.2e})", flush=True)
+        if dev <= tol / 2:
+            assert e <= tol, f"{name} rel err {e:.3e}"
+    if (causal and Tq == Tk == 1) or (not causal and Tk == 1):
+        assert not dq_r.any() and not dk_r.any()  # the reference: exactly 0
+        exact_dk = not bf or D == 128
+        if exact_dk:
+            assert not dk.any(), f"dK of one-key rows not exactly 0 (max {np.abs(dk).max():.3e})"
+        if exact_dk and not (bf and mode == "deterministic"):
+            assert not dq.any(), f"dQ of one-key rows not exactly 0 (max {np.abs(dq).max():.3e})"
+
+
+def _sweep_cases(n=60, seed=1234):
+    """Seeded shapes from the distribution of the randomized assurance sweep: fp32 / bf16,
+    D in {32, 64, 128}, causal (end-aligned Tk >= Tq) in four of five, tile-edge lengths,
+    sigma 3 in one of five; sized so the CPU oracle takes well under a second per case."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        i = len(cases)
+        dt = "bf16" if rng.random() < 0.5 else "f32"
+        D = int(rng.choice([32, 64, 128]))
+        B, H = int(rng.choice([1, 1, 2, 3])), int(rng.choice([1, 2, 3, 5]))
+        causal = bool(rng.random() < 0.8)
+        Tq = int(rng.choice([1, 2, 31, 33, 64, 65, 97, 128, 200, 257, 333, 511]))
+        Tk = Tq if rng.random() < 0.6 else Tq + int(rng.choice([0, 1, 17, 64, 100]))
+        sigma = 3.0 if rng.random() < 0.2 else 1.0
+        if B * H * Tq * Tk * D > 40_000_000:
+            continue
+        cases.append((dt, causal, B, H, Tq, Tk, D, sigma, 9000 + i))
+    return cases
+
+
+def test_sweep_per_tensor_bar(ia):
+    """The randomized sweep that found rows outside the bar, committed as a bounded, seeded run:
+    60 shapes, every field (O, LSE, dQ, dK, dV) at the per-tensor bar, stopping at the first
+    shape that misses it (named in the message)."""
+    for dt, causal, B, H, Tq, Tk, D, sigma, seed in _sweep_cases():
+        case = f"{dt} causal={causal} B{B} H{H} Tq{Tq} Tk{Tk} D{D} sigma{sigma} seed{seed}"
+        print(f"[case] sweep {case}", flush=True)
+        bf = dt == "bf16"
+        q, k, v, do = oracle.attn_inputs(B, H, Tq, D, seed=seed, qk_sigma=sigma, Tk=Tk)
+        if bf:
+            q, k, v, do = (bf16_round(x) for x in (q, k, v, do))
+        o_r, lse_r = oracle.attn_fwd(q, k, v, causal=causal)
+        dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do, causal=causal)
+        o, lse, dq, dk, dv = run_fwd_bwd(ia, q, k, v, do, causal=causal,
+                                         dtype=torch.bfloat16 if bf else torch.float32)
+        tol = TOL_BF16 if bf else TOL_F32
+        e = oracle.rel_err(lse, lse_r)
+        assert e <= (1e-3 if bf else TOL_F32), f"{case}: LSE rel err {e:.3e}"
+        for name, x, r in (("O", o, o_r), ("dQ", dq, dq_r), ("dK", dk, dk_r), ("dV", dv, dv_r)):
+            e = oracle.rel_err(x, r, floor=1e-2)
+            assert e <= tol, f"{case}: {name} rel err {e:.3e}"
 
 
 def test_noncausal_f32(ia):
