@@ -113,7 +113,7 @@ def test_round_trip_and_errors(tmp_path):
     b[0:8] = b"INFERNX\0"
     bad.write_bytes(bytes(b))
     r = run("ckpt-load", bad, "cpu")
-    assert r.returncode != 0 and "bad magic" in r.stderr
+    assert r.returncode != 0 and "not an Inferno checkpoint" in r.stderr
     # a checkpoint missing one of the module's tensors is refused (strict load)
     part = tmp_path / "part.ckpt"
     write_file(part, {n: (c, s, np.zeros(int(np.prod(s)))) for n, (c, s) in NET.items() if n != "fc.bias"})
@@ -133,3 +133,61 @@ def test_round_trip_through_hip(tmp_path):
         got = parse_printed(r2.stdout)
         for n in NET:
             assert np.array_equal(saved[n][1], got[n][1]), (dev, n)
+
+
+def test_save_replaces_the_file_whole(tmp_path):
+    """save() writes a sibling temporary file and renames it over the target: an existing file
+    is replaced, and no temporary file is left behind."""
+    f = tmp_path / "net.ckpt"
+    f.write_bytes(b"an older file")
+    r = run("ckpt-save", f, "cpu")
+    assert r.returncode == 0, r.stderr
+    assert parse_file(f)[0] == b"INFERNO\0"
+    assert sorted(p.name for p in tmp_path.iterdir()) == ["net.ckpt"]
+
+
+def _record_offsets(b):
+    """(offset of each record's header, offset past its data) of a well-formed file."""
+    off, out = 16, []
+    for _ in range(struct.unpack_from("<I", b, 12)[0]):
+        name_len, _, ndim, _, nbytes = struct.unpack_from("<IIIQQ", b, off)
+        end = off + 28 + 8 * ndim + name_len + nbytes
+        out.append((off, end))
+        off = end
+    return out
+
+
+@pytest.mark.parametrize("damage,message", [
+    ("truncate", "data runs past the end of the file"),
+    ("trailing", "bytes follow the last"),
+    ("numel", "elements but its dims hold"),
+    ("nbytes", "data bytes for"),
+    ("dtype", "unknown dtype code 5"),
+    ("version", "format version 3 is not supported"),
+    ("count", "file ends inside record 7 of 8"),
+])
+def test_malformed_files_are_refused(tmp_path, damage, message):
+    """Each field of the layout is checked on load, with the record and byte offset named."""
+    f = tmp_path / "net.ckpt"
+    assert run("ckpt-save", f, "cpu").returncode == 0
+    b = bytearray(f.read_bytes())
+    first = _record_offsets(b)[0][0]
+    if damage == "truncate":
+        b = b[:-1]
+    elif damage == "trailing":
+        b += b"\0\0\0"
+    elif damage == "numel":
+        struct.pack_into("<Q", b, first + 12, struct.unpack_from("<Q", b, first + 12)[0] + 1)
+    elif damage == "nbytes":
+        struct.pack_into("<Q", b, first + 20, struct.unpack_from("<Q", b, first + 20)[0] - 4)
+    elif damage == "dtype":
+        struct.pack_into("<I", b, first + 4, 5)  # DType::Invalid
+    elif damage == "version":
+        struct.pack_into("<I", b, 8, 3)
+    elif damage == "count":
+        struct.pack_into("<I", b, 12, len(NET) + 1)
+    bad = tmp_path / "bad.ckpt"
+    bad.write_bytes(bytes(b))
+    r = run("ckpt-load", bad, "cpu")
+    assert r.returncode != 0 and message in r.stderr, r.stderr
+    assert "at byte" in r.stderr
