@@ -39,10 +39,19 @@ HBM_PEAK_GBS = 8000.0
 # delta from O and dO itself).
 BWD_TRAFFIC = {
     "f32": {"bwd_pre": 50.40e6 + 25.56e6, "bwd_main": 202.27e6 + 201.35e6},
-    "bf16": {"bwd_pre": 0.06e6 + 25.17e6, "bwd_main": 82.15e6 + 107.62e6, "bwd_cvt": 25.22e6 + 12.58e6},
+    "bf16": {"bwd_zero": 0.06e6 + 25.17e6, "bwd_main": 82.15e6 + 107.62e6, "bwd_cvt": 25.22e6 + 12.58e6},
 }
+# where the figures above were measured (they are constants: re-measure after a kernel change)
+BWD_TRAFFIC_SOURCE = "profiles/attn_c2_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE of bench.py at config 2)"
 
 METRIC = "causal attn fwd+bwd TFLOP/s (B8 H12 T1024 D64 fp32) + % of MFMA peak"
+
+# per-config lines that --only runs alone: (B, H, T, D, Q/K sigma, dtype)
+ONLY_CONFIGS = {
+    "c2_bf16": (8, 12, 1024, 64, 1.0, "bf16"),
+    "c4_f32": (1, 16, 8192, 128, 3.0, "f32"),
+    "c4_bf16": (1, 16, 8192, 128, 3.0, "bf16"),
+}
 
 
 def flops_fwd(B, H, T, D):
@@ -185,6 +194,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16 and deterministic, config-3 and config-4 lines")
     ap.add_argument("--gpt-steps", type=int, default=5, help="timed steps of the config-3 GPT line")
+    ap.add_argument("--only", choices=sorted(ONLY_CONFIGS),
+                    help="run only this per-config line, with --steps timed steps (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 512 MiB device copy 5 times (HBM-counter calibration)")
     args = ap.parse_args()
@@ -210,6 +221,12 @@ def main():
 
     import inferno_amd as ia
     import oracle
+
+    if args.only:
+        B, H, T, D, sigma, dtype = ONLY_CONFIGS[args.only]
+        r = bench_attn(ia, oracle, torch, np, torch.device("cuda:0"), B, H, T, D, sigma, dtype, steps=args.steps)
+        print(json.dumps({"configs": {args.only: r}}), flush=True)
+        return
 
     B, H, T, D = 8, 12, 1024, 64
     dt = torch.float32 if args.dtype == "f32" else torch.bfloat16
@@ -305,6 +322,7 @@ def main():
             # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (x2.00 / x1.00 copy-kernel calibration)
             "traffic": round(sum(BWD_TRAFFIC[args.dtype].values()), -5),
             "traffic_by_kernel": BWD_TRAFFIC[args.dtype],
+            "traffic_source": BWD_TRAFFIC_SOURCE,
             "algorithmic_flop_per_launch": F_bwd,
             "avg_launch_ms": round(bwd_ms, 4),
         },
@@ -320,7 +338,7 @@ def main():
         # pass); the counter-measured traffic above is the default mode's
         out["roofline"]["kernel"] = "bwd: bwd_pre + bwd_main (no dQ) + bwd_dq (one inf_attn_bwd call)"
         out["roofline"]["traffic"] = None
-        del out["roofline"]["traffic_by_kernel"]
+        del out["roofline"]["traffic_by_kernel"], out["roofline"]["traffic_source"]
         ia.set_deterministic(False)
     if not args.no_decode:
         out["decode"] = bench_decode(ia, oracle, torch, np, dev)

@@ -598,10 +598,13 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     constexpr int NKC = D / 32;          // 32-wide d chunks: reduction steps of S / dP
     constexpr int NDB = D / 16;          // 16-row d blocks of dK^T / dV^T
     constexpr int C8 = D / 8;
-    constexpr int QS = D + 8;            // row-major Q / dO stride (bf16)
-    constexpr int TS = BQ + 8;           // transposed Q / dO stride (bf16)
-    constexpr int SS = BK + 8;           // dS stride
-    constexpr int KTS = BK + 8;          // K^T stride
+    // Row strides of 288 bytes (an odd multiple of 32): the 16-byte operand
+    // reads, lane (l16, g4) at row l16 and byte 16 g4 of a 64-byte slice, are
+    // then conflict-free on gfx950's LDS (272 bytes, D + 8, measured 1.67x
+    // slower); the 8-byte transpose reads are conflict-free with either.
+    constexpr int QS = D + 16;           // row-major Q / dO stride (bf16)
+    constexpr int SS = BK + 16;          // dS stride
+    constexpr int KTS = BK + 16;         // K^T stride
     constexpr int QTASK = (BQ / 2) * C8; // 256: Q tasks on threads 0..255, dO on 256..511
     constexpr int KTASK = (BK / 2) * C8;
     constexpr int KLPT = (KTASK + NT - 1) / NT;
@@ -614,8 +617,6 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     struct MainLds {
         __bf16 Qs2[2][BQ][QS];
         __bf16 dOs2[2][BQ][QS];
-        __bf16 QTs2[2][D][TS];
-        __bf16 dOTs2[2][D][TS];
         __bf16 dSs2[2][BQ][SS];
         __bf16 KTs[D][KTS];
         float lse_s2[2][BQ];
@@ -630,8 +631,6 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     } lds;
     auto& Qs2 = lds.m.Qs2;
     auto& dOs2 = lds.m.dOs2;
-    auto& QTs2 = lds.m.QTs2;
-    auto& dOTs2 = lds.m.dOTs2;
     auto& dSs2 = lds.m.dSs2;
     auto& KTs = lds.m.KTs;
     auto& lse_s2 = lds.m.lse_s2;
@@ -685,38 +684,31 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     const int q_end = wk.q_end;
     const float c = p.c;
 
-    // Q / dO staging as in bwd_main_bf16_kernel (prefetched one tile ahead,
-    // double-buffered with dS, one barrier per tile); the transposed copies
-    // put query q = 16 h + 4 g + c at 8 g + 4 h + c.
+    // Q / dO staging, row-major only (prefetched one tile ahead, double-
+    // buffered with dS, one barrier per tile): thread (rq, cq) stores 16-byte
+    // chunk cq of rows rq and rq + 16, so a wave's 16 lanes of one row write
+    // 256 consecutive bytes (conflict-free).  The dV^T / dK^T operands read
+    // the same rows transposed (ds_read_b64_tr_b16).
     bf16x8 ra, rb;
     float r_lse = 0.f, r_dl = 0.f;
     const int which = tid / QTASK;          // 0: Q, 1: dO (wave-uniform)
     const int rem = tid % QTASK;
-    const int qp = rem % (BQ / 2), c8q = rem / (BQ / 2);
+    const int cq = rem % C8, rq = rem / C8;
+    static_assert(QTASK == (BQ / 2) * C8 && C8 == 16, "16 chunks x 16 row pairs per tensor");
     auto gload_q = [&](int q0, int lim) {
         const int rows = min(lim - q0, BQ);
         const int64_t st = which ? p.sdo.t : p.sq.t;
         const auto rs = row_rsrc(which ? dO : Q, st, q0, rows, D);
-        const uint32_t voff = (uint32_t)(((int64_t)(2 * qp) * st + 8 * c8q) * 2);
+        const uint32_t voff = (uint32_t)(((int64_t)rq * st + 8 * cq) * 2);
         ra = buffer_ld8bf(rs, voff, 0);
-        rb = buffer_ld8bf(rs, voff, (uint32_t)(st * 2));
+        rb = buffer_ld8bf(rs, voff, (uint32_t)((BQ / 2) * st * 2));
         r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
         r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
     };
     auto sstore_q = [&](int sb) {
         __bf16(*rows)[QS] = which ? dOs2[sb] : Qs2[sb];
-        __bf16(*cols)[TS] = which ? dOTs2[sb] : QTs2[sb];
-        *reinterpret_cast<bf16x8*>(&rows[2 * qp][8 * c8q]) = ra;
-        *reinterpret_cast<bf16x8*>(&rows[2 * qp + 1][8 * c8q]) = rb;
-        const int q = 2 * qp;
-        const int pos = 8 * ((q >> 2) & 3) + 4 * (q >> 4) + (q & 3);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            bf16x2 pr;
-            pr[0] = ra[e];
-            pr[1] = rb[e];
-            *reinterpret_cast<bf16x2*>(&cols[8 * c8q + e][pos]) = pr;
-        }
+        *reinterpret_cast<bf16x8*>(&rows[rq][8 * cq]) = ra;
+        *reinterpret_cast<bf16x8*>(&rows[rq + BQ / 2][8 * cq]) = rb;
         if (tid < BQ) {
             lse_s2[sb][tid] = r_lse * kLog2e;  // LSE in base 2
             dl_s2[sb][tid] = r_dl;
@@ -761,8 +753,6 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
         gload_q(q0 + BQ, q0 + BQ < q_end ? p.Tq : 0);
         __bf16(*Qs)[QS] = Qs2[cb];
         __bf16(*dOs)[QS] = dOs2[cb];
-        __bf16(*QTs)[TS] = QTs2[cb];
-        __bf16(*dOTs)[TS] = dOTs2[cb];
         __bf16(*dSs)[SS] = dSs2[cb];
         const float* lse_s = lse_s2[cb];
         const float* dl_s = dl_s2[cb];
@@ -814,12 +804,21 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
                 p_ds(std::true_type{});
             else
                 p_ds(std::false_type{});
-            // dV^T += dO^T P ; dK^T += Q^T dS over the 32 queries (one MFMA per d block)
+            // dV^T += dO^T P ; dK^T += Q^T dS over the 32 queries (one MFMA per d block).
+            // The B operands' element j is query 16 (j / 4) + 4 g4 + j % 4, so lane
+            // (l16, g4) takes column 16 db + l16 of rows 4 g4 + {0..3} and 16 + 4 g4
+            // + {0..3}: two transpose reads, lane s of the 16 addressing row
+            // 4 g4 + s / 4 at columns 16 db + 4 (s % 4).
             bf16x8 ado[NDB], aq[NDB];
+            const int tr_row = 4 * g4 + (l16 >> 2), tr_col = 4 * (l16 & 3);
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
-                ado[db] = *reinterpret_cast<const bf16x8*>(&dOTs[16 * db + l16][8 * g4]);
-                aq[db] = *reinterpret_cast<const bf16x8*>(&QTs[16 * db + l16][8 * g4]);
+                const bf16x4 dlo = ds_read_tr16(&dOs[tr_row][16 * db + tr_col]);
+                const bf16x4 dhi = ds_read_tr16(&dOs[tr_row + 16][16 * db + tr_col]);
+                const bf16x4 qlo = ds_read_tr16(&Qs[tr_row][16 * db + tr_col]);
+                const bf16x4 qhi = ds_read_tr16(&Qs[tr_row + 16][16 * db + tr_col]);
+                ado[db] = __builtin_shufflevector(dlo, dhi, 0, 1, 2, 3, 4, 5, 6, 7);
+                aq[db] = __builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7);
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

@@ -29,14 +29,6 @@
 
 namespace inf {
 
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-// ds_read_b64_tr_b16 at an LDS address (8-byte aligned).
-__device__ __forceinline__ bf16x4 ds_read_tr16(const __bf16* p) {
-    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                          (__attribute__((address_space(3))) s16x4*)(p)));
-}
 
 template <int D>
 struct FwdBf16Tile {

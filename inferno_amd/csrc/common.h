@@ -22,6 +22,8 @@ namespace inf {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -152,6 +154,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const __bf16* base, i
 }
 __device__ __forceinline__ bf16x8 buffer_ld8bf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+// gfx950's ds_read_b64_tr_b16 at an LDS address (8-byte aligned): in each
+// group of 16 lanes, output lane i, element k is element i % 4 of the 8 bytes
+// that lane 4 k + i / 4 addresses.  With the 16 lanes addressing 4 rows x 4
+// chunks of 4 columns of a row-major bf16 tile (row r0 + s / 4, columns
+// c0 + 4 (s % 4) for lane s), lane i receives column c0 + i of those 4 rows.
+__device__ __forceinline__ bf16x4 ds_read_tr16(const __bf16* p) {
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                          (__attribute__((address_space(3))) s16x4*)(p)));
 }
 // Resource over rows [row0, row0 + rows) of a row-major fp32 matrix with
 // row stride `st` elements and `cols` used columns (rows <= 0: empty).

@@ -447,6 +447,53 @@ def test_bf16_rows_8_byte_aligned(ia, D, T):
     assert oracle.rel_err(host(dq8), host(dq)) <= 1e-2
 
 
+@pytest.mark.parametrize("mode", ["default", "deterministic"])
+@pytest.mark.parametrize("D,T", [(32, 97), (64, 150), (128, 130)])
+def test_bf16_all_rows_8_byte_aligned(ia, mode, D, T):
+    """Every bf16 operand and output of the backward (q, k, v, o, dO, dq, dk, dv) at a 4-element
+    offset in its buffer, so each row starts 8 but not 16 bytes past a 16-byte boundary: the
+    kernels' 16-byte loads of K / V into registers, of K for the K^T staging, and of Q / dO in
+    the query-major dQ pass (the deterministic mode, every D; the bf16 D = 128 main kernel) read
+    such rows.  dK and dV, and in the deterministic mode dQ, are bit-identical to those of the
+    same inputs in 16-byte-aligned buffers; the default mode's dQ (an fp32 atomic sum) is
+    within one bf16 rounding step; all against the oracle."""
+    print(f"[case] bf16 8-byte aligned all operands {mode} D{D} T{T}", flush=True)
+    B, H = 2, 2
+    q, k, v, do = (bf16_round(x) for x in oracle.attn_inputs(B, H, T, D, seed=29))
+    Q, K, V, dO = (dev(x, torch.bfloat16) for x in (q, k, v, do))
+    n = B * H * T * D
+
+    def shifted(t):
+        buf = torch.full((n + 4,), float("nan"), device="cuda", dtype=torch.bfloat16)
+        view = buf[4:].view(B, H, T, D)
+        if t is not None:
+            view.copy_(t)
+        assert view.data_ptr() % 16 == 8
+        return view
+
+    ia.set_deterministic(mode == "deterministic")
+    try:
+        o, lse = ia.attn_fwd(Q, K, V)
+        Q8, K8, V8, O8, dO8 = (shifted(t) for t in (Q, K, V, o, dO))
+        o8, lse8 = ia.attn_fwd(Q8, K8, V8, out=shifted(None))
+        dq8, dk8, dv8 = shifted(None), shifted(None), shifted(None)
+        ia.attn_bwd(Q8, K8, V8, O8, dO8, lse, dq=dq8, dk=dk8, dv=dv8)
+        dq, dk, dv = ia.attn_bwd(Q, K, V, o, dO, lse)
+        torch.cuda.synchronize()
+    finally:
+        ia.set_deterministic(False)
+    assert torch.equal(o8, o) and torch.equal(lse8, lse)
+    assert torch.equal(dk8, dk) and torch.equal(dv8, dv)
+    if mode == "deterministic":
+        assert torch.equal(dq8, dq)
+    else:
+        assert oracle.rel_err(host(dq8), host(dq)) <= 1e-2
+    dq_r, dk_r, dv_r = oracle.attn_bwd(q, k, v, do)
+    for name, x, r in (("dQ", dq8, dq_r), ("dK", dk8, dk_r), ("dV", dv8, dv_r)):
+        e = oracle.rel_err(host(x), r)
+        assert e <= TOL_BF16, f"{name} rel err {e:.3e}"
+
+
 def test_config2_full_size_heads(ia):
     """Config 2 (B8 H12 T1024 D64) at full size on the GPU; three heads checked against the oracle."""
     print("[case] config2 full size", flush=True)
