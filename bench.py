@@ -194,8 +194,11 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16 and deterministic, config-3 and config-4 lines")
     ap.add_argument("--gpt-steps", type=int, default=5, help="timed steps of the config-3 GPT line")
-    ap.add_argument("--only", choices=sorted(ONLY_CONFIGS),
-                    help="run only this per-config line, with --steps timed steps (for profiling)")
+    ap.add_argument("--only", choices=sorted(ONLY_CONFIGS) + ["shape"],
+                    help="run only this per-config line, with --steps timed steps (for profiling); "
+                         "'shape' runs --shape / --dtype / --non-causal instead")
+    ap.add_argument("--shape", default="8,12,1024,64", help="B,H,T,D for --only shape")
+    ap.add_argument("--non-causal", action="store_true", help="--only shape without the causal mask")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 512 MiB device copy 5 times (HBM-counter calibration)")
     args = ap.parse_args()
@@ -223,8 +226,14 @@ def main():
     import oracle
 
     if args.only:
-        B, H, T, D, sigma, dtype = ONLY_CONFIGS[args.only]
-        r = bench_attn(ia, oracle, torch, np, torch.device("cuda:0"), B, H, T, D, sigma, dtype, steps=args.steps)
+        causal = True
+        if args.only == "shape":
+            B, H, T, D = (int(x) for x in args.shape.split(","))
+            sigma, dtype, causal = 1.0, args.dtype, not args.non_causal
+        else:
+            B, H, T, D, sigma, dtype = ONLY_CONFIGS[args.only]
+        r = bench_attn(ia, oracle, torch, np, torch.device("cuda:0"), B, H, T, D, sigma, dtype, steps=args.steps,
+                       causal=causal)
         print(json.dumps({"configs": {args.only: r}}), flush=True)
         return
 
@@ -377,14 +386,14 @@ def warm_up(fn, torch, seconds=0.2):
                 return n
 
 
-def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10, deterministic=False):
+def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10, deterministic=False, causal=True):
     """One attention config: fwd+bwd throughput over `steps` back-to-back steps between two
     synchronizations (as `value`), and the fwd / bwd breakdown from HIP events recorded on the
     launch stream around each call in a second pass (the events add the launch gaps).  With
     `deterministic`, the backward runs in the deterministic-dQ mode (inf_set_deterministic)."""
     previous = ia.set_deterministic(deterministic)
     try:
-        r = _bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps)
+        r = _bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps, causal)
     finally:
         ia.set_deterministic(previous)
     if deterministic:
@@ -392,7 +401,7 @@ def bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps=10
     return r
 
 
-def _bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps):
+def _bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps, causal=True):
     tdt = torch.float32 if dtype == "f32" else torch.bfloat16
     q, k, v, do = oracle.attn_inputs(B, H, T, D, seed=42, qk_sigma=qk_sigma)
     Q, K, V, dO = (torch.from_numpy(x).to(dev, tdt) for x in (q, k, v, do))
@@ -407,8 +416,8 @@ def _bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps):
     stream = torch.cuda.current_stream()
 
     def step():
-        ia.attn_fwd(Q, K, V, out=O, lse=LSE, workspace=fws, stream=stream)
-        ia.attn_bwd(Q, K, V, O, dO, LSE, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
+        ia.attn_fwd(Q, K, V, causal=causal, out=O, lse=LSE, workspace=fws, stream=stream)
+        ia.attn_bwd(Q, K, V, O, dO, LSE, causal=causal, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
 
     warm_up(step, torch)
     torch.cuda.synchronize()
@@ -421,15 +430,15 @@ def _bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps):
     for i in range(steps):
         e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         e[0].record(stream)
-        ia.attn_fwd(Q, K, V, out=O, lse=LSE, workspace=fws, stream=stream)
+        ia.attn_fwd(Q, K, V, causal=causal, out=O, lse=LSE, workspace=fws, stream=stream)
         e[1].record(stream)
-        ia.attn_bwd(Q, K, V, O, dO, LSE, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
+        ia.attn_bwd(Q, K, V, O, dO, LSE, causal=causal, dq=dQ, dk=dK, dv=dV, workspace=ws, stream=stream)
         e[2].record(stream)
         evs.append(e)
     torch.cuda.synchronize()
     fwd_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
     bwd_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
-    F = flops_fwd(B, H, T, D)
+    F = flops_fwd(B, H, T, D) * (1 if causal else 2)
     peak = MFMA_FP32_PEAK_TFLOPS if dtype == "f32" else MFMA_BF16_PEAK_TFLOPS
     tot = 3.5 * F / (step_ms * 1e-3) / 1e12
     # minimal HBM bytes: fwd Q,K,V in and O out (+ fp32 LSE); bwd Q,K,V,O,dO in and dQ,dK,dV out
@@ -444,7 +453,7 @@ def _bench_attn(ia, oracle, torch, np, dev, B, H, T, D, qk_sigma, dtype, steps):
     return {
         "roofs": roofs,
         "shape": f"B{B} H{H} T{T} D{D}", "dtype": dtype if dtype == "f32" else "bf16-in/f32-acc",
-        "qk_sigma": qk_sigma, "ms_per_step": round(step_ms, 4), "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+        "qk_sigma": qk_sigma, "causal": causal, "ms_per_step": round(step_ms, 4), "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
         "fwd_tflops": round(F / (fwd_ms * 1e-3) / 1e12, 2),
         "bwd_tflops": round(2.5 * F / (bwd_ms * 1e-3) / 1e12, 2),
         "fwd_bwd_tflops": round(tot, 2), "peak_tflops": peak, "frac": round(tot / peak, 4),
