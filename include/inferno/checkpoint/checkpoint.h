@@ -27,6 +27,8 @@ struct TensorRecordHeader {
     uint64_t numel;
     uint64_t nbytes;
 };
+// Declared as the reference's header declares it, for callers that name it;
+// the files written and read here carry no training metadata.
 struct TrainingMetadata {
     uint64_t step;
     uint64_t total_steps;
@@ -49,11 +51,7 @@ public:
     static void load_into(Module& m, const StateDict& state, bool strict = true);
 
 private:
-    StateDict m_state_dict;
-    uint32_t m_step = 0;
-    uint32_t m_total_steps = 0;
-    uint32_t m_epoch = 0;
-    uint32_t m_total_epochs = 0;
+    StateDict tensors_;
 };
 
 }  // namespace Inferno

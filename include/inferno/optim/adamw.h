@@ -15,31 +15,21 @@ class OptimizerAdamW {
 public:
     OptimizerAdamW(std::vector<Tensor*> parameters, float lr = 3e-4f, float beta1 = 0.9f, float beta2 = 0.95f,
                    float eps = 1e-8f, float weight_decay = 0.1f)
-        : m_parameters(std::move(parameters)),
-          m_lr(lr),
-          m_beta1(beta1),
-          m_beta2(beta2),
-          m_eps(eps),
-          m_weight_decay(weight_decay),
-          m_step(0) {}
+        : params_(std::move(parameters)), lr_(lr), beta1_(beta1), beta2_(beta2), eps_(eps), decay_(weight_decay) {}
     void step();
     void zero_grad();
-    size_t step_count() const { return m_step; }
+    size_t step_count() const { return steps_; }
 
 private:
-    struct AdamWState {
-        Tensor m;
-        Tensor v;
-        bool initialized = false;
+    // fp32 first and second moments of one parameter, allocated on its first step
+    struct Moments {
+        Tensor first;
+        Tensor second;
     };
-    std::vector<Tensor*> m_parameters;
-    std::unordered_map<Tensor*, AdamWState> m_state;
-    float m_lr;
-    float m_beta1;
-    float m_beta2;
-    float m_eps;
-    float m_weight_decay;
-    size_t m_step;
+    std::vector<Tensor*> params_;
+    std::unordered_map<Tensor*, Moments> moments_;
+    float lr_, beta1_, beta2_, eps_, decay_;
+    size_t steps_ = 0;
 };
 
 }  // namespace Inferno

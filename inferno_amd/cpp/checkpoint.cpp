@@ -118,10 +118,10 @@ void Checkpoint::save(const std::string& path) const {
     Encoder head;
     head.put_bytes(kFileMagic, sizeof(kFileMagic));
     head.put<uint32_t>(kFileVersion);
-    head.put<uint32_t>(static_cast<uint32_t>(m_state_dict.size()));
+    head.put<uint32_t>(static_cast<uint32_t>(tensors_.size()));
     if (!out.write(head.bytes.data(), static_cast<std::streamsize>(head.bytes.size()))) abandon("writing the header failed");
 
-    for (const auto& entry : m_state_dict) {
+    for (const auto& entry : tensors_) {
         const std::string& name = entry.first;
         const Tensor t = host_contiguous(entry.second);
         Encoder rec;
@@ -145,8 +145,8 @@ void Checkpoint::save(const std::string& path) const {
     }
 }
 
-void Checkpoint::set_state_dict(const StateDict& state) { m_state_dict = state; }
-const StateDict& Checkpoint::state_dict() const { return m_state_dict; }
+void Checkpoint::set_state_dict(const StateDict& state) { tensors_ = state; }
+const StateDict& Checkpoint::state_dict() const { return tensors_; }
 
 Checkpoint Checkpoint::load(const std::string& path) {
     std::ifstream in(path, std::ios::binary | std::ios::ate);
@@ -198,11 +198,11 @@ Checkpoint Checkpoint::load(const std::string& path) {
             dec.fail(who + " declares " + std::to_string(nbytes) + " data bytes for " + std::to_string(numel) + " " +
                      dtype_name(dtype) + " elements");
         if (nbytes > dec.remaining()) dec.fail(who + "'s data runs past the end of the file");
-        if (result.m_state_dict.count(name)) dec.fail(who + " repeats a name already read");
+        if (result.tensors_.count(name)) dec.fail(who + " repeats a name already read");
 
         Tensor t(dtype, shape, name, Device::cpu());
         dec.get_bytes(t.data_ptr(), nbytes, who + "'s data");
-        result.m_state_dict.emplace(name, t);
+        result.tensors_.emplace(name, t);
     }
     if (dec.remaining() != 0)
         dec.fail(std::to_string(dec.remaining()) + " bytes follow the last of the " + std::to_string(count) + " records");

@@ -276,45 +276,44 @@ Tensor CrossEntropyLoss::forward(Tensor& logits, Tensor& target) { return cross_
 // -------------------------------------------------------------- OptimizerAdamW
 void OptimizerAdamW::step() {
     NoGradGuard guard;
-    m_step++;
-    const float bc1 = 1.0f - std::pow(m_beta1, static_cast<float>(m_step));
-    const float bc2 = 1.0f - std::pow(m_beta2, static_cast<float>(m_step));
+    steps_++;
+    const float bc1 = 1.0f - std::pow(beta1_, static_cast<float>(steps_));
+    const float bc2 = 1.0f - std::pow(beta2_, static_cast<float>(steps_));
     // HIP parameters are updated together, one multi-tensor call per (device,
     // dtype); `keep` holds the contiguous gradient copies until the calls are
     // enqueued (later reuse of their blocks is stream-ordered after them).
     std::map<std::pair<int, int>, std::vector<inf_adamw_tensor>> groups;
     std::vector<Tensor> keep;
-    for (Tensor* p : m_parameters) {
+    for (Tensor* p : params_) {
         if (p == nullptr || !p->grad()) continue;
         Tensor* grad = p->grad().get();
         if (grad->dtype() != p->dtype() || grad->shape() != p->shape())
             throw Error("OptimizerAdamW: gradient dtype / shape differs from the parameter's");
         if (!p->is_contiguous()) throw Error("OptimizerAdamW: parameters must be contiguous");
         Tensor g = grad->contiguous();
-        AdamWState& st = m_state[p];
-        if (!st.initialized) {
-            st.m = Tensor::zeros(p->shape(), DType::Float32, p->device(), "adamw_m");
-            st.v = Tensor::zeros(p->shape(), DType::Float32, p->device(), "adamw_v");
-            st.initialized = true;
+        Moments& st = moments_[p];
+        if (!st.first.defined()) {
+            st.first = Tensor::zeros(p->shape(), DType::Float32, p->device(), "adamw_m");
+            st.second = Tensor::zeros(p->shape(), DType::Float32, p->device(), "adamw_v");
         }
         const size_t n = p->numel();
         if (p->device().is_cpu()) {
             // cpu_adamw_step_impl (adamw.h:67-111)
             char* pp = static_cast<char*>(p->data_ptr());
             const char* gp = static_cast<const char*>(g.data_ptr());
-            float* mp = static_cast<float*>(st.m.data_ptr());
-            float* vp = static_cast<float*>(st.v.data_ptr());
+            float* mp = static_cast<float*>(st.first.data_ptr());
+            float* vp = static_cast<float*>(st.second.data_ptr());
             const size_t esz = dtype_size(p->dtype());
             for (size_t i = 0; i < n; ++i) {
                 const float gr = (float)detail::load_elem(gp + i * esz, p->dtype());
                 float mi = mp[i], vi = vp[i], pi = (float)detail::load_elem(pp + i * esz, p->dtype());
-                mi = m_beta1 * mi + (1.0f - m_beta1) * gr;
-                vi = m_beta2 * vi + (1.0f - m_beta2) * gr * gr;
+                mi = beta1_ * mi + (1.0f - beta1_) * gr;
+                vi = beta2_ * vi + (1.0f - beta2_) * gr * gr;
                 const float m_hat = mi / bc1;
                 const float v_hat = vi / bc2;
-                float update = m_hat / (std::sqrt(v_hat) + m_eps);
-                if (m_weight_decay != 0.0f) update += m_weight_decay * pi;
-                pi -= m_lr * update;
+                float update = m_hat / (std::sqrt(v_hat) + eps_);
+                if (decay_ != 0.0f) update += decay_ * pi;
+                pi -= lr_ * update;
                 detail::store_elem(pp + i * esz, p->dtype(), pi);
                 mp[i] = mi;
                 vp[i] = vi;
@@ -322,23 +321,23 @@ void OptimizerAdamW::step() {
         } else {
             const int dt = (int)detail::inf_dt(p->dtype(), "OptimizerAdamW");
             groups[{p->device().index, dt}].push_back(inf_adamw_tensor{p->data_ptr(), g.data_ptr(),
-                                                                       static_cast<float*>(st.m.data_ptr()),
-                                                                       static_cast<float*>(st.v.data_ptr()),
+                                                                       static_cast<float*>(st.first.data_ptr()),
+                                                                       static_cast<float*>(st.second.data_ptr()),
                                                                        (int64_t)n});
             keep.push_back(g);
         }
     }
     for (auto& [key, list] : groups) {
         detail::DeviceGuard dg(key.first);
-        detail::status_check(inf_adamw_step_multi(list.data(), (int)list.size(), m_lr, m_beta1, m_beta2, m_eps,
-                                                  m_weight_decay, bc1, bc2, (inf_dtype)key.second,
+        detail::status_check(inf_adamw_step_multi(list.data(), (int)list.size(), lr_, beta1_, beta2_, eps_,
+                                                  decay_, bc1, bc2, (inf_dtype)key.second,
                                                   detail::stream_for(key.first)),
                              "inf_adamw_step_multi");
     }
 }
 
 void OptimizerAdamW::zero_grad() {
-    for (auto& p : m_parameters)
+    for (auto& p : params_)
         if (p != nullptr) p->grad() = nullptr;
 }
 
