@@ -164,6 +164,30 @@ int inf_softmax_bwd(const void* y, const void* dy, void* dx, int64_t rows, int64
                     inf_dtype dt, void* stream);
 
 /*
+ * Softmax along axis `axis` (negative counts from the end) of strided views
+ * of rank 1..8: for every index of the other dims, the line of shape[axis]
+ * elements x_strides[axis] apart.  Replaces cuda_softmax's strided walk
+ * (src/inferno/cuda/cudasoftmax.cu:16-97, 110-172), one thread per line as
+ * there, for an axis that is not the last: no transposed copies.  Strides are
+ * in elements, >= 0; y must not overlap itself (else INF_ERR_BAD_STRIDE).
+ * dt as inf_softmax_fwd (INF_I32: x int32, y fp32).  Many lines (>= 65536)
+ * run one thread per line (an online max / sum pass and a write pass), fewer
+ * run one workgroup per line.
+ */
+int inf_softmax_fwd_axis(const void* x, const int64_t* x_strides, void* y, const int64_t* y_strides, int ndim,
+                         const int64_t* shape, int axis, inf_dtype dt, void* stream);
+
+/*
+ * Softmax backward along a strided axis: dx = y * (dy - sum(dy * y)) per line,
+ * the lines as inf_softmax_fwd_axis's.  Replaces cuda_softmax_backward
+ * (src/inferno/cuda/cudasoftmax.cu:222-373).  y, dy and dx share dt: INF_F32,
+ * INF_BF16 or INF_F64; dx must not overlap itself.
+ */
+int inf_softmax_bwd_axis(const void* y, const int64_t* y_strides, const void* dy, const int64_t* dy_strides,
+                         void* dx, const int64_t* dx_strides, int ndim, const int64_t* shape, int axis,
+                         inf_dtype dt, void* stream);
+
+/*
  * Single-query decode against a KV cache: o[b,h] = softmax(q k^T * scale) v
  * over all Tk cached keys (q, o: [B, H, 1, D]; caches [B, H, Tk, D]).  The
  * reference has no decode path; this equals the last row of a Tk-long causal

@@ -43,6 +43,8 @@ EXPORTS = (
     "inf_attn_bwd",
     "inf_softmax_fwd",
     "inf_softmax_bwd",
+    "inf_softmax_fwd_axis",
+    "inf_softmax_bwd_axis",
     "inf_attn_decode",
     "inf_fill",
     "inf_binary",
@@ -121,6 +123,11 @@ def lib() -> ctypes.CDLL:
         L.inf_softmax_fwd.restype = i32
         L.inf_softmax_bwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp]
         L.inf_softmax_bwd.restype = i32
+        i64p = ctypes.POINTER(ctypes.c_int64)
+        L.inf_softmax_fwd_axis.argtypes = [vp, i64p, vp, i64p, i32, i64p, i32, i32, vp]
+        L.inf_softmax_fwd_axis.restype = i32
+        L.inf_softmax_bwd_axis.argtypes = [vp, i64p, vp, i64p, vp, i64p, i32, i64p, i32, i32, vp]
+        L.inf_softmax_bwd_axis.restype = i32
         L.inf_attn_decode.argtypes = [vp, S, vp, S, vp, S, vp, S, i32, i32, i32, i32, f32, i32, vp,
                                       ctypes.c_size_t, vp]
         L.inf_attn_decode.restype = i32
@@ -213,6 +220,8 @@ from .ops import (  # noqa: E402  (torch-facing helpers need lib())
     attn_decode,
     attn_fwd,
     masked_fill,
+    softmax_axis_bwd,
+    softmax_axis_fwd,
     softmax_bwd,
     softmax_fwd,
     strides_of,
@@ -243,6 +252,8 @@ __all__ = [
     "attn_decode",
     "softmax_fwd",
     "softmax_bwd",
+    "softmax_axis_fwd",
+    "softmax_axis_bwd",
     "strides_of",
     "workspace_bytes",
     "set_deterministic",

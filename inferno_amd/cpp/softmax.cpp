@@ -1,12 +1,14 @@
 // softmax.cpp -- Softmax / SoftmaxBackward (include/inferno/functional/softmax.h).
 //
-// The softmax axis is moved last and made dense (a no-op for the usual
-// last-axis case), so both devices work on rows:
-//   CPU: the reference's three passes (softmax_kernels.h:77-102): max with a
-//        lowest() start, e = (float)exp((double)(x - max)), fp32 running sum,
-//        divide; backward dot = sum g*y in axis order, dx = y*(g - dot)
-//        (softmaxbackward.h:111-128).
-//   HIP: inf_softmax_fwd / inf_softmax_bwd.
+// CPU: the softmax axis is moved last and made dense (a no-op for the usual
+//      last-axis case), and the reference's three passes run per row
+//      (softmax_kernels.h:77-102): max with a lowest() start,
+//      e = (float)exp((double)(x - max)), fp32 running sum, divide; backward
+//      dot = sum g*y in axis order, dx = y*(g - dot) (softmaxbackward.h:111-128).
+// HIP: a dense last axis runs inf_softmax_fwd / inf_softmax_bwd over rows; any
+//      other axis (or layout) runs inf_softmax_fwd_axis / inf_softmax_bwd_axis
+//      on the operands' own strides, as the reference's device path walks them
+//      (cudasoftmax.cu:16-97): no transposed copies.
 // Dtypes follow the reference's dispatch (softmax.cpp:25, dtype_dispatch.h:8-52):
 // Float32 -> Float32, Int32 -> Float32, Float64 -> Float64 (double
 // arithmetic), plus BFloat16 (fp32 arithmetic); the backward works in
@@ -23,6 +25,8 @@ namespace Inferno {
 
 namespace {
 
+constexpr int kMaxSoftmaxRank = 8;  // the axis entry points' rank limit
+
 int norm_axis(int axis, size_t nd) {
     int a = axis < 0 ? axis + (int)nd : axis;
     if (a < 0 || a >= (int)nd) throw Error("Softmax: invalid axis");
@@ -35,6 +39,12 @@ Tensor rows_of(const Tensor& t, int axis) {
     Tensor x = axis == (int)t.ndim() - 1 ? t : t.transpose(axis, (int)t.ndim() - 1);
     return x.is_contiguous() ? x : x.contiguous();
 }
+
+// Whether t's `axis` is its last dim with unit stride and its rows dense
+// (the row kernels' layout).
+bool dense_rows(const Tensor& t, int axis) { return axis == (int)t.ndim() - 1 && t.is_contiguous(); }
+
+std::vector<int64_t> i64(const std::vector<size_t>& v) { return std::vector<int64_t>(v.begin(), v.end()); }
 
 Tensor restore_axis(const Tensor& rows, int axis, size_t nd) {
     NoGradGuard ng;
@@ -114,6 +124,19 @@ inf_dtype sm_dt(DType dt) {
 Tensor Softmax(Tensor& A, int axis) {
     const DType odt = softmax_out_dtype(A.dtype());
     const int ax = norm_axis(axis, A.ndim());
+    if (!A.device().is_cpu() && !dense_rows(A, ax) && (int)A.ndim() <= kMaxSoftmaxRank) {
+        Tensor out(odt, A.shape(), "softmax", A.device(), false);
+        if (A.numel()) {
+            detail::DeviceGuard g(A.device().index);
+            const auto shape = i64(A.shape()), sa = i64(A.strides()), so = i64(out.strides());
+            detail::status_check(inf_softmax_fwd_axis(A.data_ptr(), sa.data(), out.data_ptr(), so.data(), (int)A.ndim(),
+                                                      shape.data(), ax, sm_dt(A.dtype()), detail::stream_of(A)),
+                                 "inf_softmax_fwd_axis");
+        }
+        out.set_requires_grad(true);
+        if (grad_enabled && A.requires_grad()) GetImpl(out)->gradfn() = std::make_shared<SoftmaxBackward>(A, out, ax);
+        return out;
+    }
     Tensor x = rows_of(A, ax);
     const size_t cols = x.shape().back();
     const size_t rows = cols ? x.numel() / cols : 0;
@@ -151,6 +174,26 @@ SoftmaxBackward::SoftmaxBackward(const Tensor& A, const Tensor& out, int axis)
 void SoftmaxBackward::backward() {
     NoGradGuard ng;
     Tensor g = Engine::grad_in(this, 0);
+    if (!m_out.device().is_cpu() && !(dense_rows(m_out, m_axis) && dense_rows(g, m_axis)) &&
+        (int)m_out.ndim() <= kMaxSoftmaxRank) {
+        const DType rdt = softmax_grad_dtype(m_out.dtype(), g.dtype());
+        if (m_out.dtype() != g.dtype())
+            throw Error(std::string("SoftmaxBackward: on HIP the output and its gradient must share a dtype, got ") +
+                        dtype_name(m_out.dtype()) + " and " + dtype_name(g.dtype()));
+        Tensor dx(rdt, m_out.shape(), "softmax_grad", m_out.device(), false);
+        if (dx.numel()) {
+            detail::DeviceGuard dg(m_out.device().index);
+            const auto shape = i64(m_out.shape()), sy = i64(m_out.strides()), sg = i64(g.strides()),
+                       sd = i64(dx.strides());
+            detail::status_check(inf_softmax_bwd_axis(m_out.data_ptr(), sy.data(), g.data_ptr(), sg.data(),
+                                                      dx.data_ptr(), sd.data(), (int)m_out.ndim(), shape.data(), m_axis,
+                                                      sm_dt(m_out.dtype()), detail::stream_of(m_out)),
+                                 "inf_softmax_bwd_axis");
+        }
+        auto e = GetImpl(m_A)->grad_edge();
+        if (e) Engine::accumulate(e.get(), 0, dx);
+        return;
+    }
     Tensor y = rows_of(m_out, m_axis);
     Tensor gr = rows_of(g, m_axis);
     const DType rdt = softmax_grad_dtype(y.dtype(), gr.dtype());

@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdint>
@@ -317,6 +318,71 @@ int inf_softmax_bwd(const void* y, const void* dy, void* dx, int64_t rows, int64
     if (st != INF_OK) return st;
     inf::SoftmaxParams p{y, dy, dx, rows, cols, y_row_stride, dy_row_stride, dx_row_stride};
     return hip_status(inf::launch_softmax_bwd(p, sm_type(dt), vec_ok, (hipStream_t)stream));
+}
+
+// Shape / stride checks of the axis entry points, and the launch parameters
+// (strides of the operands x, g, y; g may be null for the forward).
+static int softmax_axis_common(const void* x, const int64_t* sx, const void* g, const int64_t* sg, void* y,
+                               const int64_t* sy, int ndim, const int64_t* shape, int axis, inf::SoftmaxAxis* p) {
+    if (ndim < 1) return INF_ERR_BAD_SHAPE;
+    if (ndim > inf::kMaxRank) return INF_ERR_UNSUPPORTED;
+    if (!shape || !sx || !sy || (g && !sg)) return INF_ERR_NULL_POINTER;
+    if (axis < 0) axis += ndim;
+    if (axis < 0 || axis >= ndim) return INF_ERR_BAD_SHAPE;
+    *p = inf::SoftmaxAxis{};
+    p->x = x;
+    p->g = g;
+    p->y = y;
+    p->ndim = ndim;
+    p->axis = axis;
+    p->groups = 1;
+    for (int d = 0; d < ndim; ++d) {
+        if (shape[d] < 0) return INF_ERR_BAD_SHAPE;
+        if (sx[d] < 0 || sy[d] < 0 || (g && sg[d] < 0)) return INF_ERR_BAD_STRIDE;
+        p->shape[d] = shape[d];
+        p->sx[d] = sx[d];
+        p->sy[d] = sy[d];
+        p->sg[d] = g ? sg[d] : 0;
+        if (d != axis) p->groups *= shape[d];
+    }
+    p->n = shape[axis];
+    if (p->groups > (1LL << 31) * 256) return INF_ERR_BAD_SHAPE;
+    // the output must not overlap itself: ordering its dims of extent > 1 by
+    // stride, each stride must exceed the largest offset the dims inside reach
+    int order[inf::kMaxRank], m = 0;
+    for (int d = 0; d < ndim; ++d)
+        if (shape[d] > 1) order[m++] = d;
+    std::sort(order, order + m, [&](int a, int b) { return sy[a] < sy[b]; });
+    int64_t reach = 0;
+    for (int i = 0; i < m; ++i) {
+        if (sy[order[i]] <= reach) return INF_ERR_BAD_STRIDE;
+        reach += sy[order[i]] * (shape[order[i]] - 1);
+    }
+    return INF_OK;
+}
+
+int inf_softmax_fwd_axis(const void* x, const int64_t* x_strides, void* y, const int64_t* y_strides, int ndim,
+                         const int64_t* shape, int axis, inf_dtype dt, void* stream) {
+    if (!dtype_ok(dt) && dt != INF_F64 && dt != INF_I32) return INF_ERR_BAD_DTYPE;
+    inf::SoftmaxAxis p;
+    const int st = softmax_axis_common(x, x_strides, nullptr, nullptr, y, y_strides, ndim, shape, axis, &p);
+    if (st != INF_OK) return st;
+    if (p.groups == 0 || p.n == 0) return INF_OK;
+    if (!x || !y) return INF_ERR_NULL_POINTER;
+    return hip_status(inf::launch_softmax_axis_fwd(p, sm_type(dt), (hipStream_t)stream));
+}
+
+int inf_softmax_bwd_axis(const void* y, const int64_t* y_strides, const void* dy, const int64_t* dy_strides,
+                         void* dx, const int64_t* dx_strides, int ndim, const int64_t* shape, int axis,
+                         inf_dtype dt, void* stream) {
+    if (!dtype_ok(dt) && dt != INF_F64) return INF_ERR_BAD_DTYPE;
+    if (!dy_strides) return INF_ERR_NULL_POINTER;
+    inf::SoftmaxAxis p;
+    const int st = softmax_axis_common(y, y_strides, dy ? dy : y, dy_strides, dx, dx_strides, ndim, shape, axis, &p);
+    if (st != INF_OK) return st;
+    if (p.groups == 0 || p.n == 0) return INF_OK;
+    if (!y || !dy || !dx) return INF_ERR_NULL_POINTER;
+    return hip_status(inf::launch_softmax_axis_bwd(p, sm_type(dt), (hipStream_t)stream));
 }
 
 int inf_attn_decode(const void* q, inf_strides sq, const void* kcache, inf_strides sk,

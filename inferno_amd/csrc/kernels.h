@@ -284,6 +284,21 @@ int decode_scratch(float** out);
 enum class SmType { F32, BF16, I32, F64 };
 int launch_softmax_fwd(const SoftmaxParams& p, SmType t, int vec_ok, hipStream_t s);
 int launch_softmax_bwd(const SoftmaxParams& p, SmType t, int vec_ok, hipStream_t s);
+
+// Softmax along one axis of strided views (rank <= kMaxRank), in place of
+// moving the axis last: the other dims index `groups` lines (the last dim
+// fastest), each of `n` elements `s*[axis]` apart.
+struct SoftmaxAxis {
+    const void* x;   // fwd: x; bwd: y
+    const void* g;   // bwd: dy
+    void* y;         // fwd: y; bwd: dx
+    int ndim, axis;
+    int64_t groups, n;
+    int64_t shape[kMaxRank];
+    int64_t sx[kMaxRank], sg[kMaxRank], sy[kMaxRank];  // element strides of x, g, y
+};
+int launch_softmax_axis_fwd(const SoftmaxAxis& p, SmType t, hipStream_t s);
+int launch_softmax_axis_bwd(const SoftmaxAxis& p, SmType t, hipStream_t s);
 int launch_fill(void* dst, int64_t n, int elem_bytes, uint32_t bits, hipStream_t s);
 int launch_binary(int op, const void* a, const void* b, void* out, int64_t n, int a_scalar, int b_scalar,
                   int bf16, hipStream_t s);

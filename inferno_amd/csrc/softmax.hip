@@ -189,6 +189,192 @@ __global__ __launch_bounds__(256) void softmax_bwd_block(SoftmaxParams p) {
     }
 }
 
+// ---- softmax along a strided axis -------------------------------------------
+// Each group (an index of the dims other than the axis) is one line of n
+// elements.  Many groups: one thread per line, consecutive threads on
+// consecutive groups (so the loads coalesce when the last non-axis dim is
+// dense), an online max / sum pass and a write pass.  Few groups: one
+// workgroup per line, its threads striding the line (max, sum, write passes
+// as the row kernels).
+
+// Element offsets of group `grp` in x, g and y.
+__device__ __forceinline__ void axis_bases(const SoftmaxAxis& p, int64_t grp, int64_t& bx, int64_t& bg,
+                                           int64_t& by) {
+    bx = bg = by = 0;
+    for (int d = p.ndim - 1; d >= 0; --d) {
+        if (d == p.axis) continue;
+        const int64_t c = grp % p.shape[d];
+        grp /= p.shape[d];
+        bx += c * p.sx[d];
+        bg += c * p.sg[d];
+        by += c * p.sy[d];
+    }
+}
+
+// Online (max, sum of exp) update with one element; a -inf element against a
+// -inf maximum adds nothing, NaN propagates into the sum.
+template <typename T>
+__device__ __forceinline__ void online_add(T v, T& m, T& s) {
+    if (v > m) {
+        if constexpr (std::is_same<T, double>::value)
+            s = (m == -INFINITY ? 0.0 : s * exp(m - v)) + 1.0;
+        else
+            s = (m == -INFINITY ? 0.f : s * fast_exp2((m - v) * kLog2e)) + 1.f;
+        m = v;
+    } else if (!(v == -INFINITY && m == -INFINITY)) {
+        if constexpr (std::is_same<T, double>::value)
+            s += exp(v - m);
+        else
+            s += fast_exp2((v - m) * kLog2e);
+    }
+}
+
+template <typename EI, typename EO>
+__global__ __launch_bounds__(256) void softmax_axis_fwd_lines(SoftmaxAxis p) {
+    const int64_t grp = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (grp >= p.groups) return;
+    int64_t bx, bg, by;
+    axis_bases(p, grp, bx, bg, by);
+    const EI* x = (const EI*)p.x + bx;
+    EO* y = (EO*)p.y + by;
+    const int64_t ax = p.sx[p.axis], ay = p.sy[p.axis];
+    if constexpr (std::is_same<EI, double>::value) {
+        double m = -INFINITY, s = 0.0;
+        for (int64_t k = 0; k < p.n; ++k) online_add(x[k * ax], m, s);
+        for (int64_t k = 0; k < p.n; ++k) y[k * ay] = exp(x[k * ax] - m) / s;
+    } else {
+        using Ti = ElemOf<EI>;
+        using To = ElemOf<EO>;
+        float m = -INFINITY, s = 0.f;
+        for (int64_t k = 0; k < p.n; ++k) online_add(Ti::ld(x + k * ax), m, s);
+        const float mc = m * kLog2e;
+        for (int64_t k = 0; k < p.n; ++k) To::st(y + k * ay, fast_exp2(fmaf(Ti::ld(x + k * ax), kLog2e, -mc)) / s);
+    }
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void softmax_axis_bwd_lines(SoftmaxAxis p) {
+    const int64_t grp = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (grp >= p.groups) return;
+    int64_t by, bg, bd;
+    axis_bases(p, grp, by, bg, bd);
+    const E* yy = (const E*)p.x + by;
+    const E* gg = (const E*)p.g + bg;
+    E* dx = (E*)p.y + bd;
+    const int64_t ay = p.sx[p.axis], ag = p.sg[p.axis], ad = p.sy[p.axis];
+    if constexpr (std::is_same<E, double>::value) {
+        double dot = 0.0;
+        for (int64_t k = 0; k < p.n; ++k) dot += gg[k * ag] * yy[k * ay];
+        for (int64_t k = 0; k < p.n; ++k) dx[k * ad] = yy[k * ay] * (gg[k * ag] - dot);
+    } else {
+        using Te = ElemOf<E>;
+        float dot = 0.f;
+        for (int64_t k = 0; k < p.n; ++k) dot += Te::ld(gg + k * ag) * Te::ld(yy + k * ay);
+        for (int64_t k = 0; k < p.n; ++k) Te::st(dx + k * ad, Te::ld(yy + k * ay) * (Te::ld(gg + k * ag) - dot));
+    }
+}
+
+template <typename EI, typename EO>
+__global__ __launch_bounds__(256) void softmax_axis_fwd_block(SoftmaxAxis p) {
+    __shared__ float red[4];
+    int64_t bx, bg, by;
+    axis_bases(p, blockIdx.x, bx, bg, by);
+    using Ti = ElemOf<EI>;
+    using To = ElemOf<EO>;
+    const EI* x = (const EI*)p.x + bx;
+    EO* y = (EO*)p.y + by;
+    const int64_t ax = p.sx[p.axis], ay = p.sy[p.axis];
+    float m = -INFINITY;
+    for (int64_t k = threadIdx.x; k < p.n; k += 256) m = fmaxf(m, Ti::ld(x + k * ax));
+    m = block_reduce<EI>(m, true, red);
+    const float mc = m * kLog2e;
+    float s = 0.f;
+    for (int64_t k = threadIdx.x; k < p.n; k += 256) s += fast_exp2(fmaf(Ti::ld(x + k * ax), kLog2e, -mc));
+    s = block_reduce<EI>(s, false, red);
+    for (int64_t k = threadIdx.x; k < p.n; k += 256) To::st(y + k * ay, fast_exp2(fmaf(Ti::ld(x + k * ax), kLog2e, -mc)) / s);
+}
+
+__global__ __launch_bounds__(256) void softmax_axis_fwd_block_f64(SoftmaxAxis p) {
+    __shared__ double red[4];
+    int64_t bx, bg, by;
+    axis_bases(p, blockIdx.x, bx, bg, by);
+    const double* x = (const double*)p.x + bx;
+    double* y = (double*)p.y + by;
+    const int64_t ax = p.sx[p.axis], ay = p.sy[p.axis];
+    double m = -INFINITY;
+    for (int64_t k = threadIdx.x; k < p.n; k += 256) m = fmax(m, x[k * ax]);
+    m = block_reduce_f64(m, true, red);
+    double s = 0.0;
+    for (int64_t k = threadIdx.x; k < p.n; k += 256) s += exp(x[k * ax] - m);
+    s = block_reduce_f64(s, false, red);
+    for (int64_t k = threadIdx.x; k < p.n; k += 256) y[k * ay] = exp(x[k * ax] - m) / s;
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void softmax_axis_bwd_block(SoftmaxAxis p) {
+    using R = typename std::conditional<std::is_same<E, double>::value, double, float>::type;
+    __shared__ R red[4];
+    int64_t by, bg, bd;
+    axis_bases(p, blockIdx.x, by, bg, bd);
+    const E* yy = (const E*)p.x + by;
+    const E* gg = (const E*)p.g + bg;
+    E* dx = (E*)p.y + bd;
+    const int64_t ay = p.sx[p.axis], ag = p.sg[p.axis], ad = p.sy[p.axis];
+    R dot = 0;
+    if constexpr (std::is_same<E, double>::value) {
+        for (int64_t k = threadIdx.x; k < p.n; k += 256) dot += gg[k * ag] * yy[k * ay];
+        dot = block_reduce_f64(dot, false, red);
+        for (int64_t k = threadIdx.x; k < p.n; k += 256) dx[k * ad] = yy[k * ay] * (gg[k * ag] - dot);
+    } else {
+        using Te = ElemOf<E>;
+        for (int64_t k = threadIdx.x; k < p.n; k += 256) dot += Te::ld(gg + k * ag) * Te::ld(yy + k * ay);
+        dot = block_reduce<E>(dot, false, red);
+        for (int64_t k = threadIdx.x; k < p.n; k += 256)
+            Te::st(dx + k * ad, Te::ld(yy + k * ay) * (Te::ld(gg + k * ag) - dot));
+    }
+}
+
+// Lines per thread when there are enough of them to give every CU a few
+// workgroups; a workgroup per line otherwise.
+constexpr int64_t kAxisLinesMin = 256 * 256;
+
+template <typename EI, typename EO>
+static int launch_axis_fwd(const SoftmaxAxis& p, hipStream_t s) {
+    if (p.groups >= kAxisLinesMin)
+        hipLaunchKernelGGL((softmax_axis_fwd_lines<EI, EO>), dim3((unsigned)((p.groups + 255) / 256)), dim3(256), 0, s, p);
+    else if constexpr (std::is_same<EI, double>::value)
+        hipLaunchKernelGGL(softmax_axis_fwd_block_f64, dim3((unsigned)p.groups), dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((softmax_axis_fwd_block<EI, EO>), dim3((unsigned)p.groups), dim3(256), 0, s, p);
+    return (int)hipGetLastError();
+}
+template <typename E>
+static int launch_axis_bwd(const SoftmaxAxis& p, hipStream_t s) {
+    if (p.groups >= kAxisLinesMin)
+        hipLaunchKernelGGL((softmax_axis_bwd_lines<E>), dim3((unsigned)((p.groups + 255) / 256)), dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((softmax_axis_bwd_block<E>), dim3((unsigned)p.groups), dim3(256), 0, s, p);
+    return (int)hipGetLastError();
+}
+
+int launch_softmax_axis_fwd(const SoftmaxAxis& p, SmType t, hipStream_t s) {
+    switch (t) {
+        case SmType::F32: return launch_axis_fwd<float, float>(p, s);
+        case SmType::BF16: return launch_axis_fwd<uint16_t, uint16_t>(p, s);
+        case SmType::I32: return launch_axis_fwd<int32_t, float>(p, s);
+        case SmType::F64: return launch_axis_fwd<double, double>(p, s);
+    }
+    return (int)hipErrorInvalidValue;
+}
+int launch_softmax_axis_bwd(const SoftmaxAxis& p, SmType t, hipStream_t s) {
+    switch (t) {
+        case SmType::F32: return launch_axis_bwd<float>(p, s);
+        case SmType::BF16: return launch_axis_bwd<uint16_t>(p, s);
+        case SmType::F64: return launch_axis_bwd<double>(p, s);
+        default: return (int)hipErrorInvalidValue;
+    }
+}
+
 // E: element type of every operand (backward) or of the input (forward; the
 // output is EO).
 template <typename E, typename EO, bool BWD>

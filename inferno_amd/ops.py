@@ -142,6 +142,27 @@ def softmax_bwd(y, dy, out=None, stream=None):
     return out.reshape(y.shape)
 
 
+def softmax_axis_fwd(x, axis, stream=None):
+    """Softmax along `axis` of a strided view, on its own strides (no copies); the output is
+    dense in x's shape (Int32 input -> Float32 output)."""
+    odt = torch.float32 if x.dtype == torch.int32 else x.dtype
+    out = torch.empty(x.shape, dtype=odt, device=x.device)
+    st = lib().inf_softmax_fwd_axis(x.data_ptr(), _i64(x.stride()), out.data_ptr(), _i64(out.stride()), x.dim(),
+                                    _i64(x.shape), int(axis), _dt(x), _stream(stream))
+    _check(st, "inf_softmax_fwd_axis")
+    return out
+
+
+def softmax_axis_bwd(y, dy, axis, stream=None):
+    """dx = y * (dy - sum(dy * y)) along `axis` of strided views; dx dense in y's shape."""
+    out = torch.empty(y.shape, dtype=y.dtype, device=y.device)
+    st = lib().inf_softmax_bwd_axis(y.data_ptr(), _i64(y.stride()), dy.data_ptr(), _i64(dy.stride()),
+                                    out.data_ptr(), _i64(out.stride()), y.dim(), _i64(y.shape), int(axis), _dt(y),
+                                    _stream(stream))
+    _check(st, "inf_softmax_bwd_axis")
+    return out
+
+
 def _i64(vals):
     import ctypes
 

@@ -311,6 +311,34 @@ def test_decode_and_softmax_validation():
     assert L.inf_softmax_bwd(FAKE, FAKE, FAKE, 4, 4, 4, 4, 4, 3, None) == 4
 
 
+def test_softmax_axis_validation():
+    """inf_softmax_{fwd,bwd}_axis reject bad ranks, axes, shapes, strides, dtypes and null
+    pointers on the host (no device needed); empty views succeed without launching."""
+    L = ia.lib()
+    I64 = ctypes.c_int64 * 8
+
+    def a(*v):
+        return I64(*v)
+
+    shape, st = a(4, 5, 6), a(30, 6, 1)
+    assert L.inf_softmax_fwd_axis(FAKE, st, FAKE, st, 0, shape, 0, ia.INF_F32, None) == 2      # rank 0
+    assert L.inf_softmax_fwd_axis(FAKE, st, FAKE, st, 9, shape, 0, ia.INF_F32, None) == 5      # rank > 8
+    assert L.inf_softmax_fwd_axis(FAKE, st, FAKE, st, 3, shape, 3, ia.INF_F32, None) == 2      # axis
+    assert L.inf_softmax_fwd_axis(FAKE, st, FAKE, st, 3, shape, -4, ia.INF_F32, None) == 2
+    assert L.inf_softmax_fwd_axis(FAKE, st, FAKE, st, 3, a(4, -1, 6), 1, ia.INF_F32, None) == 2
+    assert L.inf_softmax_fwd_axis(FAKE, a(30, -6, 1), FAKE, st, 3, shape, 1, ia.INF_F32, None) == 3
+    assert L.inf_softmax_fwd_axis(FAKE, st, FAKE, a(30, 6, 0), 3, shape, 1, ia.INF_F32, None) == 3  # y overlaps
+    assert L.inf_softmax_fwd_axis(FAKE, st, FAKE, a(6, 1, 1), 3, shape, 0, ia.INF_F32, None) == 3
+    assert L.inf_softmax_fwd_axis(None, st, FAKE, st, 3, shape, 1, ia.INF_F32, None) == 1
+    assert L.inf_softmax_fwd_axis(FAKE, None, FAKE, st, 3, shape, 1, ia.INF_F32, None) == 1
+    assert L.inf_softmax_fwd_axis(FAKE, st, FAKE, st, 3, shape, 1, 7, None) == 4
+    assert L.inf_softmax_fwd_axis(None, st, None, st, 3, a(4, 0, 6), 1, ia.INF_F32, None) == 0  # empty
+    assert L.inf_softmax_bwd_axis(FAKE, st, FAKE, st, FAKE, st, 3, shape, 1, ia.INF_I32, None) == 4
+    assert L.inf_softmax_bwd_axis(FAKE, st, FAKE, None, FAKE, st, 3, shape, 1, ia.INF_F32, None) == 1
+    assert L.inf_softmax_bwd_axis(FAKE, st, None, st, FAKE, st, 3, shape, 1, ia.INF_F32, None) == 1
+    assert L.inf_softmax_bwd_axis(FAKE, st, FAKE, st, FAKE, a(30, 0, 1), 3, shape, 1, ia.INF_F32, None) == 3
+
+
 def test_product_does_not_reference_oracle():
     """The product (package + C sources) never loads the CPU oracle: there is no fallback."""
     pkg = Path(ia.__file__).parent

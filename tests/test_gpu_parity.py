@@ -809,6 +809,60 @@ def test_softmax_f64_i32(ia, rows, cols):
     assert oracle.rel_err(yi.cpu().numpy(), oracle.softmax_i32(xi)) <= TOL_F32
 
 
+def _softmax_axis_ref(x, axis, f):
+    """oracle row softmax (f) along `axis`: the axis moved last, rows, moved back."""
+    xm = np.ascontiguousarray(np.moveaxis(x, axis, -1))
+    return np.moveaxis(f(xm.reshape(-1, xm.shape[-1])).reshape(xm.shape), -1, axis)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f64", "i32"])
+@pytest.mark.parametrize("shape,axis,perm", [
+    ((64, 1024), 0, None),            # 1024 lines of 64: a workgroup per line
+    ((3, 700, 130), 1, None),         # middle axis
+    ((8, 64, 16, 128), 2, None),      # 65536 lines: a thread per line, coalesced over the last dim
+    ((4, 33, 20000), 1, None),        # 80000 lines of 33
+    ((5, 40, 6, 7), -1, (0, 2, 3, 1)),  # a permuted (strided) view, softmax over its last dim
+    ((6, 300, 9), 0, (2, 1, 0)),      # permuted view, first axis
+])
+def test_softmax_along_axis(ia, dt, shape, axis, perm):
+    """inf_softmax_{fwd,bwd}_axis on the operands' own strides against the oracle's row softmax
+    of the same data with the axis moved last: fp32 1e-4, bf16 2e-2, f64 1e-12, int32 input
+    (fp32 output) 1e-4; dy a differently permuted view of its own."""
+    print(f"[case] softmax axis {dt} {shape} axis {axis} perm {perm}", flush=True)
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f64": torch.float64, "i32": torch.int32}[dt]
+    base = oracle.randn(400, shape, 3.0)
+    if dt == "i32":
+        base = (base * 3).astype(np.int32)
+    elif dt == "bf16":
+        base = bf16_round(base)
+    elif dt == "f64":
+        base = base.astype(np.float64)
+    xt = torch.from_numpy(base).to("cuda").to(tdt)
+    x = xt.permute(*perm) if perm else xt
+    xn = np.transpose(base, perm) if perm else base
+    y = ia.softmax_axis_fwd(x, axis)
+    fwd = {"f32": oracle.softmax, "bf16": oracle.softmax, "f64": oracle.softmax_f64, "i32": oracle.softmax_i32}[dt]
+    y_r = _softmax_axis_ref(xn, axis, fwd)
+    tol = {"f32": TOL_F32, "bf16": TOL_BF16, "f64": 1e-12, "i32": TOL_F32}[dt]
+    torch.cuda.synchronize()
+    assert y.shape == x.shape and y.dtype == (torch.float32 if dt == "i32" else tdt)
+    assert oracle.rel_err(y.float().cpu().numpy() if dt != "f64" else y.cpu().numpy(), y_r) <= tol
+    if dt == "i32":
+        return
+    g = oracle.randn(401, x.shape)
+    g = g.astype(np.float64) if dt == "f64" else (bf16_round(g) if dt == "bf16" else g)
+    gt = torch.from_numpy(np.ascontiguousarray(np.swapaxes(g, 0, -1))).to("cuda").to(tdt).transpose(0, -1)
+    yin = y_r.astype(np.float64) if dt == "f64" else (bf16_round(y_r) if dt == "bf16" else y_r.astype(np.float32))
+    yt = torch.from_numpy(np.ascontiguousarray(yin)).to("cuda").to(tdt)
+    dx = ia.softmax_axis_bwd(yt, gt, axis)
+    bwd = oracle.softmax_bwd_f64 if dt == "f64" else oracle.softmax_bwd
+    dx_r = np.moveaxis(bwd(np.ascontiguousarray(np.moveaxis(yin, axis, -1)).reshape(-1, x.shape[axis]),
+                           np.ascontiguousarray(np.moveaxis(g, axis, -1)).reshape(-1, x.shape[axis]))
+                       .reshape(np.moveaxis(yin, axis, -1).shape), -1, axis)
+    torch.cuda.synchronize()
+    assert oracle.rel_err(dx.float().cpu().numpy() if dt != "f64" else dx.cpu().numpy(), dx_r) <= tol
+
+
 def test_softmax_masked_scores_exact_zeros(ia):
     """Scores masked with -1e9f (masked_fill) give exactly 0 probability."""
     T = 257
