@@ -98,7 +98,9 @@ struct BwdTile {
     static constexpr int KTS = BK + 4;       // K^T row stride
 };
 
-template <int D, typename E>
+// SHORT: the launch has short rows (p.n_short > 0); without them the kernel
+// carries neither the prologue nor the low part of delta.
+template <int D, typename E, bool SHORT>
 __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >= 128) ? 1 : 2) void bwd_main_kernel(
     BwdParams p) {
     constexpr int NW = BwdTile<D>::NW;
@@ -209,8 +211,10 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
         r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
         r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
         // rows past the short ones (and every row outside key block 0) read 0
-        const int n_sh = kblk == 0 ? max(0, min(p.n_short - q0, rows)) : 0;
-        r_dlo = buffer_ld1(row_rsrc(DLO, 1, q0, n_sh, 1), (uint32_t)tid * 4, 0);
+        if constexpr (SHORT) {
+            const int n_sh = kblk == 0 ? max(0, min(p.n_short - q0, rows)) : 0;
+            r_dlo = buffer_ld1(row_rsrc(DLO, 1, q0, n_sh, 1), (uint32_t)tid * 4, 0);
+        }
     };
     auto sstore_q = [&]() {
 #pragma unroll
@@ -222,7 +226,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
         if (tid < BQ) {
             lse_s[tid] = r_lse;  // natural-log LSE; scaled by log2(e) where it is read
             dl_s[tid] = r_dl;
-            dlo_s[tid] = r_dlo;
+            if constexpr (SHORT) dlo_s[tid] = r_dlo;
         }
     };
     // Short rows (bwd_split.h): before the main loop, their delta from this
@@ -236,8 +240,8 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
     // / sum(e) as hi + lo.  Each tile's loads are issued while the previous one
     // computes; the main loop's first barrier orders the last sums' reads
     // before it writes the dS tile they sit in.
-    const int qs_end = kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short tiles: [q_begin, qs_end)
-    if (q_begin < qs_end) {
+    const int qs_end = SHORT && kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short tiles: [q_begin, qs_end)
+    if (SHORT && q_begin < qs_end) {
         double* part = reinterpret_cast<double*>(&dSs[0][0]);  // [NW][BQ] pairs (sum e, sum e dP)
         static_assert(2 * NW * BQ * sizeof(double) <= sizeof(dSs), "the sums fit the dS tile");
         gload_q(q_begin, p.Tq);
@@ -339,7 +343,8 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
                 for (int j = 0; j < 4; ++j) {
                     const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLog2e;
                     const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
-                    const f32x4 Dlo = *reinterpret_cast<const f32x4*>(&dlo_s[8 * j + 4 * g]);
+                    const f32x4 Dlo = SHORT ? *reinterpret_cast<const f32x4*>(&dlo_s[8 * j + 4 * g])
+                                            : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int cc = 0; cc < 4; ++cc) {
                         const int r = 4 * j + cc;
@@ -350,7 +355,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
                             pr = vis ? pr : 0.f;
                         }
                         s[r] = pr;
-                        ds[r] = pr * ((dp[r] - Dl[cc]) - Dlo[cc]);
+                        ds[r] = pr * (SHORT ? (dp[r] - Dl[cc]) - Dlo[cc] : dp[r] - Dl[cc]);
                     }
                 }
             };
@@ -359,6 +364,17 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
                 p_ds(std::true_type{});
             else
                 p_ds(std::false_type{});
+            // A row with one visible key: dS = P (dP - dP) = 0.  (At D = 32 without
+            // short rows the kernel keeps three workgroups per CU only without this
+            // fix, 168 VGPRs; its short-row prologue, on small problems, forms
+            // delta = dP bit for bit instead.)
+            if constexpr (D != 32 || SHORT) {
+                if (bwd_one_key_tile(p, q0, k0w)) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (bwd_one_key_row(p, q0 + 8 * (r >> 2) + 4 * g + (r & 3))) ds[r] = 0.f;
+                }
+            }
             // dV^T += dO^T P ; dK^T += Q^T dS
 #pragma unroll
             for (int kk = 0; kk < 16; ++kk) {
@@ -524,6 +540,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void bwd_dq_kernel(BwdParams
     const float Lq = qrow < p.Tq ? p.lse[(int64_t)bh * p.Tq + qrow] * kLog2e : 0.f;
     const float Dq = qrow < p.Tq ? p.delta[(int64_t)bh * p.Tq + qrow] : 0.f;
     const float Dqlo = bwd_short_row(p, qrow) ? p.delta_lo[(int64_t)bh * p.Tq + qrow] : 0.f;
+    const bool one_key = qrow < p.Tq && bwd_one_key_row(p, qrow);
 
     int kv_end = p.Tk;
     if (p.causal) kv_end = min(p.Tk, qtile * BM + BM + p.off);
@@ -592,7 +609,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void bwd_dq_kernel(BwdParams
                     const int key = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
                     pr = (key <= lim && qrow < p.Tq) ? pr : 0.f;
                 }
-                s[r] = pr * ((dp[r] - Dq) - Dqlo);  // dS^T
+                s[r] = one_key ? 0.f : pr * ((dp[r] - Dq) - Dqlo);  // dS^T (0 on a one-key row)
             }
             // dQ^T[d][q] += K^T[d][keys] dS^T[keys][q]: MFMA (j, cc) reduces keys 8j + cc, 8j + 4 + cc
 #pragma unroll
@@ -715,11 +732,11 @@ static int bwd_slots(int D, int bf16, int* per_cu, int* cus_per_xcd) {
             if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) cus = n;
             hipError_t e = hipErrorInvalidValue;
             if (!bf16 && D == 32)
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<32, float>, 64 * bwd_waves(0, 32), 0);
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<32, float, false>, 64 * bwd_waves(0, 32), 0);
             if (!bf16 && D == 64)
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<64, float>, 64 * bwd_waves(0, 64), 0);
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<64, float, false>, 64 * bwd_waves(0, 64), 0);
             if (!bf16 && D == 128)
-                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<128, float>, 64 * bwd_waves(0, 128), 0);
+                e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&o, bwd_main_kernel<128, float, false>, 64 * bwd_waves(0, 128), 0);
             if (bf16) e = (hipError_t)bwd_main_bf16_occupancy(D, &o);
             if (e == hipSuccess && o > 0) occ = o;
             (void)hipGetLastError();  // a failed query of ours: the defaults stand
@@ -746,7 +763,7 @@ static void bwd_plan_compute(int B, int H, int Tq, int Tk, int D, int bf16, int 
         max_nt = std::max(max_nt, nt[(size_t)j]);
     }
     // query tiles [0, s_tiles) of key block 0 hold its short rows and run the prologue
-    const int s_tiles = (bwd_short_rows(Tq, Tk, 1, bk) + kBwdBQ - 1) / kBwdBQ;
+    const int s_tiles = (bwd_short_rows(B, H, Tq, Tk, 1, bk) + kBwdBQ - 1) / kBwdBQ;
     struct G { double cost; int kb, a, b, chunk, n; };
     // A key block of more than ch tiles is split into ceil(n / ch) chunks of
     // near-equal cost, block 0's short tiles counted with the prologue's share
@@ -887,7 +904,10 @@ static int launch_bwd_t(const BwdParams& p_in, hipStream_t s) {
         }
     } else {
         const dim3 grid((unsigned)(p.n_groups ? p.n_groups * bwd_padded_heads(p.B * p.H) : p.n_kblocks * p.B * p.H));
-        hipLaunchKernelGGL((bwd_main_kernel<D, E>), grid, dim3(64 * bwd_waves(0, D)), 0, s, p);
+        if (p.n_short > 0)
+            hipLaunchKernelGGL((bwd_main_kernel<D, E, true>), grid, dim3(64 * bwd_waves(0, D)), 0, s, p);
+        else
+            hipLaunchKernelGGL((bwd_main_kernel<D, E, false>), grid, dim3(64 * bwd_waves(0, D)), 0, s, p);
         if (p.dq_direct)
             hipLaunchKernelGGL((bwd_dq_kernel<D>), dim3((unsigned)(p.n_qtiles * p.B * p.H)), dim3(256), 0, s, p);
     }

@@ -158,7 +158,8 @@ __device__ __forceinline__ void bwd_short_prologue(const BwdParams& p, int bh, c
 // DWS: every query row is short (Tk within one key block), so the staging
 // takes delta from the workspace for every row instead of forming it from O
 // and dO.
-template <int D, bool DWS>
+// SHORT: the launch has short rows (p.n_short > 0; DWS implies it).
+template <int D, bool DWS, bool SHORT>
 __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || D >= 128) ? 1 : 2) void bwd_main_bf16_kernel(BwdParams p) {
     constexpr int NW = bwd_bf16_waves(D);  // waves per workgroup, 32 keys each
     constexpr int NT = 64 * NW;            // threads
@@ -353,7 +354,7 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
                         // staged negated: the dP accumulator starts at -delta; a
                         // short row's (formed by the prologue) comes from sdl_s
                         const int qi = staged_q0 + rem / C8;
-                        dl_s[rem / C8] = kblk == 0 && bwd_short_row(p, qi) ? sdl_s[qi] : -d;
+                        dl_s[rem / C8] = SHORT && kblk == 0 && bwd_short_row(p, qi) ? sdl_s[qi] : -d;
                     }
                 }
                 continue;
@@ -379,8 +380,8 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     };
 
     // Short rows (bwd_split.h): their delta before the main loop.
-    const int qs_end = kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short rows: [q_begin, qs_end)
-    if (q_begin < qs_end)
+    const int qs_end = SHORT && kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short rows: [q_begin, qs_end)
+    if (SHORT && q_begin < qs_end)
         bwd_short_prologue<D, NW, BK, PR, PSTR, true>(p, bh, Q, K, V, dO, q_begin, qs_end, lds.pr.k, lds.pr.v,
                                                       lds.pr.q, lds.pr.d, DWS ? nullptr : sdl_s);
 
@@ -499,6 +500,11 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
                 p_ds(std::true_type{});
             else
                 p_ds(std::false_type{});
+            if (bwd_one_key_tile(p, q0, k0w)) {  // a row with one visible key: dS = P (dP - dP) = 0
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (bwd_one_key_row(p, q0 + 8 * (r >> 2) + 4 * g + (r & 3))) dsb[r >> 3][r & 7] = (__bf16)0.f;
+            }
             // dV^T += dO^T P ; dK^T += Q^T dS  (reduce over the 32 queries, 16 per MFMA)
 #pragma unroll
             for (int m = 0; m < 2; ++m)
@@ -587,7 +593,7 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
 //                            with the queries in that order (16-byte reads)
 //   dQ += dS K               dS through LDS (keys contiguous), K^T staged once;
 //                            each wave one 16-query half x two 16-wide d blocks
-template <int D>
+template <int D, bool SHORT>
 __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) {
     static_assert(D == 128, "16-key waves are the D = 128 kernel");
     constexpr int NW = 8;
@@ -716,8 +722,8 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     };
 
     // Short rows (bwd_split.h): their delta before the main loop.
-    const int qs_end = kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short rows: [q_begin, qs_end)
-    if (q_begin < qs_end)
+    const int qs_end = SHORT && kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short rows: [q_begin, qs_end)
+    if (SHORT && q_begin < qs_end)
         bwd_short_prologue<D, NW, BK, PR, PSTR, false>(p, bh, Q, K, V, dO, q_begin, qs_end, lds.pr.k, lds.pr.v,
                                                        lds.pr.q, lds.pr.d, nullptr);
 
@@ -804,6 +810,11 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
                 p_ds(std::true_type{});
             else
                 p_ds(std::false_type{});
+            if (bwd_one_key_tile(p, q0, k0w)) {  // a row with one visible key: dS = P (dP - dP) = 0
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+                    if (bwd_one_key_row(p, q0 + 16 * (r >> 2) + 4 * g4 + (r & 3))) dsb[r] = (__bf16)0.f;
+            }
             // dV^T += dO^T P ; dK^T += Q^T dS over the 32 queries (one MFMA per d block).
             // The B operands' element j is query 16 (j / 4) + 4 g4 + j % 4, so lane
             // (l16, g4) takes column 16 db + l16 of rows 4 g4 + {0..3} and 16 + 4 g4
@@ -961,6 +972,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
     }
     const float Lq = qrow < p.Tq ? p.lse[(int64_t)bh * p.Tq + qrow] * kLog2e : 0.f;
     const float Dq = qrow < p.Tq ? p.delta[(int64_t)bh * p.Tq + qrow] : 0.f;
+    const bool one_key = qrow < p.Tq && bwd_one_key_row(p, qrow);
 
     int kv_end = p.Tk;
     if (p.causal) kv_end = min(p.Tk, qtile * BM + BM + p.off);
@@ -1060,7 +1072,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
                         const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
                         pr = (key <= lim && qrow < p.Tq) ? pr : 0.f;
                     }
-                    dsb[kb][r >> 3][r & 7] = (__bf16)(pr * (dp[kb][r] - Dq));
+                    dsb[kb][r >> 3][r & 7] = (__bf16)(one_key ? 0.f : pr * (dp[kb][r] - Dq));  // 0 on a one-key row
                 }
             // dQ^T[d][q] += K^T[d][keys] dS^T[keys][q]
             bf16x8 akt[NDB][NKB][2];
@@ -1114,9 +1126,9 @@ int launch_bwd_dq_bf16(const BwdParams& p, hipStream_t s) {
 
 int bwd_main_bf16_occupancy(int D, int* blocks_per_cu) {
     switch (D) {
-        case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<32, false>, 64 * bwd_bf16_waves(32), 0);
-        case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<64, false>, 64 * bwd_bf16_waves(64), 0);
-        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_w16_kernel<128>, 512, 0);
+        case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<32, false, false>, 64 * bwd_bf16_waves(32), 0);
+        case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<64, false, false>, 64 * bwd_bf16_waves(64), 0);
+        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_w16_kernel<128, false>, 512, 0);
         default: return (int)hipErrorInvalidValue;
     }
 }
@@ -1127,14 +1139,19 @@ int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s) {
     const dim3 grid((unsigned)(p.n_groups ? p.n_groups * bwd_padded_heads(p.B * p.H) : p.n_kblocks * p.B * p.H));
     switch (p.D) {
         case 32:
-            if (dws) hipLaunchKernelGGL((bwd_main_bf16_kernel<32, true>), grid, dim3(64 * bwd_bf16_waves(32)), 0, s, p);
-            else hipLaunchKernelGGL((bwd_main_bf16_kernel<32, false>), grid, dim3(64 * bwd_bf16_waves(32)), 0, s, p);
+            if (dws) hipLaunchKernelGGL((bwd_main_bf16_kernel<32, true, true>), grid, dim3(64 * bwd_bf16_waves(32)), 0, s, p);
+            else if (p.n_short > 0) hipLaunchKernelGGL((bwd_main_bf16_kernel<32, false, true>), grid, dim3(64 * bwd_bf16_waves(32)), 0, s, p);
+            else hipLaunchKernelGGL((bwd_main_bf16_kernel<32, false, false>), grid, dim3(64 * bwd_bf16_waves(32)), 0, s, p);
             break;
         case 64:
-            if (dws) hipLaunchKernelGGL((bwd_main_bf16_kernel<64, true>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p);
-            else hipLaunchKernelGGL((bwd_main_bf16_kernel<64, false>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p);
+            if (dws) hipLaunchKernelGGL((bwd_main_bf16_kernel<64, true, true>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p);
+            else if (p.n_short > 0) hipLaunchKernelGGL((bwd_main_bf16_kernel<64, false, true>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p);
+            else hipLaunchKernelGGL((bwd_main_bf16_kernel<64, false, false>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p);
             break;
-        case 128: hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128>), grid, dim3(512), 0, s, p); break;
+        case 128:
+            if (p.n_short > 0) hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128, true>), grid, dim3(512), 0, s, p);
+            else hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128, false>), grid, dim3(512), 0, s, p);
+            break;
         default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();

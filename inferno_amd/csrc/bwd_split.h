@@ -104,6 +104,16 @@ __device__ __forceinline__ bool bwd_one_key_row(const BwdParams& p, int i) {
     return p.causal ? i + p.off == 0 : p.Tk == 1;
 }
 
+// Whether the 32-row query tile at q0 holds a row whose only visible key is
+// key 0 while the wave's keys start at k0w (wave-uniform): the kernels then
+// set that row's dS to 0 after forming the tile's dS.
+__device__ __forceinline__ bool bwd_one_key_tile(const BwdParams& p, int q0, int k0w) {
+    if (k0w != 0) return false;
+    if (!p.causal) return p.Tk == 1;
+    const int r = -p.off;  // the row with i + off == 0
+    return r >= q0 && r < q0 + kBwdBQ && r < p.Tq;
+}
+
 // The weight of key j in short row i's delta: e = exp2(S c - lse log2 e) when
 // visible (vis), 1 for the one key of a one-key row, else 0.
 __device__ __forceinline__ float bwd_short_weight(const BwdParams& p, int i, bool vis, float e) {

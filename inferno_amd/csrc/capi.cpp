@@ -254,7 +254,7 @@ int inf_attn_bwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     p.c = scale * 1.4426950408889634f;
     const int bk = inf::bwd_keys_per_wg(dt == INF_BF16, D);
     p.n_kblocks = (Tk + bk - 1) / bk;
-    p.n_short = inf::bwd_short_rows(Tq, Tk, p.causal, bk);
+    p.n_short = inf::bwd_short_rows(B, H, Tq, Tk, p.causal, bk);
     p.dq_direct = dq_from_pass(det, B, H, Tq, Tk, D, dt) ? 1 : 0;
     p.n_qtiles = (Tq + inf::kBwdDqBM - 1) / inf::kBwdDqBM;
     if (p.dq_direct) p.dq_acc = nullptr;  // dq is written by the dQ pass

@@ -335,11 +335,19 @@ inline int bwd_keys_per_wg(int bf16, int D) { return bf16 && D == 128 ? 128 : 32
 constexpr int kBwdBQ = 32;       // query rows per backward inner step
 // Leading query rows whose visible keys all lie in key block 0 (keys_per_wg
 // keys): their softmax-backward row dot is formed inside the block-0
-// workgroup from its own P and dP (bwd_split.h).
-inline int bwd_short_rows(int Tq, int Tk, int causal, int keys_per_wg) {
-    if (!causal) return Tk <= keys_per_wg ? Tq : 0;
-    const int64_t r = (int64_t)keys_per_wg - ((int64_t)Tk - Tq);
-    return (int)(r < 0 ? 0 : (r > Tq ? Tq : r));
+// workgroup from its own P and dP (bwd_split.h) -- on problems where those
+// rows number at most kBwdShortMaxRows over all heads, else none.  There each
+// row's rounding is measured against a scale the row itself sets (few rows),
+// and the prologue that forms it costs little; on larger problems the tensor's
+// scale comes from many rows, the row dot from rowsum(dO * O) is far within
+// the error bars, and the prologue measured +10-70% on short sequences (its S
+// and dP on every short row again).  Rows with one visible key need no row
+// dot: every kernel sets their dS to 0, as P (dP - dP) is.
+constexpr int64_t kBwdShortMaxRows = 4096;
+inline int bwd_short_rows(int B, int H, int Tq, int Tk, int causal, int keys_per_wg) {
+    int64_t r = causal ? (int64_t)keys_per_wg - ((int64_t)Tk - Tq) : (Tk <= keys_per_wg ? Tq : 0);
+    r = r < 0 ? 0 : (r > Tq ? Tq : r);
+    return (int64_t)B * H * r <= kBwdShortMaxRows ? (int)r : 0;
 }
 constexpr int kBwdDqBM = 128;    // query rows per workgroup of the query-major dQ pass
 int launch_bwd_dq_bf16(const BwdParams& p, hipStream_t s);
