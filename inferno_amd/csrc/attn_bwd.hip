@@ -541,6 +541,7 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void bwd_dq_kernel(BwdParams
     const float Dq = qrow < p.Tq ? p.delta[(int64_t)bh * p.Tq + qrow] : 0.f;
     const float Dqlo = bwd_short_row(p, qrow) ? p.delta_lo[(int64_t)bh * p.Tq + qrow] : 0.f;
     const bool one_key = qrow < p.Tq && bwd_one_key_row(p, qrow);
+    const bool one_key_wave = p.causal ? (-p.off >= q0w && -p.off < q0w + 32) : p.Tk == 1;  // wave-uniform
 
     int kv_end = p.Tk;
     if (p.causal) kv_end = min(p.Tk, qtile * BM + BM + p.off);
@@ -602,15 +603,23 @@ __global__ __launch_bounds__(256, D >= 128 ? 1 : 2) void bwd_dq_kernel(BwdParams
             // reg r: key k0 + 8 (r / 4) + 4 g + r % 4 of query qrow
             const bool need_mask = (k0 + BN > p.Tk) || (qtile * BM + BM > p.Tq) || (p.causal && (k0 + BN - 1 > q0w + p.off));
             const int lim = p.causal ? min(p.Tk - 1, qrow + p.off) : p.Tk - 1;
+            // the visibility test only on tiles that cross the diagonal or the ends
+            auto p_ds = [&](auto masked) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float pr = fast_exp2(fmaf(s[r], c, -Lq));
-                if (need_mask) {
-                    const int key = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    pr = (key <= lim && qrow < p.Tq) ? pr : 0.f;
+                for (int r = 0; r < 16; ++r) {
+                    float pr = fast_exp2(fmaf(s[r], c, -Lq));
+                    if constexpr (decltype(masked)::value) {
+                        const int key = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
+                        pr = (key <= lim && qrow < p.Tq) ? pr : 0.f;
+                    }
+                    s[r] = pr * ((dp[r] - Dq) - Dqlo);  // dS^T
                 }
-                s[r] = one_key ? 0.f : pr * ((dp[r] - Dq) - Dqlo);  // dS^T (0 on a one-key row)
-            }
+            };
+            if (need_mask)
+                p_ds(std::true_type{});
+            else
+                p_ds(std::false_type{});
+            if (one_key_wave && k0 == 0 && one_key) s = f32x16{};  // one visible key: dS = P (dP - dP) = 0
             // dQ^T[d][q] += K^T[d][keys] dS^T[keys][q]: MFMA (j, cc) reduces keys 8j + cc, 8j + 4 + cc
 #pragma unroll
             for (int j = 0; j < 4; ++j) {

@@ -174,8 +174,12 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
     // {0..3} contiguous at 16m + 8g), so an operand is one 16-byte read
     // instead of two 8-byte ones (1.5-2% faster at D = 32 and 64).
     constexpr int TS = BQ + 8;           // row stride (bf16): 20 dwords keep the 16-byte reads conflict-free
-    constexpr int SS = BK + 8;           // dS stride (bf16)
-    constexpr int KTS = BK + 8;          // K^T stride (bf16)
+    // dS and K^T row strides of an odd multiple of 32 bytes: the dQ product's
+    // 16-byte reads (lane (l16, g4) at row l16, byte 16 g4 of a 64-byte slice)
+    // are then conflict-free on gfx950's LDS (BK + 8 measured 1.67x slower
+    // per read; config 2 backward -0.8%, D = 32 -1%).
+    constexpr int SS = BK + 16;          // dS stride (bf16)
+    constexpr int KTS = BK + 16;         // K^T stride (bf16)
     constexpr int QTASK = (BQ / 2) * C8;                 // (row pair, chunk) tasks per tensor
     constexpr int QLPT = (2 * QTASK + NT - 1) / NT;      // Q and dO together, per thread
     constexpr int KTASK = (BK / 2) * C8;
@@ -973,6 +977,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
     const float Lq = qrow < p.Tq ? p.lse[(int64_t)bh * p.Tq + qrow] * kLog2e : 0.f;
     const float Dq = qrow < p.Tq ? p.delta[(int64_t)bh * p.Tq + qrow] : 0.f;
     const bool one_key = qrow < p.Tq && bwd_one_key_row(p, qrow);
+    const bool one_key_wave = p.causal ? (-p.off >= q0w && -p.off < q0w + 32) : p.Tk == 1;  // wave-uniform
 
     int kv_end = p.Tk;
     if (p.causal) kv_end = min(p.Tk, qtile * BM + BM + p.off);
@@ -1063,17 +1068,29 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
             const bool need_mask = (k0 + BN > p.Tk) || (qtile * BM + BM > p.Tq) || (p.causal && (k0 + BN - 1 > q0w + p.off));
             const int lim = p.causal ? min(p.Tk - 1, qrow + p.off) : p.Tk - 1;
             bf16x8 dsb[NKB][2];
+            // the visibility test only on tiles that cross the diagonal or the ends
+            auto p_ds = [&](auto masked) {
 #pragma unroll
-            for (int kb = 0; kb < NKB; ++kb)
+                for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float pr = fast_exp2(fmaf(s[kb][r], c, -Lq));
-                    if (need_mask) {
-                        const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                        pr = (key <= lim && qrow < p.Tq) ? pr : 0.f;
+                    for (int r = 0; r < 16; ++r) {
+                        float pr = fast_exp2(fmaf(s[kb][r], c, -Lq));
+                        if constexpr (decltype(masked)::value) {
+                            const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                            pr = (key <= lim && qrow < p.Tq) ? pr : 0.f;
+                        }
+                        dsb[kb][r >> 3][r & 7] = (__bf16)(pr * (dp[kb][r] - Dq));
                     }
-                    dsb[kb][r >> 3][r & 7] = (__bf16)(one_key ? 0.f : pr * (dp[kb][r] - Dq));  // 0 on a one-key row
-                }
+            };
+            if (need_mask)
+                p_ds(std::true_type{});
+            else
+                p_ds(std::false_type{});
+            if (one_key_wave && k0 == 0) {  // a row with one visible key: dS = P (dP - dP) = 0
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+                    if (one_key) dsb[kb][0] = dsb[kb][1] = bf16x8{};
+            }
             // dQ^T[d][q] += K^T[d][keys] dS^T[keys][q]
             bf16x8 akt[NDB][NKB][2];
 #pragma unroll
