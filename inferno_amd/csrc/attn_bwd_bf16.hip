@@ -701,7 +701,10 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     // the same rows transposed (ds_read_b64_tr_b16).
     bf16x8 ra, rb;
     float r_lse = 0.f, r_dl = 0.f;
-    const int which = tid / QTASK;          // 0: Q, 1: dO (wave-uniform)
+    // 0: Q, 1: dO; wave-uniform, and read as such so the row stride is a
+    // scalar (a per-lane value there made the compiler loop over its lanes'
+    // values for the buffer loads' scalar offset)
+    const int which = __builtin_amdgcn_readfirstlane(tid / QTASK);
     const int rem = tid % QTASK;
     const int cq = rem % C8, rq = rem / C8;
     static_assert(QTASK == (BQ / 2) * C8 && C8 == 16, "16 chunks x 16 row pairs per tensor");
