@@ -43,34 +43,51 @@
 
 namespace inf {
 
+// delta = rowsum(dO * O) per query row, and the zeroing of the fp32 dQ
+// accumulator and the split plan's arrival counters.  Each thread takes one
+// 16-byte chunk of O and dO (4 fp32 or 8 bf16 elements; TPR threads per row)
+// and the row's threads sum their products with DPP moves.
+template <int D, typename E>
+constexpr int bwd_pre_tpr() { return D / (16 / (int)sizeof(E)); }
+template <int D, typename E>
+constexpr int bwd_pre_rows_per_block() { return 256 / bwd_pre_tpr<D, E>(); }
+
 template <int D, typename E>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdParams p) {
-    constexpr int TPR = D / 4;         // threads per row
-    constexpr int RPB = 256 / TPR;     // rows per block
+    constexpr int VEC = 16 / (int)sizeof(E);   // elements per 16-byte chunk
+    constexpr int TPR = bwd_pre_tpr<D, E>();    // threads per row
+    constexpr int RPB = bwd_pre_rows_per_block<D, E>();
     const int tid = threadIdx.x;
     const int64_t row = (int64_t)blockIdx.x * RPB + tid / TPR;
-    const int c4 = tid % TPR;
+    const int c = tid % TPR;
     const int64_t rows = (int64_t)p.B * p.H * p.Tq;
     float s = 0.f;
-    int64_t bh = 0, i = 0;
     if (row < rows) {
-        bh = row / p.Tq;
-        i = row % p.Tq;
+        const int64_t bh = row / p.Tq, i = row % p.Tq;
         const int64_t b = bh / p.H, h = bh % p.H;
         if (p.pre_delta) {
-            const f32x4 o4 = ld4((const E*)p.o + b * p.so.b + h * p.so.h + i * p.so.t + 4 * c4);
-            const f32x4 d4 = ld4((const E*)p.dout + b * p.sdo.b + h * p.sdo.h + i * p.sdo.t + 4 * c4);
-            s = o4[0] * d4[0] + o4[1] * d4[1] + o4[2] * d4[2] + o4[3] * d4[3];
+            const E* po = (const E*)p.o + b * p.so.b + h * p.so.h + i * p.so.t + VEC * c;
+            const E* pd = (const E*)p.dout + b * p.sdo.b + h * p.sdo.h + i * p.sdo.t + VEC * c;
+            if constexpr (sizeof(E) == 4) {
+                const f32x4 o4 = ld4(po), d4 = ld4(pd);
+                s = o4[0] * d4[0] + o4[1] * d4[1] + o4[2] * d4[2] + o4[3] * d4[3];
+            } else {
+                const u16x8 o8 = *reinterpret_cast<const u16x8*>(po);
+                const u16x8 d8 = *reinterpret_cast<const u16x8*>(pd);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) s = fmaf(bf16_to_f32(o8[k]), bf16_to_f32(d8[k]), s);
+            }
         }
-        if (!p.dq_direct)
-            *reinterpret_cast<f32x4*>(p.dq_acc + b * p.sacc.b + h * p.sacc.h + i * p.sacc.t + 4 * c4) =
-                f32x4{0.f, 0.f, 0.f, 0.f};
+        if (!p.dq_direct) {
+            f32x4* acc = reinterpret_cast<f32x4*>(p.dq_acc + b * p.sacc.b + h * p.sacc.h + i * p.sacc.t + VEC * c);
+#pragma unroll
+            for (int k = 0; k < VEC / 4; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
     }
     // (p.pre_delta is uniform: the whole grid takes or skips the exchange)
     if (p.pre_delta) {
-#pragma unroll
-        for (int m = TPR / 2; m >= 1; m >>= 1) s += shfl_xor(s, m);
-        if (row < rows && c4 == 0) p.delta[row] = s;
+        s = group_sum<TPR>(s);
+        if (row < rows && c == 0) p.delta[row] = s;
     }
     if (blockIdx.x == 0)
         for (int i = tid; i < p.n_split * p.B * p.H; i += 256) p.counters[i] = 0u;
@@ -893,14 +910,16 @@ static int launch_bwd_t(const BwdParams& p_in, hipStream_t s) {
     p.pre_delta = (sizeof(E) == 2 && D <= 64) ? p.dq_direct : 1;
     constexpr int RPB = 256 / (D / 4);
     const int64_t rows = (int64_t)p.B * p.H * p.Tq;
-    const dim3 pre_grid((unsigned)((rows + RPB - 1) / RPB));
+    const dim3 pre_grid((unsigned)((rows + RPB - 1) / RPB));  // bwd_cvt: 4 elements per thread
+    constexpr int PRE_RPB = bwd_pre_rows_per_block<D, E>();
+    const dim3 delta_grid((unsigned)((rows + PRE_RPB - 1) / PRE_RPB));
     if (!p.pre_delta && !p.dq_direct) {
         // zeroing only: a few grid-stride workgroups per CU
         const int64_t n4 = rows * D / 4;
         const unsigned zb = (unsigned)std::min<int64_t>((n4 + 255) / 256, 2048);
         hipLaunchKernelGGL(bwd_zero_kernel, dim3(zb), dim3(256), 0, s, p);
     } else {
-        hipLaunchKernelGGL((bwd_pre_kernel<D, E>), pre_grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((bwd_pre_kernel<D, E>), delta_grid, dim3(256), 0, s, p);
     }
     if constexpr (sizeof(E) == 2) {
         const int e = launch_bwd_main_bf16(p, s);
