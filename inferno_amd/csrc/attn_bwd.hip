@@ -43,6 +43,24 @@
 
 namespace inf {
 
+// Batch, head and position of row `row` of the [B, H, Tq] rows: 32-bit
+// divisions when the row count fits (every practical shape), as 64-bit ones
+// cost tens of instructions per thread in these memory-bound passes.
+__device__ __forceinline__ void bwd_row_split(const BwdParams& p, int64_t rows, int64_t row, int64_t& b, int64_t& h,
+                                              int64_t& i) {
+    if (rows <= 0xffffffffLL) {
+        const uint32_t r = (uint32_t)row, bh = r / (uint32_t)p.Tq;
+        i = r - bh * (uint32_t)p.Tq;
+        b = bh / (uint32_t)p.H;
+        h = bh - (uint32_t)b * (uint32_t)p.H;
+    } else {
+        const int64_t bh = row / p.Tq;
+        i = row % p.Tq;
+        b = bh / p.H;
+        h = bh % p.H;
+    }
+}
+
 // delta = rowsum(dO * O) per query row, and the zeroing of the fp32 dQ
 // accumulator and the split plan's arrival counters.  Each thread takes one
 // 16-byte chunk of O and dO (4 fp32 or 8 bf16 elements; TPR threads per row)
@@ -63,8 +81,8 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdParams p) {
     const int64_t rows = (int64_t)p.B * p.H * p.Tq;
     float s = 0.f;
     if (row < rows) {
-        const int64_t bh = row / p.Tq, i = row % p.Tq;
-        const int64_t b = bh / p.H, h = bh % p.H;
+        int64_t b, h, i;
+        bwd_row_split(p, rows, row, b, h, i);
         if (p.pre_delta) {
             const E* po = (const E*)p.o + b * p.so.b + h * p.so.h + i * p.so.t + VEC * c;
             const E* pd = (const E*)p.dout + b * p.sdo.b + h * p.sdo.h + i * p.sdo.t + VEC * c;
@@ -480,8 +498,8 @@ __global__ __launch_bounds__(256) void bwd_cvt_kernel(BwdParams p) {
     const int c4 = tid % TPR;
     const int64_t rows = (int64_t)p.B * p.H * p.Tq;
     if (row >= rows) return;
-    const int64_t bh = row / p.Tq, i = row % p.Tq;
-    const int64_t b = bh / p.H, h = bh % p.H;
+    int64_t b, h, i;
+    bwd_row_split(p, rows, row, b, h, i);
     const f32x4 a = *reinterpret_cast<const f32x4*>(p.dq_acc + b * p.sacc.b + h * p.sacc.h +
                                                      i * p.sacc.t + 4 * c4);
     st4((uint16_t*)p.dq + b * p.sdq.b + h * p.sdq.h + i * p.sdq.t + 4 * c4, a);
