@@ -46,11 +46,13 @@ BWD_TRAFFIC_SOURCE = "profiles/attn_c2_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZ
 
 METRIC = "causal attn fwd+bwd TFLOP/s (B8 H12 T1024 D64 fp32) + % of MFMA peak"
 
-# per-config lines that --only runs alone: (B, H, T, D, Q/K sigma, dtype)
+# per-config lines that --only runs alone: (B, H, T, D, Q/K sigma, dtype, deterministic-dQ mode)
 ONLY_CONFIGS = {
-    "c2_bf16": (8, 12, 1024, 64, 1.0, "bf16"),
-    "c4_f32": (1, 16, 8192, 128, 3.0, "f32"),
-    "c4_bf16": (1, 16, 8192, 128, 3.0, "bf16"),
+    "c2_bf16": (8, 12, 1024, 64, 1.0, "bf16", False),
+    "c4_f32": (1, 16, 8192, 128, 3.0, "f32", False),
+    "c4_bf16": (1, 16, 8192, 128, 3.0, "bf16", False),
+    "c2_f32_deterministic": (8, 12, 1024, 64, 1.0, "f32", True),
+    "c2_bf16_deterministic": (8, 12, 1024, 64, 1.0, "bf16", True),
 }
 
 
@@ -194,7 +196,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the config-2 bf16 and deterministic, config-3 and config-4 lines")
     ap.add_argument("--gpt-steps", type=int, default=5, help="timed steps of the config-3 GPT line")
-    ap.add_argument("--only", choices=sorted(ONLY_CONFIGS) + ["shape"],
+    ap.add_argument("--only", choices=sorted(ONLY_CONFIGS) + ["shape", "c5_decode"],
                     help="run only this per-config line, with --steps timed steps (for profiling); "
                          "'shape' runs --shape / --dtype / --non-causal instead")
     ap.add_argument("--shape", default="8,12,1024,64", help="B,H,T,D for --only shape")
@@ -226,14 +228,18 @@ def main():
     import oracle
 
     if args.only:
-        causal = True
+        causal, det = True, False
+        if args.only == "c5_decode":
+            r = bench_decode(ia, oracle, torch, np, torch.device("cuda:0"))
+            print(json.dumps({"decode": r}), flush=True)
+            return
         if args.only == "shape":
             B, H, T, D = (int(x) for x in args.shape.split(","))
             sigma, dtype, causal = 1.0, args.dtype, not args.non_causal
         else:
-            B, H, T, D, sigma, dtype = ONLY_CONFIGS[args.only]
+            B, H, T, D, sigma, dtype, det = ONLY_CONFIGS[args.only]
         r = bench_attn(ia, oracle, torch, np, torch.device("cuda:0"), B, H, T, D, sigma, dtype, steps=args.steps,
-                       causal=causal)
+                       deterministic=det, causal=causal)
         print(json.dumps({"configs": {args.only: r}}), flush=True)
         return
 
