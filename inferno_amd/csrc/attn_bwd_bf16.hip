@@ -1010,6 +1010,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
         for (int i = 0; i < VLPT; ++i)
             vr[i] = buffer_ld8bf(rv, v_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sv.t * 2));
     };
+    const uint32_t vs_off = (uint32_t)(((tid / C8) * KS + 8 * (tid % C8)) * 2);
     auto sstore = [&](int buf) {
         const int k = 2 * kp;
         const int pos = (k & ~15) | ((k & 4) << 1) | ((k & 8) >> 1) | (k & 3);
@@ -1027,11 +1028,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
                 *reinterpret_cast<bf16x2*>(&KTs[buf][8 * c8 + e][pos]) = pr;
             }
         }
+        // V chunk tid + 256 i: row tid / C8 + (256 / C8) i, column chunk tid % C8
+        // (a per-thread offset plus a constant: immediate store offsets)
+        char* vb = reinterpret_cast<char*>(&Vs[buf][0][0]) + vs_off;
 #pragma unroll
-        for (int i = 0; i < VLPT; ++i) {
-            const int f = tid + 256 * i;
-            *reinterpret_cast<bf16x8*>(&Vs[buf][f / C8][8 * (f % C8)]) = vr[i];
-        }
+        for (int i = 0; i < VLPT; ++i) *reinterpret_cast<bf16x8*>(vb + i * (256 / C8) * KS * 2) = vr[i];
     };
     auto rows_of = [&](int u) { return u < nt ? min(p.Tk - u * BN, BN) : 0; };
 

@@ -131,13 +131,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
         for (int i = 0; i < KLPT; ++i)
             vr[i] = buffer_ld8bf(rv, v_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sv.t * 2));
     };
+    // Chunk tid + 256 i lands in row tid / C8 + (256 / C8) i, column chunk
+    // tid % C8: a per-thread LDS offset plus a constant per i (immediate
+    // offsets of the stores, no address arithmetic per tile).
+    const uint32_t ks_off = (uint32_t)(((tid / C8) * KS + 8 * (tid % C8)) * 2);
+    const uint32_t vs_off = (uint32_t)(((tid / C8) * VS + 8 * (tid % C8)) * 2);
     auto sstore = [&](int buf) {
+        char* kb = reinterpret_cast<char*>(&Ks[buf][0][0]) + ks_off;
+        char* vb = reinterpret_cast<char*>(&Vs[buf][0][0]) + vs_off;
 #pragma unroll
         for (int i = 0; i < KLPT; ++i) {
-            const int f = tid + 256 * i;
-            const int row = f / C8, c8 = f % C8;
-            *reinterpret_cast<bf16x8*>(&Ks[buf][row][8 * c8]) = kr[i];
-            *reinterpret_cast<bf16x8*>(&Vs[buf][row][8 * c8]) = vr[i];
+            *reinterpret_cast<bf16x8*>(kb + i * (256 / C8) * KS * 2) = kr[i];
+            *reinterpret_cast<bf16x8*>(vb + i * (256 / C8) * VS * 2) = vr[i];
         }
     };
 
