@@ -191,11 +191,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
                         if (key > lim) s[kb][r] = -INFINITY;
                     }
             }
-            float mloc = -INFINITY;
+            // row max as four independent chains (a single chain of dependent
+            // three-input maxima waits out the VALU latency at every step)
+            float mp[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[kb][r]);
+                for (int r = 0; r < 16; ++r) mp[r & 3] = fmaxf(mp[r & 3], s[kb][r]);
+            float mloc = fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]));
             mloc = max_xor32(mloc);
             // Lazy rescaling, per row: the reference max moves only when the
             // row sees a score 2^8 (in exp2 units) above it; the wave skips the
@@ -212,14 +215,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
             // A row of a split chunk may have no visible key in the chunk: it
             // keeps m_run = -inf, p = 0, and the merge skips its partial.
             const float mc = SPLIT && m_run == -INFINITY ? 0.f : m_run * c;
-            float ls[4] = {0.f, 0.f, 0.f, 0.f};  // row sum as four independent chains
+            float ls[4];  // row sum as four independent chains
             bf16x8 pb[NKB][2];
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const float e = fast_exp2(fmaf(s[kb][r], c, -mc));
-                    ls[r & 3] += e;
+                    ls[r & 3] = kb == 0 && r < 4 ? e : ls[r & 3] + e;
                     pb[kb][r >> 3][r & 7] = (__bf16)e;
                 }
             l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
