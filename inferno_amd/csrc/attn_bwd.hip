@@ -488,7 +488,25 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
     }
 }
 
-// dQ accumulator (fp32) -> bf16 dq.
+// dQ accumulator (fp32) -> bf16 dq, when dq has the accumulator's dense
+// [B, H, Tq, D] layout and 16-byte aligned rows: a flat pass, 8 elements
+// (two 16-byte loads, one 16-byte store) per thread.
+__global__ __launch_bounds__(256) void bwd_cvt_flat_kernel(BwdParams p) {
+    const int64_t n8 = (int64_t)p.B * p.H * p.Tq * p.D / 8;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    const f32x4* a = reinterpret_cast<const f32x4*>(p.dq_acc) + 2 * i;
+    const f32x4 x = a[0], y = a[1];
+    u16x8 h;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        h[k] = f32_to_bf16(x[k]);
+        h[4 + k] = f32_to_bf16(y[k]);
+    }
+    reinterpret_cast<u16x8*>(p.dq)[i] = h;
+}
+
+// dQ accumulator (fp32) -> bf16 dq on dq's own strides.
 template <int D>
 __global__ __launch_bounds__(256) void bwd_cvt_kernel(BwdParams p) {
     constexpr int TPR = D / 4;
@@ -946,7 +964,12 @@ static int launch_bwd_t(const BwdParams& p_in, hipStream_t s) {
             const int e2 = launch_bwd_dq_bf16(p, s);
             if (e2) return e2;
         } else {
-            hipLaunchKernelGGL((bwd_cvt_kernel<D>), pre_grid, dim3(256), 0, s, p);
+            const bool dense = p.sdq.t == D && p.sdq.h == (int64_t)p.Tq * D && p.sdq.b == (int64_t)p.H * p.Tq * D &&
+                               reinterpret_cast<uintptr_t>(p.dq) % 16 == 0;
+            if (dense)
+                hipLaunchKernelGGL(bwd_cvt_flat_kernel, dim3((unsigned)((rows * D / 8 + 255) / 256)), dim3(256), 0, s, p);
+            else
+                hipLaunchKernelGGL((bwd_cvt_kernel<D>), pre_grid, dim3(256), 0, s, p);
         }
     } else {
         const dim3 grid((unsigned)(p.n_groups ? p.n_groups * bwd_padded_heads(p.B * p.H) : p.n_kblocks * p.B * p.H));
