@@ -694,13 +694,13 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     const int q_end = wk.q_end;
     const float c = p.c;
 
-    // Q / dO staging, row-major only (prefetched one tile ahead, double-
-    // buffered with dS, one barrier per tile): thread (rq, cq) stores 16-byte
+    // Q / dO staging, row-major only (double-buffered with dS, one barrier
+    // per tile): thread (rq, cq) stores 16-byte
     // chunk cq of rows rq and rq + 16, so a wave's 16 lanes of one row write
     // 256 consecutive bytes (conflict-free).  The dV^T / dK^T operands read
     // the same rows transposed (ds_read_b64_tr_b16).
-    bf16x8 ra, rb;
-    float r_lse = 0.f, r_dl = 0.f;
+    bf16x8 ra[2], rb[2];
+    float r_lse[2] = {0.f, 0.f}, r_dl[2] = {0.f, 0.f};
     // 0: Q, 1: dO; wave-uniform, and read as such so the row stride is a
     // scalar (a per-lane value there made the compiler loop over its lanes'
     // values for the buffer loads' scalar offset)
@@ -708,25 +708,30 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     const int rem = tid % QTASK;
     const int cq = rem % C8, rq = rem / C8;
     static_assert(QTASK == (BQ / 2) * C8 && C8 == 16, "16 chunks x 16 row pairs per tensor");
-    auto gload_q = [&](int q0, int lim) {
+    // register set rs (0 / 1, compile-time at every call) <- tile q0
+    auto gload_q = [&](auto rs_c, int q0, int lim) {
+        constexpr int rs = decltype(rs_c)::value;
         const int rows = min(lim - q0, BQ);
         const int64_t st = which ? p.sdo.t : p.sq.t;
-        const auto rs = row_rsrc(which ? dO : Q, st, q0, rows, D);
+        const auto rsrc = row_rsrc(which ? dO : Q, st, q0, rows, D);
         const uint32_t voff = (uint32_t)(((int64_t)rq * st + 8 * cq) * 2);
-        ra = buffer_ld8bf(rs, voff, 0);
-        rb = buffer_ld8bf(rs, voff, (uint32_t)((BQ / 2) * st * 2));
-        r_lse = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
-        r_dl = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
+        ra[rs] = buffer_ld8bf(rsrc, voff, 0);
+        rb[rs] = buffer_ld8bf(rsrc, voff, (uint32_t)((BQ / 2) * st * 2));
+        r_lse[rs] = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
+        r_dl[rs] = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
     };
-    auto sstore_q = [&](int sb) {
+    auto sstore_q = [&](auto rs_c, int sb) {
+        constexpr int rs = decltype(rs_c)::value;
         __bf16(*rows)[QS] = which ? dOs2[sb] : Qs2[sb];
-        *reinterpret_cast<bf16x8*>(&rows[rq][8 * cq]) = ra;
-        *reinterpret_cast<bf16x8*>(&rows[rq + BQ / 2][8 * cq]) = rb;
+        *reinterpret_cast<bf16x8*>(&rows[rq][8 * cq]) = ra[rs];
+        *reinterpret_cast<bf16x8*>(&rows[rq + BQ / 2][8 * cq]) = rb[rs];
         if (tid < BQ) {
-            lse_s2[sb][tid] = r_lse * kLog2e;  // LSE in base 2
-            dl_s2[sb][tid] = r_dl;
+            lse_s2[sb][tid] = r_lse[rs] * kLog2e;  // LSE in base 2
+            dl_s2[sb][tid] = r_dl[rs];
         }
     };
+    using R0 = std::integral_constant<int, 0>;
+    using R1 = std::integral_constant<int, 1>;
 
     // Short rows (bwd_split.h): their delta before the main loop.
     const int qs_end = SHORT && kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short rows: [q_begin, qs_end)
@@ -753,17 +758,22 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
         }
     }
 
-    gload_q(q_begin, p.Tq);
-    sstore_q(0);
+    // Q / dO tiles are loaded two tiles ahead (two register sets), stored one
+    // tile ahead: a load that misses the L2 has a whole tile more to arrive.
+    gload_q(R0{}, q_begin, p.Tq);
+    sstore_q(R0{}, 0);
+    gload_q(R1{}, q_begin + BQ, q_begin + BQ < q_end ? p.Tq : 0);
     __syncthreads();
 
     // dQ blocks of this wave: query half qhw, d blocks 2 dcw and 2 dcw + 1
     const int qhw = wave & 1;
     const int dcw = wave >> 1;
 
-    int cb = 0;
-    for (int q0 = q_begin; q0 < q_end; q0 += BQ, cb ^= 1) {
-        gload_q(q0 + BQ, q0 + BQ < q_end ? p.Tq : 0);
+    // step of tile q0 in LDS buffer cb; register set LS holds tile q0 + BQ,
+    // the other set takes tile q0 + 2 BQ
+    auto step = [&](int q0, int cb, auto ls_c) {
+        constexpr int LS = decltype(ls_c)::value;
+        gload_q(std::integral_constant<int, 1 - LS>{}, q0 + 2 * BQ, q0 + 2 * BQ < q_end ? p.Tq : 0);
         __bf16(*Qs)[QS] = Qs2[cb];
         __bf16(*dOs)[QS] = dOs2[cb];
         __bf16(*dSs)[SS] = dSs2[cb];
@@ -852,11 +862,11 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
 #pragma unroll
             for (int r = 0; r < 8; ++r) dSs[16 * (r >> 2) + 4 * g4 + (r & 3)][wave * KW + l16] = dsb[r];
         }
-        sstore_q(cb ^ 1);
+        sstore_q(ls_c, cb ^ 1);
         __syncthreads();
 
         // ---- dQ (32 x D) += dS (32 x BK) K (BK x D): this wave's two 16x16 blocks
-        if (p.dq_direct) continue;
+        if (p.dq_direct) return;
         const auto rdq = row_rsrc(dQa, p.sacc.t, q0, min(p.Tq - q0, BQ), D);
         f32x4 acc0, acc1;
         bf16x8 a[BK / 32], b0[BK / 32], b1[BK / 32];
@@ -878,6 +888,10 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
             buffer_atomic_add(rdq, acc0[r] * p.scale, voff, (uint32_t)((int64_t)r * p.sacc.t * 4));
             buffer_atomic_add(rdq, acc1[r] * p.scale, voff + 64, (uint32_t)((int64_t)r * p.sacc.t * 4));
         }
+    };
+    for (int q0 = q_begin; q0 < q_end; q0 += 2 * BQ) {
+        step(q0, 0, R1{});
+        if (q0 + BQ < q_end) step(q0 + BQ, 1, R0{});
     }
 
     // split plans: the fix-up takes the accumulators as two f32x16 each
