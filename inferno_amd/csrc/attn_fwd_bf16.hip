@@ -118,33 +118,43 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     const int64_t kstep = (int64_t)BN * p.sk.t, vstep = (int64_t)BN * p.sv.t;
     const __bf16* kt = K + (int64_t)kb0 * p.sk.t;
     const __bf16* vt = V + (int64_t)kb0 * p.sv.t;
-    bf16x8 kr[KLPT], vr[KLPT];
+    // Two register sets (0 / 1, compile-time at every call): tile u + 2 is
+    // loaded while tile u + 1 waits in the other set to be stored at the end
+    // of step u, so a load that misses the L2 has a whole tile more to arrive.
+    bf16x8 kr[2][KLPT], vr[2][KLPT];
     const uint32_t k_voff = (uint32_t)(((int64_t)(tid / C8) * p.sk.t + 8 * (tid % C8)) * 2);
     const uint32_t v_voff = (uint32_t)(((int64_t)(tid / C8) * p.sv.t + 8 * (tid % C8)) * 2);
-    auto gload = [&](int rows) {
+    auto rows_of = [&](int t) { return t < nt ? min(klim - t * BN, BN) : 0; };
+    auto gload = [&](auto set_c, int rows) {  // the tile at kt / vt; the bases then advance one tile
+        constexpr int rs = decltype(set_c)::value;
         const auto rk = row_rsrc(kt, p.sk.t, 0, rows, D);
         const auto rv = row_rsrc(vt, p.sv.t, 0, rows, D);
 #pragma unroll
         for (int i = 0; i < KLPT; ++i)
-            kr[i] = buffer_ld8bf(rk, k_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sk.t * 2));
+            kr[rs][i] = buffer_ld8bf(rk, k_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sk.t * 2));
 #pragma unroll
         for (int i = 0; i < KLPT; ++i)
-            vr[i] = buffer_ld8bf(rv, v_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sv.t * 2));
+            vr[rs][i] = buffer_ld8bf(rv, v_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sv.t * 2));
+        kt += kstep;
+        vt += vstep;
     };
     // Chunk tid + 256 i lands in row tid / C8 + (256 / C8) i, column chunk
     // tid % C8: a per-thread LDS offset plus a constant per i (immediate
     // offsets of the stores, no address arithmetic per tile).
     const uint32_t ks_off = (uint32_t)(((tid / C8) * KS + 8 * (tid % C8)) * 2);
     const uint32_t vs_off = (uint32_t)(((tid / C8) * VS + 8 * (tid % C8)) * 2);
-    auto sstore = [&](int buf) {
+    auto sstore = [&](auto set_c, int buf) {
+        constexpr int rs = decltype(set_c)::value;
         char* kb = reinterpret_cast<char*>(&Ks[buf][0][0]) + ks_off;
         char* vb = reinterpret_cast<char*>(&Vs[buf][0][0]) + vs_off;
 #pragma unroll
         for (int i = 0; i < KLPT; ++i) {
-            *reinterpret_cast<bf16x8*>(kb + i * (256 / C8) * KS * 2) = kr[i];
-            *reinterpret_cast<bf16x8*>(vb + i * (256 / C8) * VS * 2) = vr[i];
+            *reinterpret_cast<bf16x8*>(kb + i * (256 / C8) * KS * 2) = kr[rs][i];
+            *reinterpret_cast<bf16x8*>(vb + i * (256 / C8) * VS * 2) = vr[rs][i];
         }
     };
+    using R0 = std::integral_constant<int, 0>;
+    using R1 = std::integral_constant<int, 1>;
 
     // transposed V reads: this lane's key-row offset and column offset
     const int tr_row = (lane & 15) >> 2;
@@ -157,18 +167,19 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     float l_run = 0.f;
     const float c = p.c;
 
-    gload(min(klim, BN));
-    sstore(0);
+    gload(R0{}, rows_of(0));
+    sstore(R0{}, 0);
+    gload(R1{}, rows_of(1));
     __syncthreads();
 
-    // The prefetch of tile u+1 and its store are straight-line (a row limit
-    // of 0 past the last tile: zeros into a buffer that is not read again).
-    for (int u = 0; u < nt; ++u) {
+    // The prefetch of tile u+2 and the store of tile u+1 are straight-line (a
+    // row limit of 0 past the last tile: zeros into a buffer that is not read
+    // again).  Step u: LDS buffer u % 2; register set LS holds tile u + 1.
+    auto step = [&](int u, auto ls_c) {
+        constexpr int LS = decltype(ls_c)::value;
         const int buf = u & 1;
         const int k0 = kb0 + u * BN;
-        kt += kstep;
-        vt += vstep;
-        gload(u + 1 < nt ? min(klim - (u + 1) * BN, BN) : 0);
+        gload(std::integral_constant<int, 1 - LS>{}, rows_of(u + 2));
 
         if (k0 < wave_kend) {
             f32x16 s[NKB];
@@ -255,8 +266,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
             if constexpr (kPvPrio) __builtin_amdgcn_s_setprio(0);
         }
 
-        sstore(buf ^ 1);
+        sstore(ls_c, buf ^ 1);
         __syncthreads();
+    };
+    for (int u = 0; u < nt; u += 2) {
+        step(u, R1{});
+        if (u + 1 < nt) step(u + 1, R0{});
     }
 
     const float l_tot = l_run + shfl_xor(l_run, 32);
