@@ -227,6 +227,12 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
     // tid + NT i sits NT i / C4 rows below chunk tid, and rows past the
     // resource read as zeros, so a load needs no address arithmetic or branch.
     constexpr bool PF = D <= 64;
+    // The LSE is staged in base 2 (scaled by log2(e) once per row instead of
+    // once per score) except at D = 64, which measured 2% slower that way at
+    // config 2; at D = 32 the staging keeps the kernel within the registers
+    // of three workgroups per CU (B4 H16 T1024: 134 -> 119 us).
+    constexpr float kLseStage = D == 64 ? 1.f : kLog2e;
+    constexpr float kLseRead = D == 64 ? kLog2e : 1.f;
     static_assert(NT % C4 == 0, "chunk rows must split into thread + load parts");
     static_assert(sizeof(E) == 4, "fp32 storage (bf16 has its own kernel)");
     f32x4 ra[QLPT], rd[QLPT];
@@ -259,7 +265,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
             *reinterpret_cast<f32x4*>(&dOs[f / C4][4 * (f % C4)]) = rd[i];
         }
         if (tid < BQ) {
-            lse_s[tid] = r_lse;  // natural-log LSE; scaled by log2(e) where it is read
+            lse_s[tid] = r_lse * kLseStage;
             dl_s[tid] = r_dl;
             if constexpr (SHORT) dlo_s[tid] = r_dlo;
         }
@@ -301,7 +307,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
                     dpt = mfma32x32x2(vf[i + 3], da[3], dpt);
                 }
                 const int qi = q0 + l32;
-                const float L = lse_s[l32] * kLog2e;
+                const float L = lse_s[l32] * kLseRead;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int kj = k0w + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -385,7 +391,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
             auto p_ds = [&](auto masked) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLog2e;
+                    const f32x4 L = *reinterpret_cast<const f32x4*>(&lse_s[8 * j + 4 * g]) * kLseRead;
                     const f32x4 Dl = *reinterpret_cast<const f32x4*>(&dl_s[8 * j + 4 * g]);
                     const f32x4 Dlo = SHORT ? *reinterpret_cast<const f32x4*>(&dlo_s[8 * j + 4 * g])
                                             : f32x4{0.f, 0.f, 0.f, 0.f};
