@@ -351,18 +351,23 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
     // variant, tighter on registers, measured 3% slower that way and issues
     // them at the top of the tile.
     constexpr bool EARLY = PF && !SHORT;
+    // Without PF (D = 128) a tile's loads go out in the previous tile's dQ
+    // section (ahead of its atomics, where fewer registers are live) and are
+    // stored at the top of the tile (B8 H12 T1024 686 -> 678 us, config 4
+    // 5972 -> 5937 us).
+    constexpr bool LATE_EARLY = !PF;
     if constexpr (PF) {
         gload_q(q_begin, p.Tq);
         sstore_q();
         __syncthreads();
         if constexpr (EARLY) gload_q(q_begin + BQ, q_begin + BQ < q_end ? p.Tq : 0);
     }
+    if constexpr (LATE_EARLY) gload_q(q_begin, p.Tq);
 
     for (int q0 = q_begin; q0 < q_end; q0 += BQ) {
         if constexpr (PF && !EARLY) {
             gload_q(q0 + BQ, q0 + BQ < q_end ? p.Tq : 0);
-        } else if constexpr (!PF) {
-            gload_q(q0, p.Tq);
+        } else if constexpr (LATE_EARLY) {
             sstore_q();
             __syncthreads();
         }
@@ -449,6 +454,7 @@ __global__ __launch_bounds__(64 * bwd_waves(0, D), (bwd_waves(0, D) == 8 || D >=
         __syncthreads();
         if constexpr (PF) sstore_q();  // the next tile (zeros after the last one, never read)
         if constexpr (EARLY) gload_q(q0 + 2 * BQ, q0 + 2 * BQ < q_end ? p.Tq : 0);
+        if constexpr (LATE_EARLY) gload_q(q0 + BQ, q0 + BQ < q_end ? p.Tq : 0);
         if (p.dq_direct) {
             __syncthreads();
             continue;
