@@ -38,8 +38,8 @@ HBM_PEAK_GBS = 8000.0
 # conversion pass, and its pre pass only zeroes the dQ accumulator (the bf16 main kernel forms
 # delta from O and dO itself).
 BWD_TRAFFIC = {
-    "f32": {"bwd_pre": 50.39e6 + 25.56e6, "bwd_main": 210.47e6 + 201.46e6},
-    "bf16": {"bwd_zero": 0.03e6 + 25.17e6, "bwd_main": 98.30e6 + 127.41e6, "bwd_cvt": 25.22e6 + 12.58e6},
+    "f32": {"bwd_pre": 50.39e6 + 25.56e6, "bwd_main": 200.84e6 + 201.37e6},
+    "bf16": {"bwd_zero": 0.03e6 + 25.17e6, "bwd_main": 83.94e6 + 107.60e6, "bwd_cvt": 25.20e6 + 12.58e6},
 }
 # where the figures above were measured (they are constants: re-measure after a kernel change)
 BWD_TRAFFIC_SOURCE = "profiles/attn_c2_hbm_traffic.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE of bench.py at config 2)"
