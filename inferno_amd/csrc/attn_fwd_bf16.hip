@@ -52,11 +52,15 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     constexpr int NKB = BN / 32;         // 32-key blocks per tile
     constexpr int NDB = D / 32;          // 32-wide head-dim blocks of O^T
     constexpr int C8 = D / 8;            // 8-element chunks per row
-    constexpr int KLPT = BN * C8 / 256;  // K chunks per thread per tile
-    static_assert(BN * C8 % 256 == 0, "K staging assumes whole passes");
 
-    __shared__ __attribute__((aligned(16))) __bf16 Ks[2][BN][KS];
-    __shared__ __attribute__((aligned(16))) __bf16 Vs[2][BN][VS];
+    // The two K / V buffers are distinct arrays, each step's named at compile
+    // time, so the compiler can tell the direct-to-LDS loads of one from the
+    // reads of the other (with one array indexed by the buffer number it waits
+    // for those loads before every tile's first LDS read).
+    __shared__ __attribute__((aligned(16))) __bf16 Ks0[BN][KS];
+    __shared__ __attribute__((aligned(16))) __bf16 Ks1[BN][KS];
+    __shared__ __attribute__((aligned(16))) __bf16 Vs0[BN][VS];
+    __shared__ __attribute__((aligned(16))) __bf16 Vs1[BN][VS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -106,55 +110,55 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     const int n_tiles = min((kv_end + BN - 1) / BN, t_end);
     const int wave_kend = p.causal ? min(kv_end, q0w + 32 + p.off) : kv_end;
 
-    // Tile u of the range (keys kb0 + u*BN ...) loads `rows` rows from the
-    // tile bases kt / vt through buffer resources: chunk tid + 256 i is chunk
-    // tid moved by a uniform offset (256 i / C8 rows for K, 8 i column chunks
-    // for V), and rows past `rows` read as zeros.  The bases advance by one
-    // tile per step (pointer increments, no per-step 64-bit products).
-    static_assert(256 % C8 == 0 && 256 % (BN / 2) == 0, "chunks must split into thread + load parts");
+    // Tile u of the range (keys kb0 + u*BN ...) goes from memory straight into
+    // LDS through gfx950's 16-byte direct-to-LDS buffer loads: the 64 lanes of
+    // one instruction fill 1 KiB at the instruction's LDS base, lane l at
+    // +16 l.  A tile's padded rows are one run of 16-byte slots (SK per K row,
+    // SV per V row, the last one or two of each row padding), so instruction j
+    // fills slots 64 j .. 64 j + 63, each lane loading the chunk of its slot (a
+    // pad slot loads its row's last chunk again; it is never read), and wave w
+    // issues instructions w, w + 4, ...  The buffer resources cover the tile's
+    // `rows` rows, so rows past them land as zeros, and the tile bases advance
+    // by one tile per load (pointer increments, no per-step 64-bit products).
+    constexpr int SK = KS / 8, SV = VS / 8;               // 16-byte slots per LDS row
+    constexpr int NJK = BN * SK / 64, NJV = BN * SV / 64;  // load instructions per tile
+    static_assert(BN * SK % 64 == 0 && BN * SV % 64 == 0, "a tile must fill whole instructions");
+    constexpr int NI = ((NJK > NJV ? NJK : NJV) + 3) / 4;  // per wave
     const int kb0 = t_begin * BN;
     const int nt = n_tiles - t_begin;  // tiles in this workgroup's range
     const int klim = p.Tk - kb0;       // keys of the range that exist
     const int64_t kstep = (int64_t)BN * p.sk.t, vstep = (int64_t)BN * p.sv.t;
     const __bf16* kt = K + (int64_t)kb0 * p.sk.t;
     const __bf16* vt = V + (int64_t)kb0 * p.sv.t;
-    // Two register sets (0 / 1, compile-time at every call): tile u + 2 is
-    // loaded while tile u + 1 waits in the other set to be stored at the end
-    // of step u, so a load that misses the L2 has a whole tile more to arrive.
-    bf16x8 kr[2][KLPT], vr[2][KLPT];
-    const uint32_t k_voff = (uint32_t)(((int64_t)(tid / C8) * p.sk.t + 8 * (tid % C8)) * 2);
-    const uint32_t v_voff = (uint32_t)(((int64_t)(tid / C8) * p.sv.t + 8 * (tid % C8)) * 2);
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    // Every wave issues NI instructions of each kind: one past a tile's last
+    // instruction repeats that one (the same bytes into the same slots), so no
+    // load sits behind a branch.
+    uint32_t k_voff[NI], v_voff[NI];  // this lane's byte offsets from the tile base
+    int k_lds[NI], v_lds[NI];         // the instructions' LDS offsets (wave-uniform)
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int jk = min(wave_u + 4 * i, NJK - 1), jv = min(wave_u + 4 * i, NJV - 1);
+        const int sk = 64 * jk + lane, sv = 64 * jv + lane;
+        k_voff[i] = (uint32_t)(((int64_t)(sk / SK) * p.sk.t + 8 * min(sk % SK, C8 - 1)) * 2);
+        v_voff[i] = (uint32_t)(((int64_t)(sv / SV) * p.sv.t + 8 * min(sv % SV, C8 - 1)) * 2);
+        k_lds[i] = 1024 * jk;
+        v_lds[i] = 1024 * jv;
+    }
     auto rows_of = [&](int t) { return t < nt ? min(klim - t * BN, BN) : 0; };
-    auto gload = [&](auto set_c, int rows) {  // the tile at kt / vt; the bases then advance one tile
-        constexpr int rs = decltype(set_c)::value;
+    auto dload = [&](__bf16 (&Kd)[BN][KS], __bf16 (&Vd)[BN][VS], int rows) {
         const auto rk = row_rsrc(kt, p.sk.t, 0, rows, D);
         const auto rv = row_rsrc(vt, p.sv.t, 0, rows, D);
 #pragma unroll
-        for (int i = 0; i < KLPT; ++i)
-            kr[rs][i] = buffer_ld8bf(rk, k_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sk.t * 2));
-#pragma unroll
-        for (int i = 0; i < KLPT; ++i)
-            vr[rs][i] = buffer_ld8bf(rv, v_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sv.t * 2));
+        for (int i = 0; i < NI; ++i) {
+            buffer_ld16_lds(rk, reinterpret_cast<char*>(&Kd[0][0]) + k_lds[i], k_voff[i]);
+            buffer_ld16_lds(rv, reinterpret_cast<char*>(&Vd[0][0]) + v_lds[i], v_voff[i]);
+        }
         kt += kstep;
         vt += vstep;
     };
-    // Chunk tid + 256 i lands in row tid / C8 + (256 / C8) i, column chunk
-    // tid % C8: a per-thread LDS offset plus a constant per i (immediate
-    // offsets of the stores, no address arithmetic per tile).
-    const uint32_t ks_off = (uint32_t)(((tid / C8) * KS + 8 * (tid % C8)) * 2);
-    const uint32_t vs_off = (uint32_t)(((tid / C8) * VS + 8 * (tid % C8)) * 2);
-    auto sstore = [&](auto set_c, int buf) {
-        constexpr int rs = decltype(set_c)::value;
-        char* kb = reinterpret_cast<char*>(&Ks[buf][0][0]) + ks_off;
-        char* vb = reinterpret_cast<char*>(&Vs[buf][0][0]) + vs_off;
-#pragma unroll
-        for (int i = 0; i < KLPT; ++i) {
-            *reinterpret_cast<bf16x8*>(kb + i * (256 / C8) * KS * 2) = kr[rs][i];
-            *reinterpret_cast<bf16x8*>(vb + i * (256 / C8) * VS * 2) = vr[rs][i];
-        }
-    };
-    using R0 = std::integral_constant<int, 0>;
-    using R1 = std::integral_constant<int, 1>;
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
 
     // transposed V reads: this lane's key-row offset and column offset
     const int tr_row = (lane & 15) >> 2;
@@ -167,19 +171,19 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     float l_run = 0.f;
     const float c = p.c;
 
-    gload(R0{}, rows_of(0));
-    sstore(R0{}, 0);
-    gload(R1{}, rows_of(1));
+    dload(Ks0, Vs0, rows_of(0));
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have landed in LDS
     __syncthreads();
 
-    // The prefetch of tile u+2 and the store of tile u+1 are straight-line (a
-    // row limit of 0 past the last tile: zeros into a buffer that is not read
-    // again).  Step u: LDS buffer u % 2; register set LS holds tile u + 1.
-    auto step = [&](int u, auto ls_c) {
-        constexpr int LS = decltype(ls_c)::value;
-        const int buf = u & 1;
+    // Step u reads buffer BUF (u % 2) while tile u + 1 loads into the other
+    // one, which every wave finished reading before the previous step's
+    // barrier; the step ends by waiting for its loads, then the barrier.
+    auto step = [&](int u, auto buf_c) {
+        constexpr int BUF = decltype(buf_c)::value;
+        __bf16(&Kc)[BN][KS] = BUF ? Ks1 : Ks0;
+        __bf16(&Vc)[BN][VS] = BUF ? Vs1 : Vs0;
         const int k0 = kb0 + u * BN;
-        gload(std::integral_constant<int, 1 - LS>{}, rows_of(u + 2));
+        dload(BUF ? Ks0 : Ks1, BUF ? Vs0 : Vs1, rows_of(u + 1));
 
         if (k0 < wave_kend) {
             f32x16 s[NKB];
@@ -187,7 +191,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
             for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb) {
-                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Ks[buf][kb * 32 + l32][16 * kk + 8 * g]);
+                    const bf16x8 a = *reinterpret_cast<const bf16x8*>(&Kc[kb * 32 + l32][16 * kk + 8 * g]);
                     s[kb] = mfma32x32x16bf16(a, qf[kk], kk == 0 ? f32x16{} : s[kb]);
                 }
 
@@ -256,7 +260,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
                         // lane (group G = lane / 16, i = lane % 16) addresses key row
                         // key + i / 4, columns db*32 + 16 (G % 2) + 4 (i % 4); it receives
                         // column db*32 + l32 of keys key + {0..3} (then + 8 + {0..3})
-                        const __bf16* vp = &Vs[buf][key + tr_row][db * 32 + tr_col];
+                        const __bf16* vp = &Vc[key + tr_row][db * 32 + tr_col];
                         const bf16x4 lo = ds_read_tr16(vp);
                         const bf16x4 hi = ds_read_tr16(vp + 8 * VS);
                         const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -266,12 +270,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
             if constexpr (kPvPrio) __builtin_amdgcn_s_setprio(0);
         }
 
-        sstore(ls_c, buf ^ 1);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     };
     for (int u = 0; u < nt; u += 2) {
-        step(u, R1{});
-        if (u + 1 < nt) step(u + 1, R0{});
+        step(u, B0{});
+        if (u + 1 < nt) step(u + 1, B1{});
     }
 
     const float l_tot = l_run + shfl_xor(l_run, 32);

@@ -155,6 +155,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const __bf16* base, i
 __device__ __forceinline__ bf16x8 buffer_ld8bf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
+// gfx950's 16-byte direct-to-LDS buffer load: 16 bytes at byte offset voff
+// (per lane) of the resource land in LDS at `lds` (wave-uniform) + 16 * lane,
+// without passing through VGPRs; the wave's memory counter covers them.
+__device__ __forceinline__ void buffer_ld16_lds(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
 // gfx950's ds_read_b64_tr_b16 at an LDS address (8-byte aligned): in each
 // group of 16 lanes, output lane i, element k is element i % 4 of the 8 bytes
 // that lane 4 k + i / 4 addresses.  With the 16 lanes addressing 4 rows x 4
