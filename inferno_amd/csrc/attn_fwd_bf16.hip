@@ -2,7 +2,8 @@
 // accumulation, on v_mfma_f32_32x32x16_bf16 (gfx950).
 //
 // Same structure as the fp32 kernel (attn_fwd.hip): 4 waves x 32 query rows,
-// K/V tiles of 64 keys double-buffered through LDS, S^T = K Q^T and
+// K/V tiles of 64 keys double-buffered through LDS (loaded straight into LDS
+// by direct-to-LDS buffer loads, one tile ahead), S^T = K Q^T and
 // O^T += V^T P^T with queries on the lane axis, online softmax in fp32, and
 // the same split plan (fwd_plan: a chunk of a long query tile's key range
 // leaves fp32 partials that attn_fwd_merge_kernel combines into bf16 O).
