@@ -930,36 +930,55 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
 // ---- query-major dQ pass (bf16, long key ranges) ---------------------------
 //
 // 4 waves x 32 query rows per workgroup (heaviest query tiles first), key
-// tiles of BN keys streamed through LDS as K rows, V rows and K^T (keys of each
-// 32-key block in the MFMA operand order 16m + 8g + 4h + c for key
-// 16m + 8h + 4g + c); Q and dO rows of the wave's queries in VGPRs, LSE and
-// delta one value per lane.  Per tile, with queries on the lane axis:
+// tiles of BN keys streamed through LDS as K rows and V rows; Q and dO rows of
+// the wave's queries in VGPRs, LSE and delta one value per lane.  Per tile,
+// with queries on the lane axis:
 //   S^T = K Q^T, dP^T = V dO^T, P^T = exp2(S^T c - L), dS^T = P^T (dP^T - delta)
-//   dQ^T += K^T dS^T (dS^T straight from registers, as the forward's P^T)
+//   dQ^T += K^T dS^T (dS^T straight from registers, as the forward's P^T, and
+//                     K^T read from the K rows by transpose reads, as the
+//                     forward's V^T)
 // dQ accumulates in fp32 VGPRs and is written once (bf16, times the scale):
 // no accumulator, no atomics, no conversion pass, and the same sum order on
 // every run.  It recomputes S and dP (two more products per score than the
 // atomic path's dQ), so it pays only where the atomics bound the fused
 // kernel (bwd_dq_direct): at D = 128 with many key blocks.  (At D = 64 it
 // measured 28% slower than the atomics at B1 H16 T8192.)
+//
+// The K row stride serves both reads of K without bank conflicts: 16-byte
+// row reads (lane l32 at row l32, 16 g bytes in) need an odd number of
+// 16-byte units, and the transpose reads (4 rows x 32 bytes per 16 lanes)
+// need the rows' 32-byte windows disjoint modulo 256 bytes: 304 B at D = 128,
+// 144 B at D = 64, 112 B at D = 32.
+template <int D>
+struct DqBf16Tile {
+    static constexpr int BN = D >= 128 ? 32 : 64;
+    static constexpr int KS = D == 128 ? D + 24 : D == 64 ? D + 8 : D + 24;  // K row stride (bf16)
+    static constexpr int VS = D + 8;                                         // V row stride (bf16)
+    static constexpr int SK = KS / 8, SV = VS / 8;                           // 16-byte slots per row
+    static constexpr int NJK = (BN * SK + 63) / 64, NJV = (BN * SV + 63) / 64;  // load instructions
+    // rows allocated: the last instruction's slots past the tile land in spare rows
+    static constexpr int KROWS = (NJK * 1024 + 2 * KS - 1) / (2 * KS);
+    static constexpr int VROWS = (NJV * 1024 + 2 * VS - 1) / (2 * VS);
+};
+
 template <int D>
 __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
+    using T = DqBf16Tile<D>;
     constexpr int BM = kBwdDqBM;
-    constexpr int BN = D >= 128 ? 32 : 64;
-    constexpr int KS = D + 8;            // K / V row stride (bf16)
-    constexpr int TS = BN + 8;           // K^T row stride (bf16)
+    constexpr int BN = T::BN, KS = T::KS, VS = T::VS, SK = T::SK, SV = T::SV;
+    constexpr int NJK = T::NJK, NJV = T::NJV;
     constexpr int NKK = D / 16;
     constexpr int NKB = BN / 32;
     constexpr int NDB = D / 32;
     constexpr int C8 = D / 8;
-    constexpr int KTASK = (BN / 2) * C8;  // (key pair, chunk) tasks: 128 at D = 32, else 256
-    constexpr int KLPT = (KTASK + 255) / 256;
-    constexpr int VLPT = BN * C8 / 256;
-    static_assert(BN * C8 % 256 == 0 && (KTASK % 256 == 0 || KTASK == 128), "whole staging passes");
+    constexpr int NI = ((NJK > NJV ? NJK : NJV) + 3) / 4;  // load instructions per wave and kind
 
-    __shared__ __attribute__((aligned(16))) __bf16 Ks[2][BN][KS];
-    __shared__ __attribute__((aligned(16))) __bf16 Vs[2][BN][KS];
-    __shared__ __attribute__((aligned(16))) __bf16 KTs[2][D][TS];
+    // Two buffers as separate arrays, each step's named at compile time, so
+    // the compiler can tell the loads into one from the reads of the other.
+    __shared__ __attribute__((aligned(16))) __bf16 Ks0[T::KROWS][KS];
+    __shared__ __attribute__((aligned(16))) __bf16 Ks1[T::KROWS][KS];
+    __shared__ __attribute__((aligned(16))) __bf16 Vs0[T::VROWS][VS];
+    __shared__ __attribute__((aligned(16))) __bf16 Vs1[T::VROWS][VS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1001,69 +1020,70 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
     const int nt = (kv_end + BN - 1) / BN;
     const int wave_kend = p.causal ? min(kv_end, q0w + 32 + p.off) : kv_end;
 
+    // Key tile u goes from memory straight into LDS through gfx950's 16-byte
+    // direct-to-LDS buffer loads: the 64 lanes of one instruction fill 1 KiB
+    // at the instruction's LDS base, lane l at +16 l, so a tile's padded rows
+    // are one run of 16-byte slots and instruction j fills slots 64 j ..
+    // 64 j + 63, each lane loading the chunk of its slot (a pad slot repeats
+    // its row's last chunk; slots past the tile, in the spare rows, read
+    // outside the resource: zeros).  Wave w issues instructions w, w + 4, ...,
+    // and one past the last repeats the last (the same bytes into the same
+    // slots), so no load is behind a branch.  The resources cover the tile's
+    // rows, so keys past Tk land as zeros.
     const int64_t kstep = (int64_t)BN * p.sk.t, vstep = (int64_t)BN * p.sv.t;
     const __bf16* kt = K;
     const __bf16* vt = V;
-    bf16x8 ka[KLPT], kb2[KLPT], vr[VLPT];
-    const int kp = tid % (BN / 2), kc8 = tid / (BN / 2);
-    const bool k_task = tid < KTASK;  // D = 32: threads 128..255 stage no K
-    const uint32_t k_voff = (uint32_t)(((int64_t)(2 * kp) * p.sk.t + 8 * kc8) * 2);
-    const uint32_t v_voff = (uint32_t)(((int64_t)(tid / C8) * p.sv.t + 8 * (tid % C8)) * 2);
-    auto gload = [&](int rows) {
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t k_voff[NI], v_voff[NI];
+    int k_lds[NI], v_lds[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int jk = min(wave_u + 4 * i, NJK - 1), jv = min(wave_u + 4 * i, NJV - 1);
+        const int sk = 64 * jk + lane, sv = 64 * jv + lane;
+        k_voff[i] = sk < BN * SK ? (uint32_t)(((int64_t)(sk / SK) * p.sk.t + 8 * min(sk % SK, C8 - 1)) * 2)
+                                 : 0x80000000u;
+        v_voff[i] = sv < BN * SV ? (uint32_t)(((int64_t)(sv / SV) * p.sv.t + 8 * min(sv % SV, C8 - 1)) * 2)
+                                 : 0x80000000u;
+        k_lds[i] = 1024 * jk;
+        v_lds[i] = 1024 * jv;
+    }
+    auto rows_of = [&](int u) { return u < nt ? min(p.Tk - u * BN, BN) : 0; };
+    auto dload = [&](__bf16 (&Kd)[T::KROWS][KS], __bf16 (&Vd)[T::VROWS][VS], int rows) {
         const auto rk = row_rsrc(kt, p.sk.t, 0, rows, D);
         const auto rv = row_rsrc(vt, p.sv.t, 0, rows, D);
 #pragma unroll
-        for (int i = 0; i < KLPT; ++i) {
-            const uint32_t col = (uint32_t)(8 * (256 * i / (BN / 2)) * 2);
-            ka[i] = kb2[i] = bf16x8{};
-            if (!k_task) continue;
-            ka[i] = buffer_ld8bf(rk, k_voff, col);
-            kb2[i] = buffer_ld8bf(rk, k_voff, col + (uint32_t)(p.sk.t * 2));
+        for (int i = 0; i < NI; ++i) {
+            buffer_ld16_lds(rk, reinterpret_cast<char*>(&Kd[0][0]) + k_lds[i], k_voff[i]);
+            buffer_ld16_lds(rv, reinterpret_cast<char*>(&Vd[0][0]) + v_lds[i], v_voff[i]);
         }
-#pragma unroll
-        for (int i = 0; i < VLPT; ++i)
-            vr[i] = buffer_ld8bf(rv, v_voff, (uint32_t)((int64_t)(256 * i / C8) * p.sv.t * 2));
+        kt += kstep;
+        vt += vstep;
     };
-    const uint32_t vs_off = (uint32_t)(((tid / C8) * KS + 8 * (tid % C8)) * 2);
-    auto sstore = [&](int buf) {
-        const int k = 2 * kp;
-        const int pos = (k & ~15) | ((k & 4) << 1) | ((k & 8) >> 1) | (k & 3);
-#pragma unroll
-        for (int i = 0; i < KLPT; ++i) {
-            if (!k_task) continue;
-            const int c8 = kc8 + 256 * i / (BN / 2);
-            *reinterpret_cast<bf16x8*>(&Ks[buf][k][8 * c8]) = ka[i];
-            *reinterpret_cast<bf16x8*>(&Ks[buf][k + 1][8 * c8]) = kb2[i];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                bf16x2 pr;
-                pr[0] = ka[i][e];
-                pr[1] = kb2[i][e];
-                *reinterpret_cast<bf16x2*>(&KTs[buf][8 * c8 + e][pos]) = pr;
-            }
-        }
-        // V chunk tid + 256 i: row tid / C8 + (256 / C8) i, column chunk tid % C8
-        // (a per-thread offset plus a constant: immediate store offsets)
-        char* vb = reinterpret_cast<char*>(&Vs[buf][0][0]) + vs_off;
-#pragma unroll
-        for (int i = 0; i < VLPT; ++i) *reinterpret_cast<bf16x8*>(vb + i * (256 / C8) * KS * 2) = vr[i];
-    };
-    auto rows_of = [&](int u) { return u < nt ? min(p.Tk - u * BN, BN) : 0; };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+
+    // transposed K reads: this lane's key-row offset and column offset
+    const int tr_row = (lane & 15) >> 2;
+    const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     f32x16 dq[NDB];
 #pragma unroll
     for (int i = 0; i < NDB; ++i) dq[i] = f32x16{};
     const float c = p.c;
 
-    gload(rows_of(0));
-    sstore(0);
+    dload(Ks0, Vs0, rows_of(0));
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have landed in LDS
     __syncthreads();
-    for (int u = 0; u < nt; ++u) {
-        const int buf = u & 1;
+
+    // Step u reads buffer u % 2 while tile u + 1 loads into the other one,
+    // which every wave finished reading before the previous step's barrier;
+    // the step ends by waiting for its loads, then the barrier.
+    auto step = [&](int u, auto buf_c) {
+        constexpr int BUF = decltype(buf_c)::value;
+        __bf16(&Kc)[T::KROWS][KS] = BUF ? Ks1 : Ks0;
+        __bf16(&Vc)[T::VROWS][VS] = BUF ? Vs1 : Vs0;
         const int k0 = u * BN;
-        kt += kstep;
-        vt += vstep;
-        gload(rows_of(u + 1));
+        dload(BUF ? Ks0 : Ks1, BUF ? Vs0 : Vs1, rows_of(u + 1));
         if (k0 < wave_kend) {
             f32x16 s[NKB], dp[NKB];
             bf16x8 ak[NKK][NKB], av[NKK][NKB];
@@ -1071,8 +1091,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
             for (int kk = 0; kk < NKK; ++kk)
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb) {
-                    ak[kk][kb] = *reinterpret_cast<const bf16x8*>(&Ks[buf][kb * 32 + l32][16 * kk + 8 * g]);
-                    av[kk][kb] = *reinterpret_cast<const bf16x8*>(&Vs[buf][kb * 32 + l32][16 * kk + 8 * g]);
+                    ak[kk][kb] = *reinterpret_cast<const bf16x8*>(&Kc[kb * 32 + l32][16 * kk + 8 * g]);
+                    av[kk][kb] = *reinterpret_cast<const bf16x8*>(&Vc[kb * 32 + l32][16 * kk + 8 * g]);
                 }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1109,15 +1129,23 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
                 for (int kb = 0; kb < NKB; ++kb)
                     if (one_key) dsb[kb][0] = dsb[kb][1] = bf16x8{};
             }
-            // dQ^T[d][q] += K^T[d][keys] dS^T[keys][q]
+            // dQ^T[d][q] += K^T[d][keys] dS^T[keys][q]: MFMA m of key block kb takes
+            // dS^T of keys 16 m + 4 g + {0..3} and 16 m + 8 + 4 g + {0..3}; lane
+            // (group G = lane / 16, i = lane % 16) addresses key row key + i / 4,
+            // columns db*32 + 16 (G % 2) + 4 (i % 4) and receives column
+            // db*32 + l32 of keys key + {0..3} (then + 8 + {0..3})
             bf16x8 akt[NDB][NKB][2];
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-                    for (int m = 0; m < 2; ++m)
-                        akt[db][kb][m] = *reinterpret_cast<const bf16x8*>(&KTs[buf][db * 32 + l32][kb * 32 + 16 * m + 8 * g]);
+                    for (int m = 0; m < 2; ++m) {
+                        const __bf16* kp = &Kc[kb * 32 + 16 * m + 4 * g + tr_row][db * 32 + tr_col];
+                        const bf16x4 lo = ds_read_tr16(kp);
+                        const bf16x4 hi = ds_read_tr16(kp + 8 * KS);
+                        akt[db][kb][m] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                    }
             __builtin_amdgcn_sched_barrier(0);
             // At D = 128 the dQ MFMAs run at raised wave priority (issued ahead of the
             // other wave's softmax VALU work): config 4 455 -> 439 us, B8 H12 T1024
@@ -1131,8 +1159,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_bf16_kernel(BwdParams p) {
                     for (int db = 0; db < NDB; ++db) dq[db] = mfma32x32x16bf16(akt[db][kb][m], dsb[kb][m], dq[db]);
             if constexpr (D >= 128) __builtin_amdgcn_s_setprio(0);
         }
-        sstore(buf ^ 1);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+    };
+    for (int u = 0; u < nt; u += 2) {
+        step(u, B0{});
+        if (u + 1 < nt) step(u + 1, B1{});
     }
     if (qrow < p.Tq) {
         uint16_t* dst = (uint16_t*)p.dq + b * p.sdq.b + h * p.sdq.h + (int64_t)qrow * p.sdq.t;
