@@ -597,7 +597,13 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
 //                            with the queries in that order (16-byte reads)
 //   dQ += dS K               dS through LDS (keys contiguous), K^T staged once;
 //                            each wave one 16-query half x two 16-wide d blocks
-template <int D, bool SHORT>
+//
+// DQD: the launch has the query-major dQ pass (p.dq_direct), so no dQ product
+// here; then Q / dO tiles go straight into LDS (direct-to-LDS buffer loads,
+// one tile ahead, each step waiting for them before its barrier), where the
+// atomics of the dQ product would otherwise sit in the same in-order memory
+// counter as those loads.
+template <int D, bool SHORT, bool DQD>
 __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) {
     static_assert(D == 128, "16-key waves are the D = 128 kernel");
     constexpr int NW = 8;
@@ -732,6 +738,46 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     };
     using R0 = std::integral_constant<int, 0>;
     using R1 = std::integral_constant<int, 1>;
+    // DQD: LSE / delta alone through registers (two tiles ahead), and Q / dO
+    // by direct-to-LDS loads: a tile of one tensor is 32 rows of QS / 8 16-byte
+    // slots (the last two of each row padding) = NJQ one-KiB instructions,
+    // waves 0-3 loading Q and 4-7 dO, wave w's share being instructions
+    // w % 4, w % 4 + 4, ... (one past the last repeats the last: the same
+    // bytes into the same slots, no load behind a branch).
+    auto gload_l = [&](auto rs_c, int q0, int lim) {
+        constexpr int rs = decltype(rs_c)::value;
+        const int rows = min(lim - q0, BQ);
+        r_lse[rs] = buffer_ld1(row_rsrc(LSE, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
+        r_dl[rs] = buffer_ld1(row_rsrc(DL, 1, q0, rows, 1), (uint32_t)tid * 4, 0);
+    };
+    auto sstore_l = [&](auto rs_c, int sb) {
+        constexpr int rs = decltype(rs_c)::value;
+        if (tid < BQ) {
+            lse_s2[sb][tid] = r_lse[rs] * kLog2e;  // LSE in base 2
+            dl_s2[sb][tid] = r_dl[rs];
+        }
+    };
+    constexpr int SQ = QS / 8;
+    constexpr int NJQ = BQ * SQ / 64;
+    static_assert(BQ * SQ % 64 == 0, "a tile must fill whole instructions");
+    constexpr int NIQ = (NJQ + 3) / 4;
+    const int64_t st_q = which ? p.sdo.t : p.sq.t;
+    uint32_t q_voff[NIQ];
+    int q_lds[NIQ];
+#pragma unroll
+    for (int i = 0; i < NIQ; ++i) {
+        const int j = min(((tid >> 6) & 3) + 4 * i, NJQ - 1);
+        const int slot = 64 * j + lane;
+        q_voff[i] = (uint32_t)(((int64_t)(slot / SQ) * st_q + 8 * min(slot % SQ, C8 - 1)) * 2);
+        q_lds[i] = 1024 * j;
+    }
+    auto dload_q = [&](int sb, int q0, int lim) {
+        const int rows = min(lim - q0, BQ);
+        const auto rsrc = row_rsrc(which ? dO : Q, st_q, q0, rows, D);
+        char* base = which ? reinterpret_cast<char*>(&dOs2[sb][0][0]) : reinterpret_cast<char*>(&Qs2[sb][0][0]);
+#pragma unroll
+        for (int i = 0; i < NIQ; ++i) buffer_ld16_lds(rsrc, base + q_lds[i], q_voff[i]);
+    };
 
     // Short rows (bwd_split.h): their delta before the main loop.
     const int qs_end = SHORT && kblk == 0 ? min(q_end, p.n_short) : q_begin;  // short rows: [q_begin, qs_end)
@@ -742,6 +788,7 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     // K^T of the key block (keys contiguous per d row), for dQ.
 #pragma unroll
     for (int i = 0; i < KLPT; ++i) {
+        if constexpr (DQD) break;
         const int f = tid + NT * i;
         if (f >= KTASK) continue;
         const int kp = f % (BK / 2), c8 = f / (BK / 2);
@@ -760,9 +807,18 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
 
     // Q / dO tiles are loaded two tiles ahead (two register sets), stored one
     // tile ahead: a load that misses the L2 has a whole tile more to arrive.
-    gload_q(R0{}, q_begin, p.Tq);
-    sstore_q(R0{}, 0);
-    gload_q(R1{}, q_begin + BQ, q_begin + BQ < q_end ? p.Tq : 0);
+    // (DQD: Q / dO straight into LDS one tile ahead, LSE / delta as above.)
+    if constexpr (DQD) {
+        dload_q(0, q_begin, p.Tq);
+        gload_l(R0{}, q_begin, p.Tq);
+        sstore_l(R0{}, 0);
+        gload_l(R1{}, q_begin + BQ, q_begin + BQ < q_end ? p.Tq : 0);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have landed in LDS
+    } else {
+        gload_q(R0{}, q_begin, p.Tq);
+        sstore_q(R0{}, 0);
+        gload_q(R1{}, q_begin + BQ, q_begin + BQ < q_end ? p.Tq : 0);
+    }
     __syncthreads();
 
     // dQ blocks of this wave: query half qhw, d blocks 2 dcw and 2 dcw + 1
@@ -773,7 +829,12 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
     // the other set takes tile q0 + 2 BQ
     auto step = [&](int q0, int cb, auto ls_c) {
         constexpr int LS = decltype(ls_c)::value;
-        gload_q(std::integral_constant<int, 1 - LS>{}, q0 + 2 * BQ, q0 + 2 * BQ < q_end ? p.Tq : 0);
+        if constexpr (DQD) {
+            gload_l(std::integral_constant<int, 1 - LS>{}, q0 + 2 * BQ, q0 + 2 * BQ < q_end ? p.Tq : 0);
+            if (q0 + BQ < q_end) dload_q(cb ^ 1, q0 + BQ, p.Tq);
+        } else {
+            gload_q(std::integral_constant<int, 1 - LS>{}, q0 + 2 * BQ, q0 + 2 * BQ < q_end ? p.Tq : 0);
+        }
         __bf16(*Qs)[QS] = Qs2[cb];
         __bf16(*dOs)[QS] = dOs2[cb];
         __bf16(*dSs)[SS] = dSs2[cb];
@@ -857,16 +918,20 @@ __global__ __launch_bounds__(512, 1) void bwd_main_bf16_w16_kernel(BwdParams p) 
         } else {
             pb = dsb = bf16x8{};
         }
-        // dS of this wave -> LDS (rows = queries, columns = the block's keys)
-        if (!p.dq_direct) {
+        if constexpr (DQD) {
+            sstore_l(ls_c, cb ^ 1);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's Q / dO loads have landed in LDS
+            __syncthreads();
+            return;
+        } else {
+            // dS of this wave -> LDS (rows = queries, columns = the block's keys)
 #pragma unroll
             for (int r = 0; r < 8; ++r) dSs[16 * (r >> 2) + 4 * g4 + (r & 3)][wave * KW + l16] = dsb[r];
+            sstore_q(ls_c, cb ^ 1);
+            __syncthreads();
         }
-        sstore_q(ls_c, cb ^ 1);
-        __syncthreads();
 
         // ---- dQ (32 x D) += dS (32 x BK) K (BK x D): this wave's two 16x16 blocks
-        if (p.dq_direct) return;
         const auto rdq = row_rsrc(dQa, p.sacc.t, q0, min(p.Tq - q0, BQ), D);
         f32x4 acc0, acc1;
         bf16x8 a[BK / 32], b0[BK / 32], b1[BK / 32];
@@ -1195,7 +1260,7 @@ int bwd_main_bf16_occupancy(int D, int* blocks_per_cu) {
     switch (D) {
         case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<32, false, false>, 64 * bwd_bf16_waves(32), 0);
         case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_kernel<64, false, false>, 64 * bwd_bf16_waves(64), 0);
-        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_w16_kernel<128, false>, 512, 0);
+        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, bwd_main_bf16_w16_kernel<128, false, false>, 512, 0);
         default: return (int)hipErrorInvalidValue;
     }
 }
@@ -1216,8 +1281,13 @@ int launch_bwd_main_bf16(const BwdParams& p, hipStream_t s) {
             else hipLaunchKernelGGL((bwd_main_bf16_kernel<64, false, false>), grid, dim3(64 * bwd_bf16_waves(64)), 0, s, p);
             break;
         case 128:
-            if (p.n_short > 0) hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128, true>), grid, dim3(512), 0, s, p);
-            else hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128, false>), grid, dim3(512), 0, s, p);
+            if (p.dq_direct) {
+                if (p.n_short > 0) hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128, true, true>), grid, dim3(512), 0, s, p);
+                else hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128, false, true>), grid, dim3(512), 0, s, p);
+            } else {
+                if (p.n_short > 0) hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128, true, false>), grid, dim3(512), 0, s, p);
+                else hipLaunchKernelGGL((bwd_main_bf16_w16_kernel<128, false, false>), grid, dim3(512), 0, s, p);
+            }
             break;
         default: return (int)hipErrorInvalidValue;
     }
