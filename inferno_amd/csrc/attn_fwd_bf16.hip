@@ -261,9 +261,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
                         // lane (group G = lane / 16, i = lane % 16) addresses key row
                         // key + i / 4, columns db*32 + 16 (G % 2) + 4 (i % 4); it receives
                         // column db*32 + l32 of keys key + {0..3} (then + 8 + {0..3})
-                        const __bf16* vp = &Vc[key + tr_row][db * 32 + tr_col];
-                        const bf16x4 lo = ds_read_tr16(vp);
-                        const bf16x4 hi = ds_read_tr16(vp + 8 * VS);
+                        const bf16x4 lo = ds_read_tr16(&Vc[key + tr_row][db * 32 + tr_col]);
+                        const bf16x4 hi = ds_read_tr16(&Vc[key + 8 + tr_row][db * 32 + tr_col]);
                         const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                         o[db] = mfma32x32x16bf16(a, pb[kb][mm], o[db]);
                     }
