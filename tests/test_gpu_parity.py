@@ -447,9 +447,10 @@ def test_bf16_rows_8_byte_aligned(ia, D, T):
 def test_bf16_all_rows_8_byte_aligned(ia, mode, D, T):
     """Every bf16 operand and output of the backward (q, k, v, o, dO, dq, dk, dv) at a 4-element
     offset in its buffer, so each row starts 8 but not 16 bytes past a 16-byte boundary: the
-    kernels' 16-byte loads of K / V into registers, of K for the K^T staging, and of Q / dO in
-    the query-major dQ pass (the deterministic mode, every D; the bf16 D = 128 main kernel) read
-    such rows.  dK and dV, and in the deterministic mode dQ, are bit-identical to those of the
+    kernels' 16-byte loads of K / V into registers, of K for the K^T staging, of Q / dO in the
+    query-major dQ pass, and the direct-to-LDS loads of the forward's K / V, the dQ pass's K / V
+    and the D = 128 main kernel's Q / dO where the dQ pass runs (the deterministic mode, every
+    D) read such rows.  dK and dV, and in the deterministic mode dQ, are bit-identical to those of the
     same inputs in 16-byte-aligned buffers; the default mode's dQ (an fp32 atomic sum) is
     within one bf16 rounding step; all against the oracle."""
     print(f"[case] bf16 8-byte aligned all operands {mode} D{D} T{T}", flush=True)
