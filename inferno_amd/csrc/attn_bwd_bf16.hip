@@ -580,7 +580,7 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
 }
 
 // D = 128: 8 waves x 16 keys (128 keys per workgroup) on v_mfma_f32_16x16x32_bf16,
-// two waves per SIMD (216 VGPRs).  (32 keys per wave on 32x32 MFMAs needs
+// two waves per SIMD (244 VGPRs; 216 in the DQD instantiation).  (32 keys per wave on 32x32 MFMAs needs
 // ~470 registers per wave at D = 128: one wave per SIMD; against that layout
 // this one measured 11-28% faster at T <= 2048 and 2% at config 4, whose
 // 64 key blocks per head make the dQ atomics the limit: 39% faster there
@@ -593,8 +593,9 @@ __global__ __launch_bounds__(64 * bwd_bf16_waves(D), (bwd_bf16_waves(D) == 8 || 
 //                            = key l16, registers r = queries 4 g4 + r
 //   dV^T += dO^T P, dK^T += Q^T dS: B = P / dS straight from the S / dP
 //                            outputs (a lane's 8 queries 4 g4 + {0..3} and
-//                            16 + 4 g4 + {0..3}); A = dO^T / Q^T rows staged
-//                            with the queries in that order (16-byte reads)
+//                            16 + 4 g4 + {0..3}); A = dO^T / Q^T read from the
+//                            same Q / dO rows by transpose reads
+//                            (ds_read_b64_tr_b16), two per operand
 //   dQ += dS K               dS through LDS (keys contiguous), K^T staged once;
 //                            each wave one 16-query half x two 16-wide d blocks
 //
