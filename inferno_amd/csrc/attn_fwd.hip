@@ -641,6 +641,13 @@ int fwd_plan(int B, int H, int Tq, int Tk, int D, int causal, int bf16, FwdPlan*
         }
     }
     fwd_plan_compute(B, H, Tq, Tk, D, bf16, slots, out);
+    // The bf16 D = 128 forward raises the P.V MFMAs' wave priority (a wave that
+    // reaches them issues them ahead of the other wave's softmax VALU work on
+    // its SIMD); on grids that fit one round of workgroup slots that measured
+    // 5-7% slower (B2 H8 T4096, B1 H16 T4096, B4 H8 T2048, B1 H8 T8192: 512
+    // workgroups on 512 slots) and on larger ones 1-10% faster (config 4, B4
+    // H16 T2048, B8 H16 T1024, B8 H12 T1024).
+    out->pv_prio = (int64_t)((Tq + kFwdBM - 1) / kFwdBM) * B * H > 8LL * slots.per_xcd;
     std::lock_guard<std::mutex> lk(mu);
     if (cache.size() > 256) cache.clear();
     cache[key] = *out;

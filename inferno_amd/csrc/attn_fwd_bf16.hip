@@ -43,7 +43,9 @@ struct FwdBf16Tile {
 
 // SPLIT: the launch carries a split plan (groups, partial slots); the
 // instantiation without it keeps none of that code in its loop.
-template <int D, bool SPLIT>
+// PRIO: the P.V MFMAs run at raised wave priority (D = 128 without a split
+// plan, on grids larger than one round of workgroup slots: fwd_plan).
+template <int D, bool SPLIT, bool PRIO>
 __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
     constexpr int BM = kFwdBM;
     constexpr int BN = FwdBf16Tile<D>::BN;
@@ -247,9 +249,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
             // holding waves of both) the P.V MFMAs run at raised wave priority, so
             // a wave that reaches them issues them ahead of the other wave's
             // softmax VALU work: config 4 forward 310 -> 295 us, B8 H12 T1024
-            // 44.9 -> 43.9; it measured 2% slower at D = 64 and 6% slower on
-            // split-plan grids, which keep the default priority.
-            constexpr bool kPvPrio = D >= 128 && !SPLIT;
+            // 44.9 -> 43.9; it measured 2% slower at D = 64, 6% slower on
+            // split-plan grids and 5-7% slower on grids that fit one round of
+            // workgroup slots, which keep the default priority.
+            constexpr bool kPvPrio = PRIO && D >= 128 && !SPLIT;
             if constexpr (kPvPrio) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb)
@@ -319,9 +322,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(FwdParams p) {
 template <int D>
 static void launch_t(const FwdParams& p, dim3 grid, hipStream_t s) {
     if (p.n_groups)
-        hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, true>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, true, false>), grid, dim3(256), 0, s, p);
+    else if (D >= 128 && p.pv_prio)
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, false, (D >= 128)>), grid, dim3(256), 0, s, p);
     else
-        hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, false>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, false, false>), grid, dim3(256), 0, s, p);
 }
 
 int launch_attn_fwd_bf16(const FwdParams& p, hipStream_t s) {
@@ -337,9 +342,9 @@ int launch_attn_fwd_bf16(const FwdParams& p, hipStream_t s) {
 
 int fwd_bf16_occupancy(int D, int* blocks_per_cu) {
     switch (D) {
-        case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, attn_fwd_bf16_kernel<32, true>, 256, 0);
-        case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, attn_fwd_bf16_kernel<64, true>, 256, 0);
-        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, attn_fwd_bf16_kernel<128, true>, 256, 0);
+        case 32: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, attn_fwd_bf16_kernel<32, true, false>, 256, 0);
+        case 64: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, attn_fwd_bf16_kernel<64, true, false>, 256, 0);
+        case 128: return (int)hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, attn_fwd_bf16_kernel<128, true, false>, 256, 0);
         default: return (int)hipErrorInvalidValue;
     }
 }

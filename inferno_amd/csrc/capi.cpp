@@ -194,6 +194,7 @@ int inf_attn_fwd(const void* q, inf_strides sq, const void* k, inf_strides sk, c
     p.n_qtiles = (Tq + inf::kFwdBM - 1) / inf::kFwdBM;
     inf::FwdPlan plan;
     if (inf::fwd_plan(B, H, Tq, Tk, D, p.causal, dt == INF_BF16, &plan)) return INF_ERR_HIP;
+    p.pv_prio = plan.pv_prio;
     const size_t need = inf::fwd_workspace_bytes(plan, B, H, D);
     if (need && (!workspace || ws_bytes < need)) return INF_ERR_WORKSPACE;
     if (need && reinterpret_cast<uintptr_t>(workspace) % kAlign) return INF_ERR_ALIGNMENT;

@@ -40,6 +40,7 @@ struct FwdParams {
     int n_slots;          // partial slots in use
     float* part;          // workspace: n_slots * B*H * kFwdBM * (D + 2) floats
     int n_split;          // query tiles whose key range is split
+    int pv_prio;          // bf16 D = 128 unsplit: P.V MFMAs at raised wave priority (see fwd_plan)
     FwdGroup groups[kMaxFwdGroups];
     int split_qt[kMaxFwdGroups / 2], split_slot0[kMaxFwdGroups / 2], split_count[kMaxFwdGroups / 2];
 };
@@ -47,6 +48,9 @@ struct FwdParams {
 // Split plan of the forward for a shape (causal; fp32 and bf16 kernels).
 struct FwdPlan {
     int n_groups = 0, n_slots = 0;
+    // bf16 D = 128 without a split: the P.V MFMAs at raised wave priority only
+    // when the grid exceeds one round of the device's workgroup slots
+    int pv_prio = 1;
     FwdGroup groups[kMaxFwdGroups];
     // per split query tile: first slot and number of slots
     int n_split = 0;
