@@ -146,7 +146,8 @@ def test_deterministic_random_shapes(ia, dt, causal, B, H, Tq, Tk, D):
     assert torch.equal(first[0], second[0]), "dQ differs between two deterministic calls"
 
 
-@pytest.mark.parametrize("dt,D,T", [("f32", 64, 150), ("bf16", 64, 150), ("f32", 128, 97), ("bf16", 32, 211)])
+@pytest.mark.parametrize("dt,D,T", [("f32", 64, 150), ("bf16", 64, 150), ("f32", 128, 97), ("bf16", 32, 211),
+                                    ("bf16", 128, 130)])
 def test_deterministic_strided_qkv_view(ia, dt, D, T):
     """The mode on q/k/v read straight out of a [B, T, 3, H, D] projection buffer and dq/dk/dv
     written into a gradient buffer of the same layout (the C++ layer's qkv_attention)."""

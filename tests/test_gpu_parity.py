@@ -380,7 +380,8 @@ def test_prefix_invariance_bitwise(ia, dtype, T, D, cuts):
 
 
 @pytest.mark.parametrize("dtype,D,T", [(torch.float32, 64, 150), (torch.float32, 128, 97),
-                                     (torch.bfloat16, 64, 150), (torch.bfloat16, 32, 211)])
+                                     (torch.bfloat16, 64, 150), (torch.bfloat16, 32, 211),
+                                     (torch.bfloat16, 128, 130)])
 def test_strided_qkv_view(ia, dtype, D, T):
     """q/k/v read straight out of a [B, T, 3, H, D] projection buffer and dq/dk/dv
     written straight into a gradient buffer of the same layout (no copies); O written into,
