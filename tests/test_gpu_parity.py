@@ -379,6 +379,23 @@ def test_prefix_invariance_bitwise(ia, dtype, T, D, cuts):
         assert torch.equal(l1[:, :, :t], l2[:, :, :t]), f"prefix {t}"
 
 
+def test_bf16_d128_forward_same_rows_on_both_grid_sizes(ia):
+    """The bf16 D = 128 forward runs its P.V MFMAs at raised wave priority only on grids larger
+    than one round of workgroup slots (B1 H16 T8192: 1024 workgroups). A smaller grid (the first
+    1024 positions: 128 workgroups) runs the instantiation without it. Causal rows < 1024 see the
+    same key tiles in the same order in both problems, so their O and LSE must be bit-identical."""
+    print("[case] bf16 D128 forward, rows < 1024 of B1 H16 T8192 vs T1024", flush=True)
+    B, H, T, D, t = 1, 16, 8192, 128, 1024
+    g = torch.Generator(device="cuda").manual_seed(7)
+    Q, K, V = (torch.randn(B, H, T, D, device="cuda", generator=g).to(torch.bfloat16) for _ in range(3))
+    o_long, l_long = ia.attn_fwd(Q, K, V)
+    o_short, l_short = ia.attn_fwd(Q[:, :, :t], K[:, :, :t], V[:, :, :t])
+    torch.cuda.synchronize()
+    assert torch.isfinite(o_long.float()).all() and torch.isfinite(l_long).all()
+    assert torch.equal(o_long[:, :, :t], o_short), "O rows < 1024 differ between the two grids"
+    assert torch.equal(l_long[:, :, :t], l_short), "LSE rows < 1024 differ between the two grids"
+
+
 @pytest.mark.parametrize("dtype,D,T", [(torch.float32, 64, 150), (torch.float32, 128, 97),
                                      (torch.bfloat16, 64, 150), (torch.bfloat16, 32, 211),
                                      (torch.bfloat16, 128, 130)])
