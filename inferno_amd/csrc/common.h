@@ -92,15 +92,15 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// bf16 <-> fp32 (round to nearest even; inputs here are finite).
+// bf16 <-> fp32.  fp32 -> bf16 rounds to nearest even and keeps NaN a (quiet)
+// NaN; gfx950 converts in hardware (v_cvt_pk_bf16_f32, two values per
+// instruction), branch-free, where a bit-level rounding with a NaN test
+// compiles to a divergent branch per element.
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float(((uint32_t)h) << 16);
 }
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t b = __float_as_uint(f);
-    if ((b & 0x7F800000u) == 0x7F800000u && (b & 0x007FFFFFu)) return (uint16_t)((b >> 16) | 0x40u);
-    b += 0x7FFFu + ((b >> 16) & 1u);
-    return (uint16_t)(b >> 16);
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // Element type tags: fp32 storage or bf16 storage (fp32 arithmetic either way).
